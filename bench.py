@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""Benchmark: one MMDiT block step of Qwen-Image-2.1 at 1024x1024 output with
+Q4_K_M weights on one MI355X, through the C ABI of libqimm.so.
+
+Workload (the configuration the headline metric is quoted on): hidden 4096,
+32 heads x 128, MLP 12288; 4096 image tokens (64x64 latent grid) attending over
+a cached 256-token text prefix; q/k/v/out/gate_up in Q4_K, the MLP down
+projection in Q6_K; adaLN modulation row; bf16 MFMA with f32 accumulation and
+an f32 residual stream. A step is one block forward; the timed loop cycles over
+several distinct blocks' weights (more bytes than the 256 MB last-level cache)
+and over the 32 layers of the prefix cache, as the 32-block x 20-step denoising
+loop does. Inputs are resident in HBM before timing starts.
+
+Beside the block step, each kernel of the step is timed alone with HIP events
+on the launch stream (attention at B1 H32 Sq4096 Skv 256+4096; the four
+dequant-GEMMs at M=4096) to give TFLOP/s and roofline fractions, and the CPU
+oracle is timed on a bounded sample of the same block on the host cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "qwen3-image21_amd")
+sys.path.insert(0, PKG)
+
+METRIC = "ms per MMDiT block step + attention TFLOP/s at 1024² Q4_K_M (1 GPU)"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBPS = 8000.0
+
+HID, HEADS, HD, MLP = 4096, 32, 128, 12288
+S_IMG, P_TXT, GRID = 4096, 256, 64
+LAYERS = 32
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--blocks", type=int, default=4, help="distinct block weight sets cycled in the loop")
+    ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--cpu-rows", type=int, default=256, help="token rows in the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the block step is not sharded across GPUs "
+              "(see the sharding notes); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import qimm
+    import synth
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    ctx = qimm.Context(0)
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+
+    # ---- weights: distinct blocks, Q4_K with a Q6_K down projection ----
+    t0 = time.time()
+    blocks, host_w0 = [], None
+    wbytes = 0
+    for i in range(args.blocks):
+        rng = np.random.default_rng(1000 + i)
+        w = {
+            "to_q": synth.random_blocks(rng, synth.Q4_K, HID, HID),
+            "to_k": synth.random_blocks(rng, synth.Q4_K, HID, HID),
+            "to_v": synth.random_blocks(rng, synth.Q4_K, HID, HID),
+            "to_out": synth.random_blocks(rng, synth.Q4_K, HID, HID),
+            "gate_up": synth.random_blocks(rng, synth.Q4_K, 2 * MLP, HID),
+            "down": synth.random_blocks(rng, synth.Q6_K, HID, MLP),
+        }
+        shapes = {"to_q": (synth.Q4_K, HID, HID), "to_k": (synth.Q4_K, HID, HID), "to_v": (synth.Q4_K, HID, HID),
+                  "to_out": (synth.Q4_K, HID, HID), "gate_up": (synth.Q4_K, 2 * MLP, HID),
+                  "down": (synth.Q6_K, HID, MLP)}
+        keep = []
+        T = qimm.BlockTensors()
+        for name, field in (("to_q", "to_q"), ("to_k", "to_k"), ("to_v", "to_v"), ("to_out", "to_out"),
+                            ("gate_up", "gate_up"), ("down", "mlp_out")):
+            t, r, c = shapes[name]
+            setattr(T, field, qimm.make_tensor(t, r, c, w[name].tobytes(), keep))
+        nq = (1 + 0.02 * rng.standard_normal(HD)).astype(np.float32)
+        nk = (1 + 0.02 * rng.standard_normal(HD)).astype(np.float32)
+        T.norm_q = qimm.make_tensor(synth.F32, HD, 1, nq.tobytes(), keep)
+        T.norm_k = qimm.make_tensor(synth.F32, HD, 1, nk.tobytes(), keep)
+        blocks.append(ctx.block_create(qimm.BlockConfig(HID, HEADS, HD, MLP), T))
+        if i == 0:
+            wbytes = sum(v.size for v in w.values())
+            host_w0 = (w, shapes, nq, nk)
+        del keep
+    log(f"bench: {args.blocks} blocks uploaded ({wbytes / 1e6:.1f} MB GGUF each) in {time.time() - t0:.1f}s")
+
+    # ---- prefix cache (32 layers), activations, modulation, RoPE rows ----
+    g = torch.Generator(device="cuda").manual_seed(0)
+    kv = ctx.kv_create(LAYERS, 1, HEADS, P_TXT)
+    for layer in range(LAYERS):
+        k = torch.randn((1, HEADS, P_TXT, HD), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((1, HEADS, P_TXT, HD), generator=g, device="cuda").to(torch.bfloat16)
+        kv.store(layer, k.data_ptr(), v.data_ptr(), sh)
+    x = torch.randn((1, S_IMG, HID), generator=g, device="cuda")
+    x_out = torch.empty_like(x)
+    mod = 0.5 * torch.randn((1, 1, 4 * HID), generator=g, device="cuda")
+    mask = [0] * P_TXT + [1] * S_IMG
+    pe_host = qimm.rope_table([(1, GRID, GRID)], mask)[P_TXT:]
+    pe = torch.from_numpy(np.ascontiguousarray(pe_host)).cuda()
+
+    def step(i):
+        blocks[i % len(blocks)].forward(x.data_ptr(), x_out.data_ptr(), 1, S_IMG, mod.data_ptr(), pe.data_ptr(),
+                                        kv, i % LAYERS, None, None, sh)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    log("bench: warmup done")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_step = e0.elapsed_time(e1) / args.steps
+    assert torch.isfinite(x_out).all().item(), "non-finite block output"
+    log(f"bench: block step {ms_step:.3f} ms (wall {wall * 1e3 / args.steps:.3f} ms)")
+
+    # ---- per-kernel timings (same shapes as inside the step) ----
+    def time_it(fn, iters):
+        for _ in range(2):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for _ in range(iters):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / iters
+
+    kernels = {}
+    # attention: 4096 image queries over 256 prefix + 4096 own keys
+    q = torch.randn((1, HEADS, S_IMG, HD), generator=g, device="cuda").to(torch.bfloat16)
+    ko = torch.randn((1, HEADS, S_IMG, HD), generator=g, device="cuda").to(torch.bfloat16)
+    vt = torch.randn((1, HEADS, HD, S_IMG), generator=g, device="cuda").to(torch.bfloat16)
+    ao = torch.empty((1, S_IMG, HID), dtype=torch.bfloat16, device="cuda")
+    att_ms = time_it(lambda: ctx.attention(q.data_ptr(), 1, HEADS, S_IMG, kv, 0, ko.data_ptr(), vt.data_ptr(),
+                                           S_IMG, HD ** -0.5, ao.data_ptr(), sh), args.kernel_iters)
+    att_flop = 4.0 * HEADS * S_IMG * (S_IMG + P_TXT) * HD
+    kernels["attention"] = {"ms": att_ms, "gflop": att_flop / 1e9, "tflops": att_flop / att_ms / 1e9}
+    del q, ko, vt, ao
+
+    # dequant-GEMMs with the step's shapes (M = 4096 tokens)
+    rng = np.random.default_rng(7)
+    a = torch.randn((S_IMG, MLP), generator=g, device="cuda").to(torch.bfloat16)
+    y = torch.empty((S_IMG, 2 * MLP), dtype=torch.bfloat16, device="cuda")
+    for name, t, n, k in (("gemm_qkv", synth.Q4_K, 3 * HID, HID), ("gemm_out", synth.Q4_K, HID, HID),
+                          ("gemm_gate_up", synth.Q4_K, 2 * MLP, HID), ("gemm_down", synth.Q6_K, HID, MLP)):
+        wb = synth.random_blocks(rng, t, n, k)
+        W = ctx.upload(t, n, k, wb.tobytes())
+        ms = time_it(lambda: ctx.qmatmul(W, a.data_ptr(), S_IMG, k, y.data_ptr(), synth.BF16, sh), args.kernel_iters)
+        flop = 2.0 * S_IMG * n * k
+        kernels[name] = {"ms": ms, "gflop": flop / 1e9, "tflops": flop / ms / 1e9,
+                         "weight_gbps": wb.size / ms / 1e6, "weight_mb": wb.size / 1e6}
+        W.free()
+    del a, y
+    for kname, kd in kernels.items():
+        kd["frac_bf16_peak"] = kd["tflops"] / PEAK_BF16_TFLOPS
+        log(f"bench: {kname}: {kd['ms']:.3f} ms, {kd['tflops']:.1f} TFLOP/s")
+
+    dom_name = max(kernels, key=lambda n: kernels[n]["ms"])
+    dom = kernels[dom_name]
+    roofline = {"kernel": dom_name, "bound": "mfma", "achieved": round(dom["tflops"], 2),
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(dom["tflops"] / PEAK_BF16_TFLOPS, 4),
+                "traffic": None, "flop_per_launch": dom["gflop"] * 1e9}
+
+    block_flop = att_flop + 2.0 * S_IMG * HID * (3 * HID + HID + 2 * MLP) + 2.0 * S_IMG * MLP * HID
+
+    # ---- CPU baseline: the oracle in candle mode on a bounded sample ----
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(args.cpu_rows, host_w0)
+
+    for blk in blocks:
+        blk.free()
+    kv.free()
+
+    out = {
+        "metric": METRIC,
+        "value": round(ms_step, 4),
+        "unit": "ms/block-step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "MMDiT block step, 1024x1024 T2I, Q4_K_M (Q4_K + Q6_K down), cached prefix",
+                   "hidden": HID, "heads": HEADS, "head_dim": HD, "mlp": MLP, "batch": 1,
+                   "image_tokens": S_IMG, "prefix_tokens": P_TXT, "distinct_blocks": args.blocks,
+                   "weights_mb_per_block": round(wbytes / 1e6, 1)},
+        "attention_tflops": round(kernels["attention"]["tflops"], 2),
+        "attention_frac_bf16_peak": round(kernels["attention"]["frac_bf16_peak"], 4),
+        "block_tflops": round(block_flop / ms_step / 1e9, 2),
+        "block_frac_bf16_peak": round(block_flop / ms_step / 1e9 / PEAK_BF16_TFLOPS, 4),
+        "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(rows, host_w):
+    """Oracle (candle mode: int8 activations, integer vec-dots, f32 attention)
+    on `rows` token rows of the same block: the four GEMMs and the attention of
+    `rows` queries over all 4352 keys, scaled to the 4096-token step."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    w, shapes, _, _ = host_w
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((rows, HID)).astype(np.float32)
+    h = rng.standard_normal((rows, MLP)).astype(np.float32)
+    O.lib()
+    t_gemm = 0.0
+    for name in ("to_q", "to_k", "to_v", "to_out", "gate_up", "down"):
+        t, n, k = shapes[name]
+        a = h if name == "down" else x
+        t0 = O.now()
+        O.qmatmul(t, w[name], n, k, a, O.CANDLE)
+        t_gemm += O.now() - t0
+        log(f"cpu baseline: {name} {O.now() - t0:.2f}s")
+    q = rng.standard_normal((1, HEADS, rows, HD)).astype(np.float32)
+    ko = rng.standard_normal((1, HEADS, S_IMG, HD)).astype(np.float32)
+    vo = rng.standard_normal((1, HEADS, S_IMG, HD)).astype(np.float32)
+    kp = rng.standard_normal((1, HEADS, P_TXT, HD)).astype(np.float32)
+    vp = rng.standard_normal((1, HEADS, P_TXT, HD)).astype(np.float32)
+    t0 = O.now()
+    O.attention(q, ko, vo, kp, vp, mode=O.CANDLE)
+    t_att = O.now() - t0
+    log(f"cpu baseline: attention {t_att:.2f}s")
+    scale = S_IMG / rows
+    ms = (t_gemm + t_att) * scale * 1e3
+    return {"value": round(ms, 1), "unit": "ms/block-step", "cores": O.num_threads(), "kind": "port",
+            "sample": f"{rows} of 4096 token rows through q/k/v/out/gate_up/down quantized matmuls plus "
+                      f"attention of {rows} queries over 4352 keys, timed and scaled x{scale:g}; "
+                      f"LayerNorm/modulation omitted",
+            "sample_seconds": round(t_gemm + t_att, 2)}
+
+
+if __name__ == "__main__":
+    main()

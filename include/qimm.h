@@ -1,0 +1,219 @@
+/*
+ * qimm — MI355X (gfx950) kernels for the single-stream MMDiT block of
+ * Qwen-Image-2.1: GGUF dequant-GEMM + joint attention over a persistent
+ * prefix K/V cache.
+ *
+ * C ABI. Plain pointers and sizes only. Device pointers are HIP device
+ * addresses on the context's device; "stream" is a hipStream_t (NULL = the
+ * legacy default stream). Every call returns a qimm_status; a non-zero status
+ * leaves a message retrievable with qimm_last_error(ctx).
+ *
+ * The reference engine (Rust, candle 0.11) has no FFI boundary of its own;
+ * each entry point below names the Rust item it stands in for. Paths are
+ * relative to the reference repository root.
+ *
+ * Threading: one context per device per host thread, as the reference gives
+ * each worker thread exclusive use of its device (src/server.rs:120-148).
+ */
+#ifndef QIMM_H
+#define QIMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QIMM_ABI_VERSION 1
+
+typedef enum {
+    QIMM_OK = 0,
+    QIMM_ERR_ARG = 1,      /* null pointer, bad enum, negative size */
+    QIMM_ERR_SHAPE = 2,    /* sizes inconsistent or unsupported by the kernels */
+    QIMM_ERR_TYPE = 3,     /* GGML type not supported for this use */
+    QIMM_ERR_OOM = 4,      /* device or host allocation failed */
+    QIMM_ERR_HIP = 5,      /* a HIP runtime call failed */
+    QIMM_ERR_STATE = 6     /* object used in the wrong state (e.g. missing cache) */
+} qimm_status;
+
+/* GGML tensor type ids as stored in GGUF files (GGML spec; the values
+ * candle's gguf_file reader uses). */
+typedef enum {
+    QIMM_TYPE_F32 = 0,
+    QIMM_TYPE_F16 = 1,
+    QIMM_TYPE_Q8_0 = 8,
+    QIMM_TYPE_Q4_K = 12,
+    QIMM_TYPE_Q6_K = 14,
+    QIMM_TYPE_BF16 = 30
+} qimm_ggml_type;
+
+typedef struct qimm_ctx qimm_ctx;
+typedef struct qimm_weight qimm_weight;
+typedef struct qimm_block qimm_block;
+typedef struct qimm_kv qimm_kv;
+
+/* ---------------- context ---------------- */
+
+/* One device context. Stands in for candle's Device handle as selected in
+ * src/main.rs:159-162 and owned per worker thread (src/server.rs:123-155). */
+int qimm_ctx_create(int device, qimm_ctx **out);
+int qimm_ctx_destroy(qimm_ctx *ctx);
+/* Message of the last failed call on ctx (mirrors candle's bail! text,
+ * e.g. src/quantized_transformer.rs:489). Never NULL. */
+const char *qimm_last_error(const qimm_ctx *ctx);
+const char *qimm_status_string(int status);
+int qimm_abi_version(void);
+
+/* Device memory helpers for hosts without their own device allocator
+ * (candle moves tensors with Tensor::to_device, src/transformer.rs:37-45). */
+int qimm_malloc(qimm_ctx *ctx, size_t bytes, void **dptr);
+int qimm_free(qimm_ctx *ctx, void *dptr);
+int qimm_memcpy_h2d(qimm_ctx *ctx, void *dst, const void *src, size_t bytes, void *stream);
+int qimm_memcpy_d2h(qimm_ctx *ctx, void *dst, const void *src, size_t bytes, void *stream);
+int qimm_stream_synchronize(qimm_ctx *ctx, void *stream);
+
+/* ---------------- quantized weights ---------------- */
+
+/* Upload one GGUF tensor [rows = out features, cols = in features], GGML
+ * blocks running along cols, exactly as candle's quantized VarBuilder hands
+ * it to QMatMul::from_arc (src/quantized_transformer.rs:31-33). bytes must be
+ * rows * cols / block_size * block_bytes. The library owns the device copy
+ * and may re-stride blocks for aligned loads; values are never changed. */
+int qimm_weight_upload(qimm_ctx *ctx, int ggml_type, int64_t rows, int64_t cols,
+                       const void *host_bytes, size_t nbytes, qimm_weight **out);
+int qimm_weight_free(qimm_weight *w);
+int64_t qimm_weight_device_bytes(const qimm_weight *w);
+
+/* Exact dequantization to f32 of raw GGUF block bytes already on the device.
+ * Replaces QTensor::dequantize (src/gguf_loader.rs:35-38,
+ * src/quantized_transformer.rs:68,108,110). Bit-identical to the GGML
+ * formulas: every scale product is exact in f32. n = number of values. */
+int qimm_dequant(qimm_ctx *ctx, int ggml_type, const void *dev_bytes, int64_t n,
+                 float *dev_out, void *stream);
+
+/* y[M,N] = x[M,K] * W^T with x bf16 row-major (row stride lda elements,
+ * lda % 8 == 0), y row-major [M,N] in f32 (out_type QIMM_TYPE_F32) or bf16
+ * (QIMM_TYPE_BF16). Replaces QMatMul::forward as called by Linear::forward
+ * (src/quantized_transformer.rs:19-29). Requires N % 128 == 0 and K a
+ * multiple of 64 and of the block size. */
+int qimm_qmatmul(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_t m,
+                 int64_t lda, void *y, int out_type, void *stream);
+
+/* ---------------- host-side layout and RoPE ---------------- */
+
+/* JointLayout::new (src/joint_layout.rs:52-103). text_image_mask may be NULL
+ * (text-to-image). cond_shapes: ncond (h, w) pairs. image_ids receives the
+ * per-token block id (-1 text) for total_len tokens; pass cap >= total_len. */
+int qimm_joint_layout(int64_t text_len, const uint8_t *text_image_mask,
+                      const int64_t *cond_shapes, int64_t ncond,
+                      int64_t target_h, int64_t target_w,
+                      int64_t *image_ids, int64_t cap,
+                      int64_t *prefix_len, int64_t *target_len, int64_t *total_len);
+
+/* EmbedNd::forward (src/rope.rs:104-211) with the tables of
+ * EmbedNd::new_with_mode (src/rope.rs:37-88): pe[seq][sum(axes)] = (cos, sin)
+ * interleaved per pair, frame | height | width pairs. shapes: nshapes
+ * (frame, height, width) triples; image_mask: seq bytes (nonzero = image). */
+int qimm_rope_table(const int64_t *shapes, int64_t nshapes, const uint8_t *image_mask,
+                    int64_t seq, const int64_t axes[3], double theta, float *pe_host);
+
+/* ---------------- prefix K/V cache ---------------- */
+
+/* TextKvCache (src/transformer.rs:14-19): per layer (k, v) of the prefix
+ * after Q/K norm and RoPE, stored bf16 (KV_CACHE_DTYPE, src/transformer.rs:24)
+ * in device memory owned by the library, persistent across steps. Head dim
+ * must be 128. Internally k is [B,H,P,128] and v is stored transposed
+ * [B,H,128,P] for the attention kernel. */
+int qimm_kv_create(qimm_ctx *ctx, int64_t layers, int64_t batch, int64_t heads,
+                   int64_t prefix_len, int64_t head_dim, qimm_kv **out);
+int qimm_kv_destroy(qimm_kv *kv);
+/* to_cache_entry (src/transformer.rs:37-41): store one layer given in the
+ * reference layout [B,H,P,D] bf16 (device pointers). */
+int qimm_kv_store_layer(qimm_kv *kv, int64_t layer, const uint16_t *k_bhpd,
+                        const uint16_t *v_bhpd, void *stream);
+/* from_cache_entry (src/transformer.rs:43-45): read one layer back in the
+ * reference layout [B,H,P,D] bf16 (device pointers). */
+int qimm_kv_load_layer(const qimm_kv *kv, int64_t layer, uint16_t *k_bhpd, uint16_t *v_bhpd,
+                       void *stream);
+int64_t qimm_kv_prefix_len(const qimm_kv *kv);
+
+/* ---------------- attention ---------------- */
+
+/* Per-head RmsNorm (eps 1e-6, weight norm_w[128] device f32) then RoPE with
+ * pe [S,128] (device f32) on raw projections x [B,S,H,128] f32 (device),
+ * written as bf16 [B,H,S,128] — the q/k half of Attention::forward
+ * (src/quantized_transformer.rs:137-142). */
+int qimm_qk_norm_rope(qimm_ctx *ctx, const float *x, int64_t batch, int64_t seq,
+                      int64_t heads, const float *norm_w, const float *pe, uint16_t *out,
+                      void *stream);
+/* Raw values x [B,S,H,128] f32 -> bf16 [B,H,128,S] (the kernel's V layout). */
+int qimm_v_transpose(qimm_ctx *ctx, const float *x, int64_t batch, int64_t seq,
+                     int64_t heads, uint16_t *vt_out, void *stream);
+
+/* Unmasked joint attention of queries q [B,H,Sq,128] over keys
+ * [prefix layer of kv ; own] with own keys k_own [B,H,So,128] and own values
+ * transposed vt_own [B,H,128,So] (bf16, device). kv may be NULL (no prefix).
+ * out [B,Sq,H*128] bf16. Replaces chunked_attention / flash_attention
+ * (src/transformer.rs:246-296) on the cached step, where the mask is None
+ * (src/quantized_transformer.rs:526-532) and the keys are
+ * cat([from_cache_entry(prefix), own]) (143-146). scale = 1/sqrt(128) there. */
+int qimm_attention(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64_t heads,
+                   int64_t sq, const qimm_kv *kv, int64_t layer, const uint16_t *k_own,
+                   const uint16_t *vt_own, int64_t so, float scale, uint16_t *out,
+                   void *stream);
+
+/* ---------------- the block ---------------- */
+
+typedef struct {
+    int64_t hidden;    /* heads * head_dim (Config::hidden_size, src/transformer.rs:81-84) */
+    int64_t heads;
+    int64_t head_dim;  /* must be 128 */
+    int64_t mlp;       /* Config::mlp_hidden_size = 3 * hidden (src/transformer.rs:86-88) */
+} qimm_block_config;
+
+/* One GGUF tensor in host memory, as the quantized VarBuilder returns it. */
+typedef struct {
+    int ggml_type;
+    int64_t rows;      /* out features (GGUF ne[1]) */
+    int64_t cols;      /* in features (GGUF ne[0]) */
+    const void *data;  /* NULL = absent */
+    size_t nbytes;
+} qimm_tensor;
+
+/* The tensors of transformer_blocks.{i} (src/quantized_transformer.rs:99-111,
+ * 173-188): attn.to_q/to_k/to_v/to_out.0, attn.norm_q/norm_k [128],
+ * img_mlp.gate_up (fused [2*mlp, hidden]) or img_mlp.proj + img_mlp.gate_layer,
+ * img_mlp.out. */
+typedef struct {
+    qimm_tensor to_q, to_k, to_v, to_out;
+    qimm_tensor norm_q, norm_k;
+    qimm_tensor gate_up;
+    qimm_tensor proj, gate_layer;
+    qimm_tensor mlp_out;
+} qimm_block_tensors;
+
+/* TransformerBlock::new (src/quantized_transformer.rs:249-256): uploads the
+ * block's weights (q/k/v fused along N when their types match, gate/up rows
+ * interleaved per 64 for the SwiGLU epilogue; block bytes unchanged). */
+int qimm_block_create(qimm_ctx *ctx, const qimm_block_config *cfg,
+                      const qimm_block_tensors *tensors, qimm_block **out);
+int qimm_block_destroy(qimm_block *blk);
+
+/* TransformerBlock::forward (src/quantized_transformer.rs:258-285) on the
+ * cached step: attention_mask None, prefix = layer `layer` of kv (kv NULL =
+ * no prefix). All pointers are device pointers:
+ *   x        [B,S,hidden] f32; x_out may alias x
+ *   mod      [B,1,4*hidden] f32 = (scale1, gate1, scale2, gate2) rows
+ *   pe       [S,head_dim] f32 (cos, sin interleaved), rows of this call's tokens
+ *   k_out/v_out  optional bf16 [B,H,S,head_dim]: this call's own k (after
+ *            norm and RoPE) and v, the tuple's 2nd/3rd members stored as
+ *            to_cache_entry would (src/quantized_transformer.rs:388). */
+int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t batch,
+                       int64_t seq, const float *mod, const float *pe, const qimm_kv *kv,
+                       int64_t layer, uint16_t *k_out, uint16_t *v_out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QIMM_H */

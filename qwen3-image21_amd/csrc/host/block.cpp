@@ -1,0 +1,292 @@
+// The single-stream MMDiT block on the cached step, and the standalone
+// attention entry points.
+#include <math.h>
+#include <string.h>
+
+#include <new>
+#include <vector>
+
+#include "internal.h"
+
+using namespace qimm_host;
+
+namespace {
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// Norm weights are GGUF tensors too (usually F32); dequantize on the host like
+// vb.get(d_head, "norm_q.weight")?.dequantize() (src/quantized_transformer.rs:108-110).
+int tensor_to_f32(qimm_ctx *ctx, const qimm_tensor &t, int64_t n, std::vector<float> &out) {
+    if (!t.data) return set_err(ctx, QIMM_ERR_ARG, "block: missing norm weight");
+    if (t.rows * t.cols != n && !(t.rows == n && t.cols == 1) && !(t.rows == 1 && t.cols == n))
+        return set_err(ctx, QIMM_ERR_SHAPE, "block: norm weight must have head_dim values");
+    out.resize((size_t)n);
+    const uint8_t *p = (const uint8_t *)t.data;
+    if (t.ggml_type == QIMM_TYPE_F32 && t.nbytes == (size_t)n * 4) {
+        memcpy(out.data(), p, (size_t)n * 4);
+    } else if ((t.ggml_type == QIMM_TYPE_F16 || t.ggml_type == QIMM_TYPE_BF16) && t.nbytes == (size_t)n * 2) {
+        for (int64_t i = 0; i < n; i++) {
+            uint16_t h;
+            memcpy(&h, p + 2 * i, 2);
+            uint32_t bits;
+            if (t.ggml_type == QIMM_TYPE_BF16) {
+                bits = (uint32_t)h << 16;
+            } else {
+                uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+                if (e == 0) {
+                    float v = (float)m * 5.9604644775390625e-08f;
+                    memcpy(&bits, &v, 4);
+                    bits |= sign;
+                } else if (e == 31) {
+                    bits = sign | 0x7f800000u | (m << 13);
+                } else {
+                    bits = sign | ((e + 112u) << 23) | (m << 13);
+                }
+            }
+            memcpy(&out[(size_t)i], &bits, 4);
+        }
+    } else {
+        return set_err(ctx, QIMM_ERR_TYPE, "block: norm weights must be F32, F16 or BF16");
+    }
+    return QIMM_OK;
+}
+
+bool tensor_ok(const qimm_tensor &t, int64_t rows, int64_t cols) {
+    if (!t.data || t.rows != rows || t.cols != cols) return false;
+    const int64_t rb = row_bytes(t.ggml_type, cols);
+    return rb > 0 && (size_t)(rb * rows) == t.nbytes;
+}
+
+void free_block(qimm_block *b) {
+    if (!b) return;
+    for (qimm_weight *w : {b->qkv, b->q, b->k, b->v, b->out, b->gate_up, b->down})
+        if (w) qimm_weight_free(w);
+    if (b->norm_q) (void)hipFree(b->norm_q);
+    if (b->norm_k) (void)hipFree(b->norm_k);
+    delete b;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qimm_block_create(qimm_ctx *ctx, const qimm_block_config *cfg, const qimm_block_tensors *t,
+                      qimm_block **out) {
+    if (!ctx || !cfg || !t || !out) return QIMM_ERR_ARG;
+    *out = nullptr;
+    const int64_t hid = cfg->hidden, H = cfg->heads, D = cfg->head_dim, F = cfg->mlp;
+    if (D != 128 || H <= 0 || H * D != hid || F <= 0 || F % 64 || hid % 256)
+        return set_err(ctx, QIMM_ERR_SHAPE, "block: needs head_dim 128, hidden = heads*128 (multiple of 256), mlp % 64 == 0");
+    if (!tensor_ok(t->to_q, hid, hid) || !tensor_ok(t->to_k, hid, hid) || !tensor_ok(t->to_v, hid, hid) ||
+        !tensor_ok(t->to_out, hid, hid) || !tensor_ok(t->mlp_out, hid, F))
+        return set_err(ctx, QIMM_ERR_SHAPE, "block: attention / mlp_out tensors missing or mis-shaped");
+    const bool fused_gu = t->gate_up.data != nullptr;
+    if (fused_gu ? !tensor_ok(t->gate_up, 2 * F, hid)
+                 : (!tensor_ok(t->proj, F, hid) || !tensor_ok(t->gate_layer, F, hid)))
+        return set_err(ctx, QIMM_ERR_SHAPE, "block: gate_up (or proj + gate_layer) missing or mis-shaped");
+    if (!fused_gu && t->proj.ggml_type != t->gate_layer.ggml_type)
+        return set_err(ctx, QIMM_ERR_TYPE, "block: proj and gate_layer must share a GGML type");
+    if (hipSetDevice(ctx->device) != hipSuccess) return set_err(ctx, QIMM_ERR_HIP, "hipSetDevice failed");
+
+    qimm_block *b = new (std::nothrow) qimm_block();
+    if (!b) return QIMM_ERR_OOM;
+    b->ctx = ctx;
+    b->cfg = *cfg;
+    int rc = QIMM_OK;
+    try {
+        // q | k | v fused along N when the types match (GGML blocks run along K,
+        // so stacking rows keeps every block intact).
+        const int tq = t->to_q.ggml_type;
+        if (t->to_k.ggml_type == tq && t->to_v.ggml_type == tq) {
+            const int64_t rb = row_bytes(tq, hid);
+            std::vector<uint8_t> cat((size_t)(3 * hid * rb));
+            memcpy(cat.data(), t->to_q.data, (size_t)(hid * rb));
+            memcpy(cat.data() + hid * rb, t->to_k.data, (size_t)(hid * rb));
+            memcpy(cat.data() + 2 * hid * rb, t->to_v.data, (size_t)(hid * rb));
+            rc = upload_weight_rows(ctx, tq, 3 * hid, hid, cat.data(), &b->qkv);
+            b->qkv_fused = true;
+        } else {
+            rc = upload_weight_rows(ctx, t->to_q.ggml_type, hid, hid, (const uint8_t *)t->to_q.data, &b->q);
+            if (!rc) rc = upload_weight_rows(ctx, t->to_k.ggml_type, hid, hid, (const uint8_t *)t->to_k.data, &b->k);
+            if (!rc) rc = upload_weight_rows(ctx, t->to_v.ggml_type, hid, hid, (const uint8_t *)t->to_v.data, &b->v);
+        }
+        if (!rc)
+            rc = upload_weight_rows(ctx, t->to_out.ggml_type, hid, hid, (const uint8_t *)t->to_out.data, &b->out);
+        if (!rc) {
+            // [gate ; up] -> per 64 output columns: 64 gate rows then 64 up rows,
+            // so one 128-wide GEMM tile holds both halves of its SwiGLU outputs.
+            const int tg = fused_gu ? t->gate_up.ggml_type : t->gate_layer.ggml_type;
+            const int64_t rb = row_bytes(tg, hid);
+            const uint8_t *gate = fused_gu ? (const uint8_t *)t->gate_up.data : (const uint8_t *)t->gate_layer.data;
+            const uint8_t *up = fused_gu ? gate + F * rb : (const uint8_t *)t->proj.data;
+            std::vector<uint8_t> il((size_t)(2 * F * rb));
+            for (int64_t tile = 0; tile < F / 64; tile++) {
+                memcpy(il.data() + (2 * tile) * 64 * rb, gate + tile * 64 * rb, (size_t)(64 * rb));
+                memcpy(il.data() + (2 * tile + 1) * 64 * rb, up + tile * 64 * rb, (size_t)(64 * rb));
+            }
+            rc = upload_weight_rows(ctx, tg, 2 * F, hid, il.data(), &b->gate_up);
+        }
+        if (!rc)
+            rc = upload_weight_rows(ctx, t->mlp_out.ggml_type, hid, F, (const uint8_t *)t->mlp_out.data, &b->down);
+        std::vector<float> nq, nk;
+        if (!rc) rc = tensor_to_f32(ctx, t->norm_q, D, nq);
+        if (!rc) rc = tensor_to_f32(ctx, t->norm_k, D, nk);
+        if (!rc) {
+            hipError_t e = hipMalloc((void **)&b->norm_q, (size_t)D * 4);
+            if (e == hipSuccess) e = hipMalloc((void **)&b->norm_k, (size_t)D * 4);
+            if (e == hipSuccess) e = hipMemcpy(b->norm_q, nq.data(), (size_t)D * 4, hipMemcpyHostToDevice);
+            if (e == hipSuccess) e = hipMemcpy(b->norm_k, nk.data(), (size_t)D * 4, hipMemcpyHostToDevice);
+            if (e != hipSuccess) rc = hip_err(ctx, e, "block norm weights");
+        }
+    } catch (const std::bad_alloc &) {
+        rc = set_err(ctx, QIMM_ERR_OOM, "block: host staging allocation failed");
+    }
+    if (rc) {
+        free_block(b);
+        return rc;
+    }
+    *out = b;
+    return QIMM_OK;
+}
+
+int qimm_block_destroy(qimm_block *blk) {
+    if (!blk) return QIMM_ERR_ARG;
+    free_block(blk);
+    return QIMM_OK;
+}
+
+int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t batch, int64_t seq,
+                       const float *mod, const float *pe, const qimm_kv *kv, int64_t layer, uint16_t *k_out,
+                       uint16_t *v_out, void *stream) {
+    if (!blk || !x || !x_out || !mod || !pe) return QIMM_ERR_ARG;
+    qimm_ctx *ctx = blk->ctx;
+    const int64_t hid = blk->cfg.hidden, H = blk->cfg.heads, F = blk->cfg.mlp;
+    if (batch <= 0 || seq <= 0) return set_err(ctx, QIMM_ERR_SHAPE, "block forward: batch and seq must be positive");
+    if (!aligned16(x) || !aligned16(x_out) || !aligned16(mod) || !aligned16(pe) ||
+        (k_out && !aligned16(k_out)) || (v_out && !aligned16(v_out)))
+        return set_err(ctx, QIMM_ERR_ARG, "block forward: device pointers must be 16-byte aligned");
+    int64_t P = 0;
+    if (kv) {
+        if (kv->batch != batch || kv->heads != H)
+            return set_err(ctx, QIMM_ERR_SHAPE, "block forward: cache batch/heads differ from the block call");
+        if (layer < 0 || layer >= kv->layers) return set_err(ctx, QIMM_ERR_SHAPE, "block forward: cache layer out of range");
+        P = kv->prefix;
+    }
+    const int64_t M = batch * seq;
+    hipStream_t s = (hipStream_t)stream;
+
+    // workspace: modp [B,4h] f32 | xn [M,h] | q | k | vt | attn [M,h] | hmid [M,F] (bf16)
+    size_t off = 0;
+    const size_t o_modp = off; off += align_up((size_t)(batch * 4 * hid) * 4);
+    const size_t o_xn = off; off += align_up((size_t)(M * hid) * 2);
+    const size_t o_q = off; off += align_up((size_t)(M * hid) * 2);
+    const size_t o_k = off; off += align_up((size_t)(M * hid) * 2);
+    const size_t o_vt = off; off += align_up((size_t)(M * hid) * 2);
+    const size_t o_att = off; off += align_up((size_t)(M * hid) * 2);
+    const size_t o_h = off; off += align_up((size_t)(M * F) * 2);
+    QIMM_HIP(ctx, hipSetDevice(ctx->device));
+    int rc = ensure_workspace(ctx, off);
+    if (rc) return rc;
+    char *ws = (char *)ctx->ws;
+    float *modp = (float *)(ws + o_modp);
+    uint16_t *xn = (uint16_t *)(ws + o_xn), *qb = (uint16_t *)(ws + o_q);
+    uint16_t *kb = k_out ? k_out : (uint16_t *)(ws + o_k);
+    uint16_t *vt = (uint16_t *)(ws + o_vt), *att = (uint16_t *)(ws + o_att), *hm = (uint16_t *)(ws + o_h);
+
+    // modulation.chunk(4) -> (1 + scale1, tanh gate1, 1 + scale2, tanh gate2)
+    QIMM_HIP(ctx, qimm::launch_mod_prep(mod, batch, hid, modp, s));
+    // norm1(x) * (1 + scale1)                                  (:267-269)
+    QIMM_HIP(ctx, qimm::launch_ln_mod(x, M, hid, modp, 4 * hid, seq, xn, s));
+    // to_q/to_k/to_v + per-head RmsNorm + RoPE                 (:133-142)
+    qimm::EpiParams ep{};
+    ep.q = qb;
+    ep.k = kb;
+    ep.vt = vt;
+    ep.v_bhsd = v_out;
+    ep.norm_q = blk->norm_q;
+    ep.norm_k = blk->norm_k;
+    ep.pe = pe;
+    ep.seq = seq;
+    ep.heads = H;
+    ep.hidden = hid;
+    if (blk->qkv_fused) {
+        ep.n_offset = 0;
+        QIMM_HIP(ctx, qimm::launch_qgemm(blk->qkv->gw, xn, M, hid, qimm::EPI_QKV, ep, s));
+    } else {
+        const qimm_weight *parts[3] = {blk->q, blk->k, blk->v};
+        for (int i = 0; i < 3; i++) {
+            ep.n_offset = i * hid;
+            QIMM_HIP(ctx, qimm::launch_qgemm(parts[i]->gw, xn, M, hid, qimm::EPI_QKV, ep, s));
+        }
+    }
+    // attention over [prefix ; own]                            (:143-148)
+    QIMM_HIP(ctx, qimm::launch_attention(qb, kv ? kv->k + layer * kv->layer_elems() : nullptr,
+                                         kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, kb, vt, seq,
+                                         batch, H, seq, 1.0f / sqrtf(128.0f), att, s));
+    // x1 = x + tanh(gate1) * to_out(attn)                       (:150-151, 271-273)
+    qimm::EpiParams er{};
+    er.x_in = x;
+    er.x_out = x_out;
+    er.gvec = modp + hid;
+    er.g_stride = 4 * hid;
+    er.g_rows_per = seq;
+    QIMM_HIP(ctx, qimm::launch_qgemm(blk->out->gw, att, M, hid, qimm::EPI_RESID, er, s));
+    // norm2(x1) * (1 + scale2)                                 (:276-278)
+    QIMM_HIP(ctx, qimm::launch_ln_mod(x_out, M, hid, modp + 2 * hid, 4 * hid, seq, xn, s));
+    // silu(gate) * up                                          (:191-201)
+    qimm::EpiParams eg{};
+    eg.hmid = hm;
+    eg.ldh = F;
+    QIMM_HIP(ctx, qimm::launch_qgemm(blk->gate_up->gw, xn, M, hid, qimm::EPI_SWIGLU, eg, s));
+    // x2 = x1 + tanh(gate2) * out(hidden)                       (:202, 280-282)
+    qimm::EpiParams ed{};
+    ed.x_in = x_out;
+    ed.x_out = x_out;
+    ed.gvec = modp + 3 * hid;
+    ed.g_stride = 4 * hid;
+    ed.g_rows_per = seq;
+    QIMM_HIP(ctx, qimm::launch_qgemm(blk->down->gw, hm, M, F, qimm::EPI_RESID, ed, s));
+    return QIMM_OK;
+}
+
+int qimm_qk_norm_rope(qimm_ctx *ctx, const float *x, int64_t batch, int64_t seq, int64_t heads,
+                      const float *norm_w, const float *pe, uint16_t *out, void *stream) {
+    if (!ctx || !x || !norm_w || !pe || !out) return QIMM_ERR_ARG;
+    if (batch < 0 || seq < 0 || heads < 0) return set_err(ctx, QIMM_ERR_SHAPE, "qk_norm_rope: negative size");
+    if (!aligned16(out)) return set_err(ctx, QIMM_ERR_ARG, "qk_norm_rope: out must be 16-byte aligned");
+    QIMM_HIP(ctx, qimm::launch_qk_prep(x, batch, seq, heads, norm_w, pe, 0, out, (hipStream_t)stream));
+    return QIMM_OK;
+}
+
+int qimm_v_transpose(qimm_ctx *ctx, const float *x, int64_t batch, int64_t seq, int64_t heads, uint16_t *vt_out,
+                     void *stream) {
+    if (!ctx || !x || !vt_out) return QIMM_ERR_ARG;
+    if (batch < 0 || seq < 0 || heads < 0) return set_err(ctx, QIMM_ERR_SHAPE, "v_transpose: negative size");
+    QIMM_HIP(ctx, qimm::launch_qk_prep(x, batch, seq, heads, nullptr, nullptr, 1, vt_out, (hipStream_t)stream));
+    return QIMM_OK;
+}
+
+int qimm_attention(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64_t heads, int64_t sq, const qimm_kv *kv,
+                   int64_t layer, const uint16_t *k_own, const uint16_t *vt_own, int64_t so, float scale,
+                   uint16_t *out, void *stream) {
+    if (!ctx || !q || !out || (so > 0 && (!k_own || !vt_own))) return QIMM_ERR_ARG;
+    if (batch <= 0 || heads <= 0 || sq < 0 || so < 0) return set_err(ctx, QIMM_ERR_SHAPE, "attention: bad sizes");
+    if (!aligned16(q) || !aligned16(out) || (k_own && !aligned16(k_own)))
+        return set_err(ctx, QIMM_ERR_ARG, "attention: q, k and out must be 16-byte aligned");
+    int64_t P = 0;
+    if (kv) {
+        if (kv->batch != batch || kv->heads != heads)
+            return set_err(ctx, QIMM_ERR_SHAPE, "attention: cache batch/heads differ");
+        if (layer < 0 || layer >= kv->layers) return set_err(ctx, QIMM_ERR_SHAPE, "attention: cache layer out of range");
+        P = kv->prefix;
+    }
+    if (P + so == 0) return set_err(ctx, QIMM_ERR_SHAPE, "attention: no keys");
+    QIMM_HIP(ctx, qimm::launch_attention(q, kv ? kv->k + layer * kv->layer_elems() : nullptr,
+                                         kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, k_own, vt_own, so,
+                                         batch, heads, sq, scale, out, (hipStream_t)stream));
+    return QIMM_OK;
+}
+
+}  // extern "C"

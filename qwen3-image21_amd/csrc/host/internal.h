@@ -1,0 +1,67 @@
+// Host-side objects behind the C ABI of include/qimm.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../kernels/kernels.h"
+#include "qimm.h"
+
+struct qimm_ctx {
+    int device = 0;
+    std::string err;
+    // Growable scratch for block intermediates, reused across calls on this
+    // context (calls on one context are serialized by the caller).
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+};
+
+struct qimm_weight {
+    qimm_ctx *ctx = nullptr;
+    int ggml_type = 0;
+    int64_t rows = 0, cols = 0;
+    void *dev = nullptr;        // codes / blocks
+    void *dev_scales = nullptr; // Q8_0 f16 scales
+    size_t dev_bytes = 0;
+    qimm::GemmWeight gw{};
+};
+
+struct qimm_kv {
+    qimm_ctx *ctx = nullptr;
+    int64_t layers = 0, batch = 0, heads = 0, prefix = 0, head_dim = 0;
+    uint16_t *k = nullptr;   // [L][B][H][P][128]
+    uint16_t *vt = nullptr;  // [L][B][H][128][P]
+    int64_t layer_elems() const { return batch * heads * prefix * head_dim; }
+};
+
+struct qimm_block {
+    qimm_ctx *ctx = nullptr;
+    qimm_block_config cfg{};
+    bool qkv_fused = false;
+    qimm_weight *qkv = nullptr;          // fused [3*hidden, hidden] when types match
+    qimm_weight *q = nullptr, *k = nullptr, *v = nullptr;
+    qimm_weight *out = nullptr;
+    qimm_weight *gate_up = nullptr;      // rows interleaved per 64: gate | up
+    qimm_weight *down = nullptr;
+    float *norm_q = nullptr, *norm_k = nullptr;  // device [128]
+};
+
+namespace qimm_host {
+
+int set_err(qimm_ctx *ctx, int status, const std::string &msg);
+int hip_err(qimm_ctx *ctx, hipError_t e, const char *what);
+int ensure_workspace(qimm_ctx *ctx, size_t bytes);
+int upload_weight_rows(qimm_ctx *ctx, int type, int64_t rows, int64_t cols, const uint8_t *bytes,
+                       qimm_weight **out);
+int64_t row_bytes(int type, int64_t cols);
+int block_values(int type);
+
+}  // namespace qimm_host
+
+#define QIMM_HIP(ctx, call)                                         \
+    do {                                                            \
+        hipError_t e_ = (call);                                     \
+        if (e_ != hipSuccess) return qimm_host::hip_err((ctx), e_, #call); \
+    } while (0)

@@ -1,0 +1,88 @@
+// Launch interface of the gfx950 kernels (host side of the .hip files).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qimm {
+
+// Device weight formats after upload. The GGUF block bytes are the source of
+// truth; these layouts only move bytes (no value changes):
+//   WF_Q8_0  codes int8 [N][K] + f16 scales [N][K/32]      (34 B blocks split)
+//   WF_Q4_K  GGUF blocks as stored, [N][K/256] x 144 B        (already 16 B aligned)
+//   WF_Q6_K  GGUF blocks re-strided to 224 B, [N][K/256]      (210 B + 14 B pad)
+//   WF_BF16  bf16 [N][K]
+enum : int { WF_Q8_0 = 0, WF_Q4_K = 1, WF_Q6_K = 2, WF_BF16 = 3 };
+
+enum : int { EPI_F32 = 0, EPI_BF16 = 1, EPI_QKV = 2, EPI_RESID = 3, EPI_SWIGLU = 4 };
+
+struct EpiParams {
+    // EPI_F32 / EPI_BF16: out[m * ldo + n]
+    void *out;
+    int64_t ldo;
+    // EPI_RESID: x_out[m*N+n] = x_in[m*N+n] + gvec[(m / g_rows_per) * g_stride + n] * acc
+    const float *x_in;
+    float *x_out;
+    const float *gvec;
+    int64_t g_stride;
+    int64_t g_rows_per;
+    // EPI_QKV: fused-column n + n_offset in [0, 3*hidden): q | k | v sections.
+    // q, k: RmsNorm per 128-wide head, then RoPE with pe[s][128], to [B,H,S,D].
+    // v: transposed to vt [B,H,D,S]; also [B,H,S,D] into v_bhsd when non-null.
+    uint16_t *q;
+    uint16_t *k;
+    uint16_t *vt;
+    uint16_t *v_bhsd;
+    const float *norm_q;
+    const float *norm_k;
+    const float *pe;
+    int64_t seq;
+    int64_t heads;
+    int64_t hidden;
+    int64_t n_offset;
+    // EPI_SWIGLU: tile columns [0,64) gate, [64,128) up -> hmid[m*ldh + n/2 + j]
+    uint16_t *hmid;
+    int64_t ldh;
+};
+
+struct GemmWeight {
+    int fmt;
+    int64_t n, k;
+    const uint8_t *q;       // codes / blocks
+    const uint16_t *scales; // WF_Q8_0 only
+};
+
+// y = A[M,K] (bf16, row stride lda) x W[N,K]^T with the epilogue selected by epi.
+hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda,
+                        int epi, const EpiParams &ep, hipStream_t stream);
+
+// Exact GGUF dequantization of raw block bytes (device) to f32 (device).
+hipError_t launch_dequant(int ggml_type, const uint8_t *src, int64_t n, float *out,
+                          hipStream_t stream);
+
+// modp[r][0:h] = 1 + scale1, [h:2h] = tanh(gate1), [2h:3h] = 1 + scale2,
+// [3h:4h] = tanh(gate2), for each of rows modulation rows [rows][4h].
+hipError_t launch_mod_prep(const float *mod, int64_t rows, int64_t hidden, float *modp,
+                           hipStream_t stream);
+
+// out[m][:] = bf16(LayerNorm(x[m][:]) * modp_scale[(m / rows_per) * stride + :])
+hipError_t launch_ln_mod(const float *x, int64_t m, int64_t hidden, const float *scale,
+                         int64_t stride, int64_t rows_per, uint16_t *out, hipStream_t stream);
+
+// Joint attention over [prefix ; own] keys. q, k_* : [B,H,S,128] bf16;
+// vt_* : [B,H,128,S] bf16; out [B,Sq,H*128] bf16.
+hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp,
+                            int64_t p, const uint16_t *ko, const uint16_t *vto, int64_t so,
+                            int64_t b, int64_t h, int64_t sq, float scale, uint16_t *out,
+                            hipStream_t stream);
+
+// Per-head RmsNorm + RoPE of raw projections x [B,S,H,128] (f32) into the
+// attention layouts; mode 0: q/k -> [B,H,S,128]; mode 1: v -> vt [B,H,128,S].
+hipError_t launch_qk_prep(const float *x, int64_t b, int64_t s, int64_t h, const float *w,
+                          const float *pe, int mode, uint16_t *out, hipStream_t stream);
+
+// [B,H,S,128] bf16 -> [B,H,128,S] bf16 (and back when inverse != 0).
+hipError_t launch_transpose_sd(const uint16_t *in, int64_t bh, int64_t s, uint16_t *out,
+                               int inverse, hipStream_t stream);
+
+}  // namespace qimm

@@ -1,0 +1,260 @@
+// Memory-bound helpers of the block step on gfx950: exact GGUF dequant,
+// adaLN modulation prep, LayerNorm*(1+scale) to bf16, per-head RmsNorm+RoPE
+// prep for standalone attention inputs, and the bf16 [S,D] <-> [D,S]
+// transpose used by the prefix cache.
+#include "device_common.h"
+#include "kernels.h"
+
+namespace qimm {
+namespace {
+
+// ---- exact dequantization (QTensor::dequantize, src/gguf_loader.rs:35-38) ----
+// One thread per 32 output values. All scale products are exact in f32, so
+// the only rounding is Q4_K's final subtraction, as on the CPU.
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+
+__device__ void q4k_sc_m(const uint8_t *s, int j, float &sc, float &mn) {
+    uint32_t a, b;
+    if (j < 4) {
+        a = s[j] & 63u;
+        b = s[j + 4] & 63u;
+    } else {
+        a = (s[j + 4] & 0xFu) | ((uint32_t)(s[j - 4] >> 6) << 4);
+        b = (uint32_t)(s[j + 4] >> 4) | ((uint32_t)(s[j] >> 6) << 4);
+    }
+    sc = (float)a;
+    mn = (float)b;
+}
+
+__global__ void dequant_kernel(int type, const uint8_t *__restrict__ src, int64_t ngroups,
+                               float *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= ngroups) return;
+    float *o = out + i * 32;
+    if (type == 8) {  // Q8_0: 34 B = f16 d + 32 x i8
+        const uint8_t *b = src + i * 34;
+        const float d = f16_bits_to_f32(ld_u16(b));
+        for (int l = 0; l < 32; l++) o[l] = (float)(int8_t)b[2 + l] * d;
+    } else if (type == 12) {  // Q4_K: 144 B
+        const uint8_t *b = src + (i >> 3) * 144;
+        const int j = (int)(i & 7), c = j >> 1;
+        const float d = f16_bits_to_f32(ld_u16(b)), dmin = f16_bits_to_f32(ld_u16(b + 2));
+        float sc, mn;
+        q4k_sc_m(b + 4, j, sc, mn);
+        const float ds = d * sc, dm = dmin * mn;
+        const uint8_t *qs = b + 16 + 32 * c;
+        for (int l = 0; l < 32; l++) {
+            const uint32_t q = (j & 1) ? (qs[l] >> 4) : (qs[l] & 0xFu);
+            o[l] = ds * (float)q - dm;
+        }
+    } else if (type == 14) {  // Q6_K: 210 B = ql[128] qh[64] sc[16] d
+        const uint8_t *b = src + (i >> 3) * 210;
+        const int w = (int)(i & 7), hh = w >> 2, r = w & 3;
+        const float d = f16_bits_to_f32(ld_u16(b + 208));
+        for (int l = 0; l < 32; l++) {
+            const uint8_t qlb = b[64 * hh + l + 32 * (r & 1)];
+            const uint32_t lo = r < 2 ? (qlb & 0xFu) : (uint32_t)(qlb >> 4);
+            const uint32_t hi = (b[128 + 32 * hh + l] >> (2 * r)) & 3u;
+            const int q = (int)(lo | (hi << 4)) - 32;
+            const float ds = d * (float)(int8_t)b[192 + 8 * hh + (32 * r + l) / 16];
+            o[l] = ds * (float)q;
+        }
+    } else if (type == 0) {
+        const float *s = (const float *)src + i * 32;
+        for (int l = 0; l < 32; l++) o[l] = s[l];
+    } else if (type == 1) {
+        const uint16_t *s = (const uint16_t *)src + i * 32;
+        for (int l = 0; l < 32; l++) o[l] = f16_bits_to_f32(s[l]);
+    } else {  // 30: BF16
+        const uint16_t *s = (const uint16_t *)src + i * 32;
+        for (int l = 0; l < 32; l++) o[l] = bf16_bits_to_f32(s[l]);
+    }
+}
+
+// ---- adaLN modulation rows (src/quantized_transformer.rs:259-282) ----
+__global__ void mod_prep_kernel(const float *__restrict__ mod, int64_t n, int64_t hidden,
+                                float *__restrict__ modp) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t part = (i % (4 * hidden)) / hidden;
+    const float v = mod[i];
+    modp[i] = (part & 1) ? tanhf(v) : v + 1.0f;
+}
+
+// ---- LayerNorm (weight 1, bias 0, eps 1e-6) * (1 + scale) -> bf16 ----
+// src/quantized_transformer.rs:231-237, 267-269, 276-278. One 256-thread
+// workgroup per row; the row stays in registers for the two-pass variance.
+constexpr int LN_MAXV = 8;  // float4 chunks per thread: hidden <= 8192
+
+__global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x, int64_t hidden,
+                                                     const float *__restrict__ scale, int64_t stride,
+                                                     int64_t rows_per, uint16_t *__restrict__ out) {
+    __shared__ float red[8];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const float *xr = x + row * hidden;
+    const int nv = (int)(hidden / 4);
+    f32x4 v[LN_MAXV];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < LN_MAXV; i++) {
+        const int c = tid + 256 * i;
+        if (c < nv) {
+            v[i] = *(const f32x4 *)(xr + 4 * c);
+            s += v[i][0] + v[i][1] + v[i][2] + v[i][3];
+        }
+    }
+    s = wave_sum(s);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    const float mean = (red[0] + red[1] + red[2] + red[3]) / (float)hidden;
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < LN_MAXV; i++) {
+        const int c = tid + 256 * i;
+        if (c < nv) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float t = v[i][e] - mean;
+                ss += t * t;
+            }
+        }
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[4 + (tid >> 6)] = ss;
+    __syncthreads();
+    const float var = (red[4] + red[5] + red[6] + red[7]) / (float)hidden;
+    const float rstd = 1.0f / sqrtf(var + 1e-6f);
+    const float *sc = scale + (row / rows_per) * stride;
+    uint16_t *orow = out + row * hidden;
+#pragma unroll
+    for (int i = 0; i < LN_MAXV; i++) {
+        const int c = tid + 256 * i;
+        if (c < nv) {
+            const f32x4 s4 = *(const f32x4 *)(sc + 4 * c);
+            u32x2 pk{pack_bf16x2((v[i][0] - mean) * rstd * s4[0], (v[i][1] - mean) * rstd * s4[1]),
+                     pack_bf16x2((v[i][2] - mean) * rstd * s4[2], (v[i][3] - mean) * rstd * s4[3])};
+            *(u32x2 *)(orow + 4 * c) = pk;
+        }
+    }
+}
+
+// ---- per-head RmsNorm + RoPE prep (src/quantized_transformer.rs:137-142) ----
+// x [B,S,H,128] f32. mode 0: out [B,H,S,128] bf16 after norm (w) and RoPE
+// (pe [S,128]); mode 1 (values): out = vt [B,H,128,S] bf16, no norm.
+__global__ __launch_bounds__(256) void qk_prep_kernel(const float *__restrict__ x, int64_t B, int64_t S,
+                                                      int64_t H, const float *__restrict__ w,
+                                                      const float *__restrict__ pe,
+                                                      uint16_t *__restrict__ out) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t row = gid >> 4;  // (b, s, h) row of 128
+    const int cg = (int)(gid & 15) * 8;
+    const bool ok = row < B * S * H;
+    const int64_t rr = ok ? row : 0;
+    const float *xr = x + rr * 128 + cg;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = xr[i];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) ss += v[i] * v[i];
+    ss = group_sum(ss, 16);
+    if (!ok) return;
+    const float rs = 1.0f / sqrtf(ss * (1.0f / 128.0f) + 1e-6f);
+    const int64_t h = rr % H, s = (rr / H) % S, b = rr / (H * S);
+    const float *pr = pe + s * 128 + cg;
+    uint32_t pk[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float x0 = v[2 * i] * rs * w[cg + 2 * i], x1 = v[2 * i + 1] * rs * w[cg + 2 * i + 1];
+        const float c = pr[2 * i], sn = pr[2 * i + 1];
+        pk[i] = pack_bf16x2(x0 * c - x1 * sn, x0 * sn + x1 * c);
+    }
+    *(u32x4 *)(out + ((b * H + h) * S + s) * 128 + cg) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+}
+
+__global__ void v_prep_kernel(const float *__restrict__ x, int64_t B, int64_t S, int64_t H,
+                              uint16_t *__restrict__ vt) {
+    // element (b, h, d, s) with s fastest: coalesced writes, strided reads
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= B * H * 128 * S) return;
+    const int64_t s = i % S, d = (i / S) % 128, h = (i / (S * 128)) % H, b = i / (S * 128 * H);
+    vt[i] = (uint16_t)(pack_bf16x2(x[((b * S + s) * H + h) * 128 + d], 0.f) & 0xffffu);
+}
+
+// ---- [BH][S][128] <-> [BH][128][S] bf16 via 64x64 LDS tiles ----
+__global__ __launch_bounds__(256) void transpose_sd_kernel(const uint16_t *__restrict__ in, int64_t S,
+                                                           uint16_t *__restrict__ out, int inverse) {
+    __shared__ uint16_t tile[64][65];
+    const int64_t bh = blockIdx.z;
+    const int64_t s0 = (int64_t)blockIdx.x * 64, d0 = (int64_t)blockIdx.y * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    // source rows: forward reads [S][128] (row = s), inverse reads [128][S] (row = d)
+    for (int r = ty; r < 64; r += 4) {
+        if (!inverse) {
+            const int64_t s = s0 + r, d = d0 + tx;
+            tile[r][tx] = s < S ? in[(bh * S + s) * 128 + d] : (uint16_t)0;
+        } else {
+            const int64_t d = d0 + r, s = s0 + tx;
+            tile[tx][r] = s < S ? in[(bh * 128 + d) * S + s] : (uint16_t)0;
+        }
+    }
+    __syncthreads();
+    for (int r = ty; r < 64; r += 4) {
+        if (!inverse) {
+            const int64_t d = d0 + r, s = s0 + tx;
+            if (s < S) out[(bh * 128 + d) * S + s] = tile[tx][r];
+        } else {
+            const int64_t s = s0 + r, d = d0 + tx;
+            if (s < S) out[(bh * S + s) * 128 + d] = tile[r][tx];
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_dequant(int ggml_type, const uint8_t *src, int64_t n, float *out, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int64_t groups = n / 32;
+    dequant_kernel<<<dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, stream>>>(ggml_type, src, groups, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_mod_prep(const float *mod, int64_t rows, int64_t hidden, float *modp, hipStream_t stream) {
+    const int64_t n = rows * 4 * hidden;
+    if (n <= 0) return hipSuccess;
+    mod_prep_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream>>>(mod, n, hidden, modp);
+    return hipGetLastError();
+}
+
+hipError_t launch_ln_mod(const float *x, int64_t m, int64_t hidden, const float *scale, int64_t stride,
+                         int64_t rows_per, uint16_t *out, hipStream_t stream) {
+    if (m <= 0) return hipSuccess;
+    ln_mod_kernel<<<dim3((unsigned)m), dim3(256), 0, stream>>>(x, hidden, scale, stride, rows_per, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_qk_prep(const float *x, int64_t b, int64_t s, int64_t h, const float *w, const float *pe,
+                          int mode, uint16_t *out, hipStream_t stream) {
+    const int64_t rows = b * s * h;
+    if (rows <= 0) return hipSuccess;
+    if (mode == 0) {
+        const int64_t threads = rows * 16;
+        qk_prep_kernel<<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream>>>(x, b, s, h, w, pe, out);
+    } else {
+        const int64_t n = rows * 128;
+        v_prep_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream>>>(x, b, s, h, out);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose_sd(const uint16_t *in, int64_t bh, int64_t s, uint16_t *out, int inverse,
+                               hipStream_t stream) {
+    if (bh <= 0 || s <= 0) return hipSuccess;
+    dim3 grid((unsigned)((s + 63) / 64), 2u, (unsigned)bh);
+    transpose_sd_kernel<<<grid, dim3(256), 0, stream>>>(in, s, out, inverse);
+    return hipGetLastError();
+}
+
+}  // namespace qimm

@@ -1,0 +1,267 @@
+"""ctypes binding of libqimm.so, the C ABI declared in include/qimm.h.
+
+Thin host-side mirror of the reference's block interface for Python callers
+(tests, benchmark): device buffers are passed as integer device addresses
+(e.g. ``torch.Tensor.data_ptr()``) and streams as ``hipStream_t`` handles
+(e.g. ``torch.cuda.current_stream().cuda_stream``).
+
+Loading order matters on ROCm: import torch first when torch is used, so this
+library binds to the HIP runtime torch already loaded (same SONAME) and
+torch's streams and allocations are valid here.
+
+The library is required: loading fails loudly when libqimm.so is missing; there
+is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqimm.so")
+
+# GGML type ids (include/qimm.h)
+F32, F16, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 8, 12, 14, 30
+
+OK = 0
+STATUS = {0: "QIMM_OK", 1: "QIMM_ERR_ARG", 2: "QIMM_ERR_SHAPE", 3: "QIMM_ERR_TYPE",
+          4: "QIMM_ERR_OOM", 5: "QIMM_ERR_HIP", 6: "QIMM_ERR_STATE"}
+
+# Every symbol include/qimm.h declares: (name, restype, argtypes)
+_vp, _i64, _i32, _f32 = C.c_void_p, C.c_int64, C.c_int, C.c_float
+SIGNATURES = [
+    ("qimm_abi_version", _i32, []),
+    ("qimm_status_string", C.c_char_p, [_i32]),
+    ("qimm_ctx_create", _i32, [_i32, C.POINTER(_vp)]),
+    ("qimm_ctx_destroy", _i32, [_vp]),
+    ("qimm_last_error", C.c_char_p, [_vp]),
+    ("qimm_malloc", _i32, [_vp, C.c_size_t, C.POINTER(_vp)]),
+    ("qimm_free", _i32, [_vp, _vp]),
+    ("qimm_memcpy_h2d", _i32, [_vp, _vp, _vp, C.c_size_t, _vp]),
+    ("qimm_memcpy_d2h", _i32, [_vp, _vp, _vp, C.c_size_t, _vp]),
+    ("qimm_stream_synchronize", _i32, [_vp, _vp]),
+    ("qimm_weight_upload", _i32, [_vp, _i32, _i64, _i64, _vp, C.c_size_t, C.POINTER(_vp)]),
+    ("qimm_weight_free", _i32, [_vp]),
+    ("qimm_weight_device_bytes", _i64, [_vp]),
+    ("qimm_dequant", _i32, [_vp, _i32, _vp, _i64, _vp, _vp]),
+    ("qimm_qmatmul", _i32, [_vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp]),
+    ("qimm_joint_layout", _i32, [_i64, _vp, _vp, _i64, _i64, _i64, _vp, _i64,
+                                 C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i64)]),
+    ("qimm_rope_table", _i32, [_vp, _i64, _vp, _i64, _vp, C.c_double, _vp]),
+    ("qimm_kv_create", _i32, [_vp, _i64, _i64, _i64, _i64, _i64, C.POINTER(_vp)]),
+    ("qimm_kv_destroy", _i32, [_vp]),
+    ("qimm_kv_store_layer", _i32, [_vp, _i64, _vp, _vp, _vp]),
+    ("qimm_kv_load_layer", _i32, [_vp, _i64, _vp, _vp, _vp]),
+    ("qimm_kv_prefix_len", _i64, [_vp]),
+    ("qimm_qk_norm_rope", _i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
+    ("qimm_v_transpose", _i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    ("qimm_attention", _i32, [_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _f32, _vp, _vp]),
+    ("qimm_block_create", _i32, [_vp, _vp, _vp, C.POINTER(_vp)]),
+    ("qimm_block_destroy", _i32, [_vp]),
+    ("qimm_block_forward", _i32, [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp]),
+]
+
+
+class BlockConfig(C.Structure):
+    _fields_ = [("hidden", _i64), ("heads", _i64), ("head_dim", _i64), ("mlp", _i64)]
+
+
+class Tensor(C.Structure):
+    """qimm_tensor: one GGUF tensor in host memory."""
+    _fields_ = [("ggml_type", _i32), ("rows", _i64), ("cols", _i64), ("data", _vp),
+                ("nbytes", C.c_size_t)]
+
+
+class BlockTensors(C.Structure):
+    _fields_ = [(n, Tensor) for n in ("to_q", "to_k", "to_v", "to_out", "norm_q", "norm_k",
+                                      "gate_up", "proj", "gate_layer", "mlp_out")]
+
+
+class QimmError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> C.CDLL:
+    """Load libqimm.so once; raise if it is missing (no fallback path)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise QimmError(f"libqimm.so not built at {path}; run __graft_entry__.build()")
+    try:  # bind to the HIP runtime torch ships (same SONAME) rather than a second copy
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    lib = C.CDLL(path)
+    for name, res, args in SIGNATURES:
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def status_name(rc: int) -> str:
+    return STATUS.get(rc, f"status {rc}")
+
+
+class Context:
+    """One device context (qimm_ctx)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load()
+        h = C.c_void_p()
+        rc = self.lib.qimm_ctx_create(device, C.byref(h))
+        if rc != OK:
+            raise QimmError(f"qimm_ctx_create({device}) -> {status_name(rc)}")
+        self.h = h
+
+    def check(self, rc: int, what: str):
+        if rc != OK:
+            msg = self.lib.qimm_last_error(self.h)
+            raise QimmError(f"{what} -> {status_name(rc)}: {msg.decode() if msg else ''}")
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.qimm_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- weights --
+    def upload(self, ggml_type: int, rows: int, cols: int, data: bytes) -> "Weight":
+        h = C.c_void_p()
+        buf = C.create_string_buffer(bytes(data), len(data))
+        self.check(self.lib.qimm_weight_upload(self.h, ggml_type, rows, cols, buf, len(data), C.byref(h)),
+                   "qimm_weight_upload")
+        return Weight(self, h, ggml_type, rows, cols)
+
+    def dequant(self, ggml_type: int, dev_bytes: int, n: int, dev_out: int, stream: int = 0):
+        self.check(self.lib.qimm_dequant(self.h, ggml_type, dev_bytes, n, dev_out, stream), "qimm_dequant")
+
+    def qmatmul(self, w: "Weight", x_dev: int, m: int, lda: int, y_dev: int, out_type: int, stream: int = 0):
+        self.check(self.lib.qimm_qmatmul(self.h, w.h, x_dev, m, lda, y_dev, out_type, stream), "qimm_qmatmul")
+
+    # -- cache --
+    def kv_create(self, layers: int, batch: int, heads: int, prefix_len: int, head_dim: int = 128) -> "KvCache":
+        h = C.c_void_p()
+        self.check(self.lib.qimm_kv_create(self.h, layers, batch, heads, prefix_len, head_dim, C.byref(h)),
+                   "qimm_kv_create")
+        return KvCache(self, h, layers, batch, heads, prefix_len)
+
+    # -- attention --
+    def qk_norm_rope(self, x_dev, batch, seq, heads, norm_w_dev, pe_dev, out_dev, stream=0):
+        self.check(self.lib.qimm_qk_norm_rope(self.h, x_dev, batch, seq, heads, norm_w_dev, pe_dev, out_dev,
+                                              stream), "qimm_qk_norm_rope")
+
+    def v_transpose(self, x_dev, batch, seq, heads, vt_dev, stream=0):
+        self.check(self.lib.qimm_v_transpose(self.h, x_dev, batch, seq, heads, vt_dev, stream), "qimm_v_transpose")
+
+    def attention(self, q_dev, batch, heads, sq, kv, layer, k_own, vt_own, so, scale, out_dev, stream=0):
+        self.check(self.lib.qimm_attention(self.h, q_dev, batch, heads, sq, kv.h if kv else None, layer,
+                                           k_own, vt_own, so, scale, out_dev, stream), "qimm_attention")
+
+    # -- block --
+    def block_create(self, cfg: BlockConfig, tensors: BlockTensors) -> "Block":
+        h = C.c_void_p()
+        self.check(self.lib.qimm_block_create(self.h, C.byref(cfg), C.byref(tensors), C.byref(h)),
+                   "qimm_block_create")
+        return Block(self, h, cfg)
+
+
+class Weight:
+    def __init__(self, ctx, h, t, rows, cols):
+        self.ctx, self.h, self.ggml_type, self.rows, self.cols = ctx, h, t, rows, cols
+
+    def device_bytes(self) -> int:
+        return int(self.ctx.lib.qimm_weight_device_bytes(self.h))
+
+    def free(self):
+        if self.h:
+            self.ctx.lib.qimm_weight_free(self.h)
+            self.h = None
+
+
+class KvCache:
+    def __init__(self, ctx, h, layers, batch, heads, prefix_len):
+        self.ctx, self.h = ctx, h
+        self.layers, self.batch, self.heads, self.prefix_len = layers, batch, heads, prefix_len
+
+    def store(self, layer, k_dev, v_dev, stream=0):
+        self.ctx.check(self.ctx.lib.qimm_kv_store_layer(self.h, layer, k_dev, v_dev, stream), "qimm_kv_store_layer")
+
+    def load(self, layer, k_dev, v_dev, stream=0):
+        self.ctx.check(self.ctx.lib.qimm_kv_load_layer(self.h, layer, k_dev, v_dev, stream), "qimm_kv_load_layer")
+
+    def free(self):
+        if self.h:
+            self.ctx.lib.qimm_kv_destroy(self.h)
+            self.h = None
+
+
+class Block:
+    def __init__(self, ctx, h, cfg):
+        self.ctx, self.h, self.cfg = ctx, h, cfg
+
+    def forward(self, x_dev, x_out_dev, batch, seq, mod_dev, pe_dev, kv=None, layer=0, k_out=None, v_out=None,
+                stream=0):
+        self.ctx.check(self.ctx.lib.qimm_block_forward(self.h, x_dev, x_out_dev, batch, seq, mod_dev, pe_dev,
+                                                       kv.h if kv else None, layer, k_out, v_out, stream),
+                       "qimm_block_forward")
+
+    def free(self):
+        if self.h:
+            self.ctx.lib.qimm_block_destroy(self.h)
+            self.h = None
+
+
+def make_tensor(ggml_type: int, rows: int, cols: int, data: bytes | None, keep: list) -> Tensor:
+    """qimm_tensor over host bytes; `keep` holds the buffer alive."""
+    if data is None:
+        return Tensor(0, 0, 0, None, 0)
+    buf = C.create_string_buffer(bytes(data), len(data))
+    keep.append(buf)
+    return Tensor(ggml_type, rows, cols, C.cast(buf, C.c_void_p), len(data))
+
+
+def joint_layout(text_len: int, text_image_mask=None, cond_shapes=(), target=(1, 1)):
+    """JointLayout::new restated host-side: returns (image_ids, prefix_len, target_len)."""
+    lib = load()
+    cap = text_len * 8 + sum(h * w for h, w in cond_shapes) + target[0] * target[1] + 16
+    ids = (C.c_int64 * cap)()
+    mask = None
+    if text_image_mask is not None:
+        mask = (C.c_uint8 * max(1, text_len))(*[1 if m else 0 for m in text_image_mask])
+    flat = [v for hw in cond_shapes for v in hw]
+    shapes = (C.c_int64 * max(1, len(flat)))(*flat)
+    pl, tl, total = C.c_int64(), C.c_int64(), C.c_int64()
+    rc = lib.qimm_joint_layout(text_len, mask, shapes, len(cond_shapes), target[0], target[1], ids, cap,
+                               C.byref(pl), C.byref(tl), C.byref(total))
+    if rc != OK:
+        raise QimmError(f"qimm_joint_layout -> {status_name(rc)}")
+    return list(ids[: total.value]), pl.value, tl.value
+
+
+def rope_table(shapes, image_mask, axes=(16, 56, 56), theta=10000.0):
+    """EmbedNd::forward restated host-side: returns a flat list pe[seq * sum(axes)]."""
+    import numpy as np
+    lib = load()
+    seq = len(image_mask)
+    width = int(sum(axes))
+    pe = np.zeros((seq, width), dtype=np.float32)
+    flat = np.array([v for s in shapes for v in s], dtype=np.int64)
+    m = np.array([1 if v else 0 for v in image_mask], dtype=np.uint8)
+    ax = np.array(axes, dtype=np.int64)
+    rc = lib.qimm_rope_table(flat.ctypes.data if len(flat) else None, len(shapes),
+                             m.ctypes.data if seq else None, seq, ax.ctypes.data, theta,
+                             pe.ctypes.data if seq else None)
+    if rc != OK:
+        raise QimmError(f"qimm_rope_table -> {status_name(rc)}")
+    return pe

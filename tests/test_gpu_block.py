@@ -1,0 +1,145 @@
+"""GPU parity of the whole block step (TransformerBlock::forward on the cached
+step, src/quantized_transformer.rs:258-285) through qimm_block_create /
+qimm_block_forward, against the oracle on identical seeded inputs.
+
+Bar (north star): cosine >= 0.9999 and max|a-b|/max|b| <= 2e-2 against the
+oracle's f32 candle-mode output. The cosine is taken on the block's update
+x_out - x (stricter than on x_out, where the residual dominates); the
+max-abs-rel on x_out. The own k / v the block returns are checked the same way.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as O
+import qimm
+import synth
+from gpu_util import cos_sim, dev, host, max_abs_rel, stream
+
+pytestmark = pytest.mark.gpu
+
+
+def block_tensors(w, keep):
+    T = qimm.BlockTensors()
+    for name, field in (("to_q", "to_q"), ("to_k", "to_k"), ("to_v", "to_v"), ("to_out", "to_out"),
+                        ("gate_up", "gate_up"), ("proj", "proj"), ("gate_layer", "gate_layer"),
+                        ("down", "mlp_out")):
+        if name in w:
+            t, data, rows, cols = w[name]
+            setattr(T, field, qimm.make_tensor(t, rows, cols, data.tobytes(), keep))
+    for name in ("norm_q", "norm_k"):
+        arr = np.ascontiguousarray(w[name], dtype=np.float32)
+        setattr(T, name, qimm.make_tensor(synth.F32, arr.size, 1, arr.tobytes(), keep))
+    return T
+
+
+def run_block(torch, qctx, cfg, w, x, mod, pe, kpre=None, vpre=None, alias=False, want_kv=False):
+    keep = []
+    c = qimm.BlockConfig(cfg["hidden"], cfg["heads"], cfg["head_dim"], cfg["mlp"])
+    blk = qctx.block_create(c, block_tensors(w, keep))
+    b, s, hid = x.shape
+    x_dev = dev(torch, x)
+    x_out = x_dev if alias else torch.empty_like(x_dev)
+    kv = None
+    if kpre is not None:
+        kv = qctx.kv_create(3, b, cfg["heads"], kpre.shape[2])
+        kv.store(2, dev(torch, kpre.view(np.int16)).data_ptr(), dev(torch, vpre.view(np.int16)).data_ptr(),
+                 stream(torch))
+    k_out = v_out = None
+    if want_kv:
+        k_out = torch.empty((b, cfg["heads"], s, 128), dtype=torch.bfloat16, device="cuda")
+        v_out = torch.empty_like(k_out)
+    blk.forward(x_dev.data_ptr(), x_out.data_ptr(), b, s, dev(torch, mod).data_ptr(), dev(torch, pe).data_ptr(),
+                kv, 2, k_out.data_ptr() if want_kv else None, v_out.data_ptr() if want_kv else None, stream(torch))
+    out = host(x_out)
+    kvs = (host(k_out.float()), host(v_out.float())) if want_kv else (None, None)
+    blk.free()
+    if kv is not None:
+        kv.free()
+    return out, kvs
+
+
+def make_case(seed, cfg, b, s, p, attn_type, down_type, fused=True):
+    rng = np.random.default_rng(seed)
+    w = synth.block_weights(seed, cfg["hidden"], cfg["heads"], cfg["mlp"], attn_type, down_type, fused)
+    x = rng.standard_normal((b, s, cfg["hidden"])).astype(np.float32)
+    mod = (rng.standard_normal((b, 1, 4 * cfg["hidden"])) * 0.5).astype(np.float32)
+    gh = int(np.sqrt(s))
+    while s % gh:
+        gh -= 1
+    pe = O.rope_table([(1, gh, s // gh)], [0] * p + [1] * s)[p:]
+    kpre = vpre = None
+    if p:
+        kpre = O.f32_to_bf16(rng.standard_normal((b, cfg["heads"], p, 128)))
+        vpre = O.f32_to_bf16(rng.standard_normal((b, cfg["heads"], p, 128)))
+    return w, x, mod, pe, kpre, vpre
+
+
+SMALL = dict(hidden=256, heads=2, head_dim=128, mlp=768)
+
+
+def check(got, ref, x):
+    cs = cos_sim(got - x, ref - x)
+    mr = max_abs_rel(got, ref)
+    assert cs >= 0.9999 and mr <= 2e-2, (cs, mr)
+
+
+@pytest.mark.parametrize("attn_type,down_type", [(synth.Q8_0, synth.Q8_0), (synth.Q4_K, synth.Q6_K),
+                                                 (synth.Q6_K, synth.Q4_K)])
+@pytest.mark.parametrize("b,s,p", [(1, 96, 40), (2, 64, 64), (1, 130, 0)])
+def test_block_matches_oracle(torch_cuda, qctx, attn_type, down_type, b, s, p):
+    w, x, mod, pe, kpre, vpre = make_case(b * 1000 + s + p, SMALL, b, s, p, attn_type, down_type)
+    got, (k, v) = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre, want_kv=True)
+    ref, kr, vr = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
+    check(got, ref, x)
+    ref_e, kre, vre = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
+    check(got, ref_e, x)
+    assert cos_sim(k, kr) >= 0.9999 and max_abs_rel(k, kr) <= 2e-2
+    assert cos_sim(v, vr) >= 0.9999 and max_abs_rel(v, vr) <= 2e-2
+
+
+def test_block_in_place_and_separate_mlp_inputs(torch_cuda, qctx):
+    w, x, mod, pe, kpre, vpre = make_case(7, SMALL, 1, 64, 16, synth.Q8_0, synth.Q8_0, fused=False)
+    got, _ = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre, alias=True)
+    ref, _, _ = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
+    check(got, ref, x)
+
+
+def test_block_mixed_qkv_types_unfused_path(torch_cuda, qctx):
+    w, x, mod, pe, kpre, vpre = make_case(8, SMALL, 1, 64, 32, synth.Q4_K, synth.Q6_K)
+    rng = np.random.default_rng(80)
+    w["to_v"] = synth.weight(rng, synth.Q6_K, SMALL["hidden"], SMALL["hidden"])
+    got, _ = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre)
+    ref, _, _ = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
+    check(got, ref, x)
+
+
+def test_block_deterministic(torch_cuda, qctx):
+    w, x, mod, pe, kpre, vpre = make_case(9, SMALL, 1, 96, 32, synth.Q4_K, synth.Q6_K)
+    a, _ = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre)
+    b, _ = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre)
+    assert np.array_equal(a, b)
+
+
+def test_block_config1_shape(torch_cuda, qctx):
+    """Hidden 3072, 24 heads x 128, MLP 9216, 256 image tokens over a 64-token
+    prefix, Q8_0 weights: the reference CPU-path configuration."""
+    cfg = dict(hidden=3072, heads=24, head_dim=128, mlp=9216)
+    w, x, mod, pe, kpre, vpre = make_case(11, cfg, 1, 256, 64, synth.Q8_0, synth.Q8_0)
+    got, _ = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
+    ref, _, _ = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
+    check(got, ref, x)
+
+
+def test_block_rejects_bad_config(torch_cuda, qctx):
+    keep = []
+    w = synth.block_weights(1, 256, 2, 768, synth.Q8_0)
+    bad = qimm.BlockConfig(256, 4, 64, 768)   # head_dim 64 unsupported
+    with pytest.raises(qimm.QimmError, match="QIMM_ERR_SHAPE"):
+        qctx.block_create(bad, block_tensors(w, keep))
+    c = qimm.BlockConfig(256, 2, 128, 768)
+    T = block_tensors(w, keep)
+    T.to_q = qimm.make_tensor(synth.Q8_0, 256, 256, b"\0" * 100, keep)   # wrong byte count
+    with pytest.raises(qimm.QimmError, match="QIMM_ERR_SHAPE"):
+        qctx.block_create(c, T)

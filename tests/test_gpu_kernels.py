@@ -1,0 +1,197 @@
+"""GPU parity: exact dequantization, the dequant-GEMM and the joint attention,
+through the C ABI, against the oracle on the same seeded inputs.
+
+Bars: dequantization bit-exact. GEMM: against float64 products of the same
+bf16 activations and the bf16-rounded dequantized weights the MFMA consumes,
+error <= 2e-4 of sum|a||w| per output (accumulation order only); and against
+the oracle's exact and candle modes, cosine >= 0.9999 and
+max|a-b|/max|b| <= 2e-2. Attention: against the oracle on the same bf16
+Q/K/V, cosine >= 0.9999 and max|a-b|/max|b| <= 2e-2.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import synth
+from gpu_util import bf16_dev, cos_sim, dev, host, max_abs_rel, stream
+from test_oracle_codecs import q4k_block, q6k_block, q8_block, Q8_CODES
+
+pytestmark = pytest.mark.gpu
+
+
+# ---------------------------------------------------------------- dequant
+
+def _dequant_gpu(torch, qctx, t, data, n):
+    src = dev(torch, np.asarray(data, dtype=np.uint8))
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    qctx.dequant(t, src.data_ptr(), n, out.data_ptr(), stream(torch))
+    return host(out)
+
+
+@pytest.mark.parametrize("t", [O.Q8_0, O.Q4_K, O.Q6_K, O.F16, O.BF16, O.F32])
+def test_dequant_bit_exact_random(torch_cuda, qctx, t):
+    rng = np.random.default_rng(100 + t)
+    n = 256 * 37
+    x = (rng.standard_normal(n) * 0.02 * 2.0 ** rng.integers(-8, 8, n)).astype(np.float32)
+    data = O.quantize(t, x)
+    got = _dequant_gpu(torch_cuda, qctx, t, data, n)
+    want = O.dequantize(t, data, n)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_bit_exact_known_answer_blocks(torch_cuda, qctx):
+    blocks = {
+        O.Q8_0: np.concatenate([q8_block(b, Q8_CODES) for b in (0x3C00, 0xB800, 0x0001, 0x7BFF, 0x03FF)]),
+        O.Q4_K: np.concatenate([q4k_block(0x3C00, 0x3C00), q4k_block(0x3800, 0x3400), q4k_block(0x0001, 0x0401)]),
+        O.Q6_K: np.concatenate([q6k_block(0x3C00), q6k_block(0x3800), q6k_block(0x0003)]),
+    }
+    for t, data in blocks.items():
+        n = data.size // O.lib().oq_block_bytes(t) * O.lib().oq_block_size(t)
+        got = _dequant_gpu(torch_cuda, qctx, t, data, n)
+        want = O.dequantize(t, data, n)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), t
+
+
+# ---------------------------------------------------------------- GEMM
+
+def _gemm_case(torch, qctx, t, m, n, k, seed, out_type=synth.F32, std=0.02):
+    rng = np.random.default_rng(seed)
+    _, w, _, _ = synth.weight(rng, t, n, k, std)
+    W = qctx.upload(t, n, k, w.tobytes())
+    a_dev, a = bf16_dev(torch, rng.standard_normal((m, k)).astype(np.float32))
+    if out_type == synth.F32:
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    else:
+        y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    qctx.qmatmul(W, a_dev.data_ptr(), m, k, y.data_ptr(), out_type, stream(torch))
+    got = host(y.float())
+    W.free()
+    return got, a, w
+
+
+@pytest.mark.parametrize("t", [synth.Q8_0, synth.Q4_K, synth.Q6_K, synth.BF16])
+@pytest.mark.parametrize("m,n,k", [(1, 128, 256), (17, 256, 512), (130, 384, 1024), (300, 128, 4096)])
+def test_qmatmul_matches_bf16_weight_products(torch_cuda, qctx, t, m, n, k):
+    got, a, w = _gemm_case(torch_cuda, qctx, t, m, n, k, seed=m * 7 + n + k + t)
+    Wd = O.dequantize(t, w, n * k).reshape(n, k)
+    Wb = O.bf16_round(Wd).astype(np.float64)
+    want = a.astype(np.float64) @ Wb.T
+    scale = np.abs(a).astype(np.float64) @ np.abs(Wb).T
+    assert np.all(np.abs(got - want) <= 2e-4 * scale + 1e-6)
+    # against the oracle: exact weights (exact mode) and candle's int8 activations
+    ye = O.qmatmul(t, w, n, k, a, O.EXACT)
+    assert cos_sim(got, ye) >= 0.9999 and max_abs_rel(got, ye) <= 2e-2
+    if t != synth.BF16:
+        yc = O.qmatmul(t, w, n, k, a, O.CANDLE)
+        assert cos_sim(got, yc) >= 0.9999 and max_abs_rel(got, yc) <= 2e-2
+
+
+def test_qmatmul_bf16_output(torch_cuda, qctx):
+    got, a, w = _gemm_case(torch_cuda, qctx, synth.Q4_K, 64, 256, 512, seed=5, out_type=synth.BF16)
+    want = O.qmatmul(synth.Q4_K, w, 256, 512, a, O.EXACT)
+    assert cos_sim(got, want) >= 0.9999 and max_abs_rel(got, want) <= 2e-2
+
+
+def test_qmatmul_full_qkv_shape_sampled_rows(torch_cuda, qctx):
+    """M=4352 tokens x fused QKV [12288 x 4096] in Q8_0; rows sampled for the oracle."""
+    torch = torch_cuda
+    m, n, k = 4352, 12288, 4096
+    rng = np.random.default_rng(7)
+    _, w, _, _ = synth.weight(rng, synth.Q8_0, n, k)
+    W = qctx.upload(synth.Q8_0, n, k, w.tobytes())
+    a_dev, a = bf16_dev(torch, rng.standard_normal((m, k)).astype(np.float32))
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    qctx.qmatmul(W, a_dev.data_ptr(), m, k, y.data_ptr(), synth.F32, stream(torch))
+    got = host(y)
+    rows = np.concatenate([np.arange(0, 8), rng.choice(m, 16, replace=False), np.arange(m - 8, m)])
+    want = O.qmatmul(synth.Q8_0, w, n, k, a[rows], O.EXACT)
+    assert cos_sim(got[rows], want) >= 0.9999 and max_abs_rel(got[rows], want) <= 2e-2
+    assert np.isfinite(got).all()
+    W.free()
+
+
+def test_qmatmul_rejects_bad_shapes(torch_cuda, qctx):
+    import qimm
+    rng = np.random.default_rng(8)
+    _, w, _, _ = synth.weight(rng, synth.Q8_0, 96, 64)   # N not a multiple of 128
+    W = qctx.upload(synth.Q8_0, 96, 64, w.tobytes())
+    x = torch_cuda.zeros((4, 64), dtype=torch_cuda.bfloat16, device="cuda")
+    y = torch_cuda.zeros((4, 96), dtype=torch_cuda.float32, device="cuda")
+    with pytest.raises(qimm.QimmError, match="QIMM_ERR_SHAPE"):
+        qctx.qmatmul(W, x.data_ptr(), 4, 64, y.data_ptr(), synth.F32)
+    W.free()
+    with pytest.raises(qimm.QimmError, match="QIMM_ERR_SHAPE"):
+        qctx.upload(synth.Q4_K, 128, 100, b"\0" * 10)
+
+
+# ---------------------------------------------------------------- attention
+
+def _attention_case(torch, qctx, b, h, sq, p, so, seed):
+    rng = np.random.default_rng(seed)
+    q_dev, q = bf16_dev(torch, rng.standard_normal((b, h, sq, 128)).astype(np.float32))
+    ko_dev, ko = bf16_dev(torch, rng.standard_normal((b, h, so, 128)).astype(np.float32))
+    vo = O.bf16_round(rng.standard_normal((b, h, so, 128)).astype(np.float32))
+    vt_dev, _ = bf16_dev(torch, np.ascontiguousarray(vo.transpose(0, 1, 3, 2)))
+    kv = None
+    kp = vp = None
+    if p > 0:
+        kp_dev, kp = bf16_dev(torch, rng.standard_normal((b, h, p, 128)).astype(np.float32))
+        vp_dev, vp = bf16_dev(torch, rng.standard_normal((b, h, p, 128)).astype(np.float32))
+        kv = qctx.kv_create(2, b, h, p)
+        kv.store(1, kp_dev.data_ptr(), vp_dev.data_ptr(), stream(torch))
+        # round trip through the cache layout
+        k2 = torch.empty_like(kp_dev)
+        v2 = torch.empty_like(vp_dev)
+        kv.load(1, k2.data_ptr(), v2.data_ptr(), stream(torch))
+        assert torch.equal(k2, kp_dev) and torch.equal(v2, vp_dev)
+    out = torch.empty((b, sq, h * 128), dtype=torch.bfloat16, device="cuda")
+    qctx.attention(q_dev.data_ptr(), b, h, sq, kv, 1, ko_dev.data_ptr(), vt_dev.data_ptr(), so, 128 ** -0.5,
+                   out.data_ptr(), stream(torch))
+    got = host(out.float()).reshape(b, sq, h, 128).transpose(0, 2, 1, 3)
+    if kv is not None:
+        kv.free()
+    return got, q, ko, vo, kp, vp
+
+
+@pytest.mark.parametrize("b,h,sq,p,so", [
+    (1, 2, 128, 64, 128),     # aligned
+    (1, 2, 200, 70, 200),     # ragged query tile, unaligned prefix (scalar V^T path)
+    (2, 3, 64, 256, 96),      # batch 2, prefix longer than own
+    (1, 1, 33, 0, 45),        # no prefix, odd lengths
+    (1, 2, 16, 8, 8),         # tiny
+])
+def test_attention_matches_oracle(torch_cuda, qctx, b, h, sq, p, so):
+    got, q, ko, vo, kp, vp = _attention_case(torch_cuda, qctx, b, h, sq, p, so, seed=b + h + sq + p + so)
+    want = O.attention(q, ko, vo, kp, vp, mode=O.EXACT)
+    assert cos_sim(got, want) >= 0.9999, cos_sim(got, want)
+    assert max_abs_rel(got, want) <= 2e-2, max_abs_rel(got, want)
+
+
+def test_attention_config2_shape_sampled_rows(torch_cuda, qctx):
+    """B1 H32, 4096 image queries over 256 prefix + 4096 own keys; sampled query rows."""
+    torch = torch_cuda
+    b, h, sq, p = 1, 32, 4096, 256
+    got, q, ko, vo, kp, vp = _attention_case(torch, qctx, b, h, sq, p, sq, seed=2)
+    rows = np.array([0, 1, 127, 128, 1000, 2047, 3000, 4094, 4095])
+    want = O.attention(q[:, :, rows], ko, vo, kp, vp, mode=O.EXACT)
+    g = got[:, :, rows]
+    assert cos_sim(g, want) >= 0.9999 and max_abs_rel(g, want) <= 2e-2
+    assert np.isfinite(got).all()
+
+
+def test_qk_norm_rope_matches_oracle(torch_cuda, qctx):
+    torch = torch_cuda
+    rng = np.random.default_rng(9)
+    b, s, h = 2, 40, 3
+    x = rng.standard_normal((b, s, h, 128)).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(128)).astype(np.float32)
+    pe = O.rope_table([(1, 5, 8)], [1] * s)
+    out = torch.empty((b, h, s, 128), dtype=torch.bfloat16, device="cuda")
+    qctx.qk_norm_rope(dev(torch, x).data_ptr(), b, s, h, dev(torch, w).data_ptr(), dev(torch, pe).data_ptr(),
+                      out.data_ptr(), stream(torch))
+    got = host(out.float())
+    want = O.apply_rope(O.rmsnorm(x, w).transpose(0, 2, 1, 3), pe)
+    assert np.max(np.abs(got - want)) <= 2 ** -7 * np.abs(want).max()
+    vt = torch.empty((b, h, 128, s), dtype=torch.bfloat16, device="cuda")
+    qctx.v_transpose(dev(torch, x).data_ptr(), b, s, h, vt.data_ptr(), stream(torch))
+    assert np.array_equal(host(vt.float()), O.bf16_round(x.transpose(0, 2, 3, 1)))

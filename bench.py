@@ -11,10 +11,10 @@ several distinct blocks' weights (more bytes than the 256 MB last-level cache)
 and over the 32 layers of the prefix cache, as the 32-block x 20-step denoising
 loop does. Inputs are resident in HBM before timing starts.
 
-Beside the block step, each kernel of the step is timed alone with HIP events
-on the launch stream (attention at B1 H32 Sq4096 Skv 256+4096; the four
-dequant-GEMMs at M=4096) to give TFLOP/s and roofline fractions, and the CPU
-oracle is timed on a bounded sample of the same block on the host cores.
+After the timed loop, a profiled pass records HIP events on the launch stream
+between the stages of each step (qimm_block_profile), giving each in-step
+kernel's duration, TFLOP/s and roofline fraction; the CPU oracle is timed on a
+bounded sample of the same block on the host cores.
 """
 import argparse
 import json
@@ -45,8 +45,8 @@ def main():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--blocks", type=int, default=4, help="distinct block weight sets cycled in the loop")
-    ap.add_argument("--kernel-iters", type=int, default=20)
-    ap.add_argument("--cpu-rows", type=int, default=256, help="token rows in the CPU baseline sample")
+    ap.add_argument("--profile-steps", type=int, default=16, help="steps timed stage by stage after the loop")
+    ap.add_argument("--cpu-rows", type=int, default=4096, help="token rows in the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -134,47 +134,35 @@ def main():
     assert torch.isfinite(x_out).all().item(), "non-finite block output"
     log(f"bench: block step {ms_step:.3f} ms (wall {wall * 1e3 / args.steps:.3f} ms)")
 
-    # ---- per-kernel timings (same shapes as inside the step) ----
-    def time_it(fn, iters):
-        for _ in range(2):
-            fn()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        a.record(stream)
-        for _ in range(iters):
-            fn()
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / iters
+    # ---- per-stage device times inside the step (HIP events on the launch stream) ----
+    stage_sum, nprof = {}, 0
+    for blk in blocks:
+        blk.profile(True)
+    for i in range(args.profile_steps):
+        step(i)
+        for k, v in blocks[i % len(blocks)].stage_times().items():
+            stage_sum[k] = stage_sum.get(k, 0.0) + v
+        nprof += 1
+    for blk in blocks:
+        blk.profile(False)
+    stages = {k: v / nprof for k, v in stage_sum.items()}
+    log("bench: stages " + ", ".join(f"{k} {v:.3f}" for k, v in stages.items()) + " ms")
 
-    kernels = {}
-    # attention: 4096 image queries over 256 prefix + 4096 own keys
-    q = torch.randn((1, HEADS, S_IMG, HD), generator=g, device="cuda").to(torch.bfloat16)
-    ko = torch.randn((1, HEADS, S_IMG, HD), generator=g, device="cuda").to(torch.bfloat16)
-    vt = torch.randn((1, HEADS, HD, S_IMG), generator=g, device="cuda").to(torch.bfloat16)
-    ao = torch.empty((1, S_IMG, HID), dtype=torch.bfloat16, device="cuda")
-    att_ms = time_it(lambda: ctx.attention(q.data_ptr(), 1, HEADS, S_IMG, kv, 0, ko.data_ptr(), vt.data_ptr(),
-                                           S_IMG, HD ** -0.5, ao.data_ptr(), sh), args.kernel_iters)
     att_flop = 4.0 * HEADS * S_IMG * (S_IMG + P_TXT) * HD
-    kernels["attention"] = {"ms": att_ms, "gflop": att_flop / 1e9, "tflops": att_flop / att_ms / 1e9}
-    del q, ko, vt, ao
-
-    # dequant-GEMMs with the step's shapes (M = 4096 tokens)
-    rng = np.random.default_rng(7)
-    a = torch.randn((S_IMG, MLP), generator=g, device="cuda").to(torch.bfloat16)
-    y = torch.empty((S_IMG, 2 * MLP), dtype=torch.bfloat16, device="cuda")
-    for name, t, n, k in (("gemm_qkv", synth.Q4_K, 3 * HID, HID), ("gemm_out", synth.Q4_K, HID, HID),
-                          ("gemm_gate_up", synth.Q4_K, 2 * MLP, HID), ("gemm_down", synth.Q6_K, HID, MLP)):
-        wb = synth.random_blocks(rng, t, n, k)
-        W = ctx.upload(t, n, k, wb.tobytes())
-        ms = time_it(lambda: ctx.qmatmul(W, a.data_ptr(), S_IMG, k, y.data_ptr(), synth.BF16, sh), args.kernel_iters)
-        flop = 2.0 * S_IMG * n * k
-        kernels[name] = {"ms": ms, "gflop": flop / 1e9, "tflops": flop / ms / 1e9,
-                         "weight_gbps": wb.size / ms / 1e6, "weight_mb": wb.size / 1e6}
-        W.free()
-    del a, y
+    gemm = {"qkv": (3 * HID, HID), "out_proj": (HID, HID), "gate_up": (2 * MLP, HID), "down": (HID, MLP)}
+    kernels = {"attention": {"ms": stages["attention"], "gflop": att_flop / 1e9}}
+    for name, (n, k) in gemm.items():
+        kernels[name] = {"ms": stages[name], "gflop": 2.0 * S_IMG * n * k / 1e9}
+    qk4 = synth.row_bytes(synth.Q4_K, HID)
+    kernels["qkv"]["weight_bytes"] = 3 * HID * qk4
+    kernels["out_proj"]["weight_bytes"] = HID * qk4
+    kernels["gate_up"]["weight_bytes"] = 2 * MLP * qk4
+    kernels["down"]["weight_bytes"] = HID * synth.row_bytes(synth.Q6_K, MLP)
     for kname, kd in kernels.items():
+        kd["tflops"] = kd["gflop"] / kd["ms"]
         kd["frac_bf16_peak"] = kd["tflops"] / PEAK_BF16_TFLOPS
+        if "weight_bytes" in kd:
+            kd["weight_gbps"] = kd["weight_bytes"] / kd["ms"] / 1e6
         log(f"bench: {kname}: {kd['ms']:.3f} ms, {kd['tflops']:.1f} TFLOP/s")
 
     dom_name = max(kernels, key=lambda n: kernels[n]["ms"])
@@ -215,6 +203,7 @@ def main():
         "attention_frac_bf16_peak": round(kernels["attention"]["frac_bf16_peak"], 4),
         "block_tflops": round(block_flop / ms_step / 1e9, 2),
         "block_frac_bf16_peak": round(block_flop / ms_step / 1e9 / PEAK_BF16_TFLOPS, 4),
+        "stages_ms": {k: round(v, 4) for k, v in stages.items()},
         "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},
         "roofline": roofline,
         "cpu_baseline": cpu,

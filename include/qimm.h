@@ -213,6 +213,19 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
                        int64_t seq, const float *mod, const float *pe, const qimm_kv *kv,
                        int64_t layer, uint16_t *k_out, uint16_t *v_out, void *stream);
 
+/* Stage timing of qimm_block_forward, the device-side counterpart of the
+ * reference's per-phase wall-clock prints (src/service.rs:190-203). While
+ * enabled, each forward records HIP events on its stream around its stages;
+ * qimm_block_stage_times waits for the last forward and writes the durations
+ * in ms of its QIMM_BLOCK_STAGES stages:
+ *   0 modulation prep + norm1   1 q/k/v projection + norm + RoPE
+ *   2 attention                 3 output projection + gated residual
+ *   4 norm2                     5 gate_up projection + SwiGLU
+ *   6 down projection + gated residual */
+#define QIMM_BLOCK_STAGES 7
+int qimm_block_profile(qimm_block *blk, int enable);
+int qimm_block_stage_times(qimm_block *blk, float *ms_out, int n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,6 +65,8 @@ void free_block(qimm_block *b) {
         if (w) qimm_weight_free(w);
     if (b->norm_q) (void)hipFree(b->norm_q);
     if (b->norm_k) (void)hipFree(b->norm_k);
+    for (hipEvent_t e : b->ev)
+        if (e) (void)hipEventDestroy(e);
     delete b;
 }
 
@@ -195,10 +197,14 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     uint16_t *kb = k_out ? k_out : (uint16_t *)(ws + o_k);
     uint16_t *vt = (uint16_t *)(ws + o_vt), *att = (uint16_t *)(ws + o_att), *hm = (uint16_t *)(ws + o_h);
 
+#define STAGE_MARK(i) \
+    if (blk->profiling) QIMM_HIP(ctx, hipEventRecord(blk->ev[i], s))
+    STAGE_MARK(0);
     // modulation.chunk(4) -> (1 + scale1, tanh gate1, 1 + scale2, tanh gate2)
     QIMM_HIP(ctx, qimm::launch_mod_prep(mod, batch, hid, modp, s));
     // norm1(x) * (1 + scale1)                                  (:267-269)
     QIMM_HIP(ctx, qimm::launch_ln_mod(x, M, hid, modp, 4 * hid, seq, xn, s));
+    STAGE_MARK(1);
     // to_q/to_k/to_v + per-head RmsNorm + RoPE                 (:133-142)
     qimm::EpiParams ep{};
     ep.q = qb;
@@ -221,10 +227,12 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
             QIMM_HIP(ctx, qimm::launch_qgemm(parts[i]->gw, xn, M, hid, qimm::EPI_QKV, ep, s));
         }
     }
+    STAGE_MARK(2);
     // attention over [prefix ; own]                            (:143-148)
     QIMM_HIP(ctx, qimm::launch_attention(qb, kv ? kv->k + layer * kv->layer_elems() : nullptr,
                                          kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, kb, vt, seq,
                                          batch, H, seq, 1.0f / sqrtf(128.0f), att, s));
+    STAGE_MARK(3);
     // x1 = x + tanh(gate1) * to_out(attn)                       (:150-151, 271-273)
     qimm::EpiParams er{};
     er.x_in = x;
@@ -233,13 +241,16 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     er.g_stride = 4 * hid;
     er.g_rows_per = seq;
     QIMM_HIP(ctx, qimm::launch_qgemm(blk->out->gw, att, M, hid, qimm::EPI_RESID, er, s));
+    STAGE_MARK(4);
     // norm2(x1) * (1 + scale2)                                 (:276-278)
     QIMM_HIP(ctx, qimm::launch_ln_mod(x_out, M, hid, modp + 2 * hid, 4 * hid, seq, xn, s));
+    STAGE_MARK(5);
     // silu(gate) * up                                          (:191-201)
     qimm::EpiParams eg{};
     eg.hmid = hm;
     eg.ldh = F;
     QIMM_HIP(ctx, qimm::launch_qgemm(blk->gate_up->gw, xn, M, hid, qimm::EPI_SWIGLU, eg, s));
+    STAGE_MARK(6);
     // x2 = x1 + tanh(gate2) * out(hidden)                       (:202, 280-282)
     qimm::EpiParams ed{};
     ed.x_in = x_out;
@@ -248,6 +259,31 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     ed.g_stride = 4 * hid;
     ed.g_rows_per = seq;
     QIMM_HIP(ctx, qimm::launch_qgemm(blk->down->gw, hm, M, F, qimm::EPI_RESID, ed, s));
+    STAGE_MARK(7);
+#undef STAGE_MARK
+    if (blk->profiling) blk->profiled_once = true;
+    return QIMM_OK;
+}
+
+int qimm_block_profile(qimm_block *blk, int enable) {
+    if (!blk) return QIMM_ERR_ARG;
+    qimm_ctx *ctx = blk->ctx;
+    if (enable && !blk->ev[0]) {
+        QIMM_HIP(ctx, hipSetDevice(ctx->device));
+        for (int i = 0; i <= QIMM_BLOCK_STAGES; i++) QIMM_HIP(ctx, hipEventCreate(&blk->ev[i]));
+    }
+    blk->profiling = enable != 0;
+    blk->profiled_once = false;
+    return QIMM_OK;
+}
+
+int qimm_block_stage_times(qimm_block *blk, float *ms_out, int n) {
+    if (!blk || !ms_out || n < QIMM_BLOCK_STAGES) return QIMM_ERR_ARG;
+    qimm_ctx *ctx = blk->ctx;
+    if (!blk->profiled_once) return set_err(ctx, QIMM_ERR_STATE, "stage times: no profiled forward since enabling");
+    QIMM_HIP(ctx, hipEventSynchronize(blk->ev[QIMM_BLOCK_STAGES]));
+    for (int i = 0; i < QIMM_BLOCK_STAGES; i++)
+        QIMM_HIP(ctx, hipEventElapsedTime(&ms_out[i], blk->ev[i], blk->ev[i + 1]));
     return QIMM_OK;
 }
 

@@ -46,6 +46,10 @@ struct qimm_block {
     qimm_weight *gate_up = nullptr;      // rows interleaved per 64: gate | up
     qimm_weight *down = nullptr;
     float *norm_q = nullptr, *norm_k = nullptr;  // device [128]
+    // stage timing (qimm_block_profile): events around the stages of a forward
+    bool profiling = false;
+    bool profiled_once = false;
+    hipEvent_t ev[QIMM_BLOCK_STAGES + 1] = {};
 };
 
 namespace qimm_host {

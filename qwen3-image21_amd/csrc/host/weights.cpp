@@ -63,8 +63,9 @@ static inline float f16_to_f32(uint16_t h) {
 int upload_weight_rows(qimm_ctx *ctx, int type, int64_t rows, int64_t cols, const uint8_t *src,
                        qimm_weight **out) {
     *out = nullptr;
+    if (!block_values(type)) return set_err(ctx, QIMM_ERR_TYPE, "weight: unsupported GGML type");
     const int64_t rb = row_bytes(type, cols);
-    if (rb < 0) return set_err(ctx, QIMM_ERR_TYPE, "weight: unsupported GGML type or cols not a block multiple");
+    if (rb < 0) return set_err(ctx, QIMM_ERR_SHAPE, "weight: cols is not a multiple of the block size");
     if (rows <= 0 || cols <= 0) return set_err(ctx, QIMM_ERR_SHAPE, "weight: empty tensor");
     qimm_weight *w = new (std::nothrow) qimm_weight();
     if (!w) return QIMM_ERR_OOM;
@@ -149,8 +150,9 @@ extern "C" {
 int qimm_weight_upload(qimm_ctx *ctx, int ggml_type, int64_t rows, int64_t cols, const void *host_bytes,
                        size_t nbytes, qimm_weight **out) {
     if (!ctx || !host_bytes || !out) return QIMM_ERR_ARG;
+    if (!block_values(ggml_type)) return set_err(ctx, QIMM_ERR_TYPE, "weight: unsupported GGML type");
     const int64_t rb = row_bytes(ggml_type, cols);
-    if (rb < 0) return set_err(ctx, QIMM_ERR_TYPE, "weight: unsupported GGML type or cols not a block multiple");
+    if (rb < 0) return set_err(ctx, QIMM_ERR_SHAPE, "weight: cols is not a multiple of the block size");
     if (rows <= 0 || (size_t)(rb * rows) != nbytes)
         return set_err(ctx, QIMM_ERR_SHAPE, "weight: byte count does not match rows x cols");
     return upload_weight_rows(ctx, ggml_type, rows, cols, (const uint8_t *)host_bytes, out);

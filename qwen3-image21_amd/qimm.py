@@ -59,7 +59,10 @@ SIGNATURES = [
     ("qimm_block_create", _i32, [_vp, _vp, _vp, C.POINTER(_vp)]),
     ("qimm_block_destroy", _i32, [_vp]),
     ("qimm_block_forward", _i32, [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp]),
+    ("qimm_block_profile", _i32, [_vp, _i32]),
+    ("qimm_block_stage_times", _i32, [_vp, C.POINTER(C.c_float), _i32]),
 ]
+BLOCK_STAGES = ("norm1", "qkv", "attention", "out_proj", "norm2", "gate_up", "down")
 
 
 class BlockConfig(C.Structure):
@@ -215,6 +218,15 @@ class Block:
         self.ctx.check(self.ctx.lib.qimm_block_forward(self.h, x_dev, x_out_dev, batch, seq, mod_dev, pe_dev,
                                                        kv.h if kv else None, layer, k_out, v_out, stream),
                        "qimm_block_forward")
+
+    def profile(self, enable: bool = True):
+        self.ctx.check(self.ctx.lib.qimm_block_profile(self.h, 1 if enable else 0), "qimm_block_profile")
+
+    def stage_times(self) -> dict:
+        """ms per stage of the last forward since profiling was enabled."""
+        ms = (C.c_float * len(BLOCK_STAGES))()
+        self.ctx.check(self.ctx.lib.qimm_block_stage_times(self.h, ms, len(BLOCK_STAGES)), "qimm_block_stage_times")
+        return dict(zip(BLOCK_STAGES, list(ms)))
 
     def free(self):
         if self.h:

@@ -2,10 +2,14 @@
 step, src/quantized_transformer.rs:258-285) through qimm_block_create /
 qimm_block_forward, against the oracle on identical seeded inputs.
 
-Bar (north star): cosine >= 0.9999 and max|a-b|/max|b| <= 2e-2 against the
-oracle's f32 candle-mode output. The cosine is taken on the block's update
-x_out - x (stricter than on x_out, where the residual dominates); the
-max-abs-rel on x_out. The own k / v the block returns are checked the same way.
+Bars: against the oracle's f32 candle-mode output (int8 activations, the
+reference CPU path), the block output reaches cosine >= 0.9999 and
+max|a-b|/max|b| <= 2e-2. Against the oracle's exact mode (f32 activations, f64
+accumulation), the stricter cosine of the block's update x_out - x (the
+residual excluded) is >= 0.9999 as well; candle mode itself sits at update
+cosine ~0.99982-0.99994 from exact mode because of its int8 activations, so the
+update metric is only meaningful against exact mode. The own k / v the block
+returns are checked against both modes.
 """
 import ctypes as C
 
@@ -42,15 +46,16 @@ def run_block(torch, qctx, cfg, w, x, mod, pe, kpre=None, vpre=None, alias=False
     x_dev = dev(torch, x)
     x_out = x_dev if alias else torch.empty_like(x_dev)
     kv = None
+    mod_d, pe_d = dev(torch, mod), dev(torch, pe)  # device buffers stay referenced until the step ran
     if kpre is not None:
         kv = qctx.kv_create(3, b, cfg["heads"], kpre.shape[2])
-        kv.store(2, dev(torch, kpre.view(np.int16)).data_ptr(), dev(torch, vpre.view(np.int16)).data_ptr(),
-                 stream(torch))
+        k_d, v_d = dev(torch, kpre.view(np.int16)), dev(torch, vpre.view(np.int16))
+        kv.store(2, k_d.data_ptr(), v_d.data_ptr(), stream(torch))
     k_out = v_out = None
     if want_kv:
         k_out = torch.empty((b, cfg["heads"], s, 128), dtype=torch.bfloat16, device="cuda")
         v_out = torch.empty_like(k_out)
-    blk.forward(x_dev.data_ptr(), x_out.data_ptr(), b, s, dev(torch, mod).data_ptr(), dev(torch, pe).data_ptr(),
+    blk.forward(x_dev.data_ptr(), x_out.data_ptr(), b, s, mod_d.data_ptr(), pe_d.data_ptr(),
                 kv, 2, k_out.data_ptr() if want_kv else None, v_out.data_ptr() if want_kv else None, stream(torch))
     out = host(x_out)
     kvs = (host(k_out.float()), host(v_out.float())) if want_kv else (None, None)
@@ -79,8 +84,10 @@ def make_case(seed, cfg, b, s, p, attn_type, down_type, fused=True):
 SMALL = dict(hidden=256, heads=2, head_dim=128, mlp=768)
 
 
-def check(got, ref, x):
-    cs = cos_sim(got - x, ref - x)
+def check(got, ref, x, exact=False):
+    """exact=False: ref is candle mode, cosine on the output; exact=True: ref is
+    exact mode, cosine on the update."""
+    cs = cos_sim(got - x, ref - x) if exact else cos_sim(got, ref)
     mr = max_abs_rel(got, ref)
     assert cs >= 0.9999 and mr <= 2e-2, (cs, mr)
 
@@ -94,9 +101,10 @@ def test_block_matches_oracle(torch_cuda, qctx, attn_type, down_type, b, s, p):
     ref, kr, vr = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
     check(got, ref, x)
     ref_e, kre, vre = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
-    check(got, ref_e, x)
-    assert cos_sim(k, kr) >= 0.9999 and max_abs_rel(k, kr) <= 2e-2
-    assert cos_sim(v, vr) >= 0.9999 and max_abs_rel(v, vr) <= 2e-2
+    check(got, ref_e, x, exact=True)
+    for kk, vv in ((kr, vr), (kre, vre)):
+        assert cos_sim(k, kk) >= 0.9999 and max_abs_rel(k, kk) <= 2e-2
+        assert cos_sim(v, vv) >= 0.9999 and max_abs_rel(v, vv) <= 2e-2
 
 
 def test_block_in_place_and_separate_mlp_inputs(torch_cuda, qctx):
@@ -104,6 +112,8 @@ def test_block_in_place_and_separate_mlp_inputs(torch_cuda, qctx):
     got, _ = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre, alias=True)
     ref, _, _ = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
     check(got, ref, x)
+    ref_e, _, _ = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
+    check(got, ref_e, x, exact=True)
 
 
 def test_block_mixed_qkv_types_unfused_path(torch_cuda, qctx):
@@ -113,6 +123,8 @@ def test_block_mixed_qkv_types_unfused_path(torch_cuda, qctx):
     got, _ = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre)
     ref, _, _ = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
     check(got, ref, x)
+    ref_e, _, _ = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
+    check(got, ref_e, x, exact=True)
 
 
 def test_block_deterministic(torch_cuda, qctx):
@@ -130,6 +142,8 @@ def test_block_config1_shape(torch_cuda, qctx):
     got, _ = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
     ref, _, _ = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
     check(got, ref, x)
+    ref_e, _, _ = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
+    check(got, ref_e, x, exact=True)
 
 
 def test_block_rejects_bad_config(torch_cuda, qctx):

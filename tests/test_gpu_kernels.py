@@ -187,11 +187,11 @@ def test_qk_norm_rope_matches_oracle(torch_cuda, qctx):
     w = (1 + 0.02 * rng.standard_normal(128)).astype(np.float32)
     pe = O.rope_table([(1, 5, 8)], [1] * s)
     out = torch.empty((b, h, s, 128), dtype=torch.bfloat16, device="cuda")
-    qctx.qk_norm_rope(dev(torch, x).data_ptr(), b, s, h, dev(torch, w).data_ptr(), dev(torch, pe).data_ptr(),
-                      out.data_ptr(), stream(torch))
+    x_d, w_d, pe_d = dev(torch, x), dev(torch, w), dev(torch, pe)
+    qctx.qk_norm_rope(x_d.data_ptr(), b, s, h, w_d.data_ptr(), pe_d.data_ptr(), out.data_ptr(), stream(torch))
     got = host(out.float())
     want = O.apply_rope(O.rmsnorm(x, w).transpose(0, 2, 1, 3), pe)
     assert np.max(np.abs(got - want)) <= 2 ** -7 * np.abs(want).max()
     vt = torch.empty((b, h, 128, s), dtype=torch.bfloat16, device="cuda")
-    qctx.v_transpose(dev(torch, x).data_ptr(), b, s, h, vt.data_ptr(), stream(torch))
+    qctx.v_transpose(x_d.data_ptr(), b, s, h, vt.data_ptr(), stream(torch))
     assert np.array_equal(host(vt.float()), O.bf16_round(x.transpose(0, 2, 3, 1)))

@@ -53,8 +53,13 @@ struct GemmWeight {
 };
 
 // y = A[M,K] (bf16, row stride lda) x W[N,K]^T with the epilogue selected by epi.
+// Dispatches to the 256x256 large-M kernel when qgemm_large_fits, else to the
+// 128x128 kernel.
 hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda,
                         int epi, const EpiParams &ep, hipStream_t stream);
+bool qgemm_large_fits(const GemmWeight &w, int64_t m);
+hipError_t launch_qgemm_large(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda,
+                              int epi, const EpiParams &ep, hipStream_t stream);
 
 // Exact GGUF dequantization of raw block bytes (device) to f32 (device).
 hipError_t launch_dequant(int ggml_type, const uint8_t *src, int64_t n, float *out,

@@ -171,12 +171,12 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(const uint16_t *__restric
     u32x4 ra[4];
     WRaw rw;
 
+    // rows past M are clamped to row M-1: they only feed unwritten output rows
     auto load_a = [&](int64_t k0) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int64_t gm = m0 + a_row + 32 * i;
-            if (gm < M) ra[i] = *(const u32x4 *)(A + gm * lda + k0 + a_kc);
-            else ra[i] = u32x4{0u, 0u, 0u, 0u};
+            const int64_t gm = min(m0 + a_row + 32 * i, M - 1);
+            ra[i] = *(const u32x4 *)(A + gm * lda + k0 + a_kc);
         }
     };
     auto store_a = [&](uint16_t *as) {
@@ -390,6 +390,7 @@ hipError_t launch_fmt(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t
 hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
                         const EpiParams &ep, hipStream_t stream) {
     if (m <= 0) return hipSuccess;
+    if (qgemm_large_fits(w, m)) return launch_qgemm_large(w, a, m, lda, epi, ep, stream);
     switch (w.fmt) {
     case WF_Q8_0: return launch_fmt<WF_Q8_0>(w, a, m, lda, epi, ep, stream);
     case WF_Q4_K: return launch_fmt<WF_Q4_K>(w, a, m, lda, epi, ep, stream);

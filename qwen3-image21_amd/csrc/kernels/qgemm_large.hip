@@ -1,0 +1,498 @@
+// Large-M dequant-GEMM for gfx950 (M >= 512 token rows): C = A (bf16) x W^T
+// (GGUF blocks), same epilogues as the 128x128 kernel.
+//
+// Replaces candle's QMatMul::forward (src/quantized_transformer.rs:19-33) on
+// the block's token-parallel projections (call sites 133-135, 151, 196, 202).
+//
+// Tile 256x256x64, 256 threads = 4 waves in a 2x2 grid, each wave 128x128 as
+// 4x4 v_mfma_f32_32x32x16_bf16 tiles (accumulators live in AGPRs), one
+// workgroup per CU. Per 16-wide k slice a wave reads 8 KB of operands from LDS
+// for 16 MFMAs, half the LDS traffic per flop of a 64x64 wave tile. LDS rows
+// are dense 128 B with the 16 B chunk index XOR-swizzled by (row & 7), so both
+// the staging writes and the MFMA operand reads are bank-conflict free.
+// The A tile goes global->LDS directly (no registers), one k step ahead; the
+// raw weights of step k+2 are loaded while step k computes and the weights of
+// step k+1 are dequantized into the other LDS stage between its MFMAs. The q/k/v epilogue stages its outputs
+// through LDS; the others work on the accumulators in place.
+// Tiles are ordered XCD-aware: each XCD gets a contiguous range of tiles,
+// grouped 4 M-tiles at a time so concurrently resident tiles share A rows and
+// W columns in that XCD's L2.
+#include "device_common.h"
+#include "kernels.h"
+
+namespace qimm {
+namespace {
+
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int ROWB = 128;                      // bytes per LDS row: 64 bf16
+constexpr int STAGE = 2 * 256 * ROWB;          // A rows then B rows: 64 KB
+constexpr int LDS_BYTES = 2 * STAGE;           // 128 KB
+constexpr int GROUP_M = 4;
+
+// 16 B chunk c of LDS row r sits at slot c ^ key(r), key = (r & 7) ^ ((r >> 3) & 1).
+// Measured on gfx950: 16 B reads are served 16 lanes (256 B) per cycle and are
+// conflict free when the 16 rows of a group cover all 16 slots of a 256 B
+// window (same-parity rows need distinct keys); 16 B writes are served 8 lanes
+// (128 B) per cycle and need distinct keys on each aligned group of 8 rows.
+// This key satisfies both.
+__device__ __forceinline__ int swz_key(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int swz(int r, int c) { return r * ROWB + ((c ^ swz_key(r)) << 4); }
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+// A word whose value the optimizer must not look through (keeps nibble masks as
+// whole-word ops so the byte converts below stay v_cvt_f32_ubyte{0..3}).
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+__device__ __forceinline__ uint32_t byte_of(const u32x4 &x, int i) {
+    return (x[i >> 2] >> (8 * (i & 3))) & 0xffu;
+}
+
+// Q4_K 6-bit scale/min of sub-block j from the 12 packed bytes at bytes 4..15
+// of the block header word (GGML layout).
+__device__ __forceinline__ void q4k_sc_m(const u32x4 &h, int j, float &sc, float &mn) {
+    uint32_t s, m;
+    if (j < 4) {
+        s = byte_of(h, 4 + j) & 63u;
+        m = byte_of(h, 8 + j) & 63u;
+    } else {
+        s = (byte_of(h, 8 + j) & 0xFu) | ((byte_of(h, j) >> 6) << 4);
+        m = (byte_of(h, 8 + j) >> 4) | ((byte_of(h, 4 + j) >> 6) << 4);
+    }
+    sc = (float)s;
+    mn = (float)m;
+}
+
+// 8 unsigned byte codes (two words) -> 8 bf16 of code*ds + off (exact f32 value,
+// rounded to nearest even).
+__device__ __forceinline__ u32x4 cvt8(uint32_t x0, uint32_t x1, float ds, float off) {
+    auto f = [&](uint32_t x, int i) { return __builtin_fmaf((float)((x >> (8 * i)) & 0xffu), ds, off); };
+    return u32x4{pack_bf16x2(f(x0, 0), f(x0, 1)), pack_bf16x2(f(x0, 2), f(x0, 3)),
+                 pack_bf16x2(f(x1, 0), f(x1, 1)), pack_bf16x2(f(x1, 2), f(x1, 3))};
+}
+
+__device__ __forceinline__ uint32_t word(const u32x4 *v, int byte_off) {
+    return v[byte_off >> 4][(byte_off >> 2) & 3];
+}
+
+// Raw bytes of one weight row for one 64-wide k step.
+struct WRaw {
+    u32x4 v[8];
+    uint32_t s;
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_w(const GemmWeight &w, int64_t n, int64_t k0, WRaw &r) {
+    const int64_t K = w.k;
+    if constexpr (FMT == WF_Q8_0) {
+        const uint8_t *p = w.q + n * K + k0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.v[i] = *(const u32x4 *)(p + 16 * i);
+        r.s = *(const uint32_t *)(w.scales + n * (K / 32) + k0 / 32);
+    } else if constexpr (FMT == WF_Q4_K) {
+        const uint8_t *blk = w.q + (n * (K / 256) + k0 / 256) * 144;
+        const int c = (int)((k0 & 255) >> 6);
+        r.v[0] = *(const u32x4 *)blk;
+        r.v[1] = *(const u32x4 *)(blk + 16 + 32 * c);
+        r.v[2] = *(const u32x4 *)(blk + 32 + 32 * c);
+    } else if constexpr (FMT == WF_Q6_K) {
+        const uint8_t *blk = w.q + (n * (K / 256) + k0 / 256) * 224;
+        const int hh = (int)((k0 & 255) >> 7);
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.v[i] = *(const u32x4 *)(blk + 64 * hh + 16 * i);
+        r.v[4] = *(const u32x4 *)(blk + 128 + 32 * hh);
+        r.v[5] = *(const u32x4 *)(blk + 144 + 32 * hh);
+        r.v[6] = *(const u32x4 *)(blk + 192);
+        r.s = *(const uint16_t *)(blk + 208);
+    } else {
+        const uint8_t *p = w.q + (n * K + k0) * 2;
+#pragma unroll
+        for (int i = 0; i < 8; i++) r.v[i] = *(const u32x4 *)(p + 16 * i);
+    }
+}
+
+// Per-step dequant constants of one row.
+struct WScale {
+    float a0, b0, a1, b1, a2, b2, a3, b3;
+};
+
+template <int FMT>
+__device__ __forceinline__ WScale w_scales(const WRaw &r, int64_t k0) {
+    WScale s{};
+    if constexpr (FMT == WF_Q8_0) {
+        const float d0 = f16_bits_to_f32(r.s & 0xffffu), d1 = f16_bits_to_f32(r.s >> 16);
+        s.a0 = d0;  // codes biased to unsigned: (q+128)*d - 128*d, exact
+        s.b0 = -128.f * d0;
+        s.a1 = d1;
+        s.b1 = -128.f * d1;
+    } else if constexpr (FMT == WF_Q4_K) {
+        const int c = (int)((k0 & 255) >> 6);
+        const float d = f16_bits_to_f32(r.v[0][0] & 0xffffu), dmin = f16_bits_to_f32(r.v[0][0] >> 16);
+        float sc0, m0, sc1, m1;
+        q4k_sc_m(r.v[0], 2 * c, sc0, m0);
+        q4k_sc_m(r.v[0], 2 * c + 1, sc1, m1);
+        s.a0 = d * sc0;
+        s.b0 = -(dmin * m0);
+        s.a1 = d * sc1;
+        s.b1 = -(dmin * m1);
+    } else if constexpr (FMT == WF_Q6_K) {
+        // values 32 r + l of half hh, r in {2o, 2o+1}; scale index 8hh + 2r + l/16
+        const int hh = (int)((k0 & 255) >> 7), o = (int)((k0 & 127) >> 6);
+        const float d = f16_bits_to_f32(r.s);
+        const int base = 8 * hh + 4 * o;
+        s.a0 = d * (float)(int8_t)byte_of(r.v[6], base + 0);
+        s.a1 = d * (float)(int8_t)byte_of(r.v[6], base + 1);
+        s.a2 = d * (float)(int8_t)byte_of(r.v[6], base + 2);
+        s.a3 = d * (float)(int8_t)byte_of(r.v[6], base + 3);
+        s.b0 = -32.f * s.a0;  // (q+32)*ds - 32*ds, exact
+        s.b1 = -32.f * s.a1;
+        s.b2 = -32.f * s.a2;
+        s.b3 = -32.f * s.a3;
+    }
+    return s;
+}
+
+// bf16 values k in [8j, 8j+8) of the step.
+template <int FMT>
+__device__ __forceinline__ u32x4 w_chunk(const WRaw &r, const WScale &s, int j, int64_t k0) {
+    if constexpr (FMT == WF_Q8_0) {
+        const uint32_t x0 = opaque(word(r.v, 8 * j) ^ 0x80808080u), x1 = opaque(word(r.v, 8 * j + 4) ^ 0x80808080u);
+        return j < 4 ? cvt8(x0, x1, s.a0, s.b0) : cvt8(x0, x1, s.a1, s.b1);
+    } else if constexpr (FMT == WF_Q4_K) {
+        // k < 32: low nibbles of qs bytes [8j, 8j+8); k >= 32: high nibbles of bytes [8(j-4), ...)
+        const int jb = j & 3;
+        const uint32_t y0 = word(r.v + 1, 8 * jb), y1 = word(r.v + 1, 8 * jb + 4);
+        if (j < 4) return cvt8(opaque(y0 & 0x0F0F0F0Fu), opaque(y1 & 0x0F0F0F0Fu), s.a0, s.b0);
+        return cvt8(opaque((y0 >> 4) & 0x0F0F0F0Fu), opaque((y1 >> 4) & 0x0F0F0F0Fu), s.a1, s.b1);
+    } else if constexpr (FMT == WF_Q6_K) {
+        // k = 32 rl + l with rl = j/4, l in [8(j%4), +8): low 4 bits from ql byte
+        // 32 rl + l (low nibble when o == 0, else high), high 2 bits from qh byte l
+        // >> 2r with r = 2o + rl; scale index 2 rl + l/16.
+        const int o = (int)((k0 & 127) >> 6);
+        const int rl = j >> 2, l0 = 8 * (j & 3);
+        const int rr = 2 * o + rl;
+        uint32_t q0 = word(r.v, 32 * rl + l0), q1 = word(r.v, 32 * rl + l0 + 4);
+        if (o) {
+            q0 >>= 4;
+            q1 >>= 4;
+        }
+        const uint32_t h0 = word(r.v + 4, l0), h1 = word(r.v + 4, l0 + 4);
+        const uint32_t c0 = opaque((q0 & 0x0F0F0F0Fu) | (((h0 >> (2 * rr)) & 0x03030303u) << 4));
+        const uint32_t c1 = opaque((q1 & 0x0F0F0F0Fu) | (((h1 >> (2 * rr)) & 0x03030303u) << 4));
+        const int si = 2 * rl + (l0 >> 4);
+        const float a = si == 0 ? s.a0 : (si == 1 ? s.a1 : (si == 2 ? s.a2 : s.a3));
+        const float b = si == 0 ? s.b0 : (si == 1 ? s.b1 : (si == 2 ? s.b2 : s.b3));
+        return cvt8(c0, c1, a, b);
+    } else {
+        return r.v[j];
+    }
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+template <int FMT, int EPI>
+__global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__restrict__ A, int64_t M,
+                                                             int64_t lda, GemmWeight w, EpiParams ep,
+                                                             int mt, int nt) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, l32 = lane & 31, g = lane >> 5;
+
+    // XCD-aware, M-grouped tile order
+    const int total = mt * nt;
+    int L = blockIdx.x;
+    if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
+    const int per_group = GROUP_M * nt;
+    const int grp = L / per_group;
+    const int first_m = grp * GROUP_M;
+    const int gm = min(mt - first_m, GROUP_M);
+    const int mtile = first_m + (L % per_group) % gm;
+    const int ntile = (L % per_group) / gm;
+    const int64_t m0 = (int64_t)mtile * BM, n0 = (int64_t)ntile * BN;
+    const int64_t K = w.k;
+    const int KT = (int)(K / BK);
+
+    // A staging by direct global->LDS loads (16 B per lane, lane l lands at
+    // base + 16 l): instruction i of wave w fills LDS rows 8(8w+i) .. +8, lane l
+    // row 8(8w+i) + l/8 at slot l%8, which must hold logical chunk
+    // (l%8) ^ swz_key(row). Rows past M are clamped to row M-1: they only feed
+    // output rows the epilogue never writes.
+    const uint16_t *asrc[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int row = 8 * (8 * wave + i) + (lane >> 3);
+        const int c = (lane & 7) ^ swz_key(row);
+        asrc[i] = A + min(m0 + row, M - 1) * lda + 8 * c;
+    }
+    auto dma_a = [&](int stage, int64_t k0) {
+        uint8_t *base = lds + stage * STAGE;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(asrc[i] + k0), (lds_ptr_t)(base + (8 * wave + i) * 8 * ROWB),
+                                             16, 0, 0);
+    };
+    // W staging: row n0 + tid, all 8 chunks, through registers (dequantized)
+    const int64_t wrow = n0 + tid;
+    WRaw rw0, rw1;
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    // MFMAs of one stage; with `store`, the weights in rw (step at knext) are
+    // dequantized into the other stage, two 8-wide chunks after each group of
+    // eight MFMAs so the VALU work overlaps the matrix pipe.
+    auto compute = [&](int stage, const WRaw &rw, int64_t knext, bool store) {
+        const uint8_t *as = lds + stage * STAGE;
+        const uint8_t *bs = as + 256 * ROWB;
+        uint8_t *bn = lds + (stage ^ 1) * STAGE + 256 * ROWB;
+        WScale sc{};
+        if (store) sc = w_scales<FMT>(rw, knext);
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            bf16x8 af[4], bfr[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = wm * 128 + i * 32 + l32;
+                af[i] = *(const bf16x8 *)(as + swz(r, 2 * kk + g));
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int r = wn * 128 + j * 32 + l32;
+                bfr[j] = *(const bf16x8 *)(bs + swz(r, 2 * kk + g));
+            }
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const int i = 2 * half + (q >> 2), j = q & 3;
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+                }
+                if (store) {
+                    const int c = 2 * kk + half;
+                    *(u32x4 *)(bn + swz(tid, c)) = w_chunk<FMT>(rw, sc, c, knext);
+                }
+            }
+        }
+    };
+
+    // vmcnt(8): every vector-memory op older than the 8 A-tile loads just
+    // issued has completed (loads complete in issue order).
+    constexpr int WAIT_ALL_BUT_8 = 0x0f70 | 8;
+    // prologue: A and W of step 0 into stage 0; W of step 1 in registers; A of
+    // step 1 in flight (step indices clamped to the last step: redundant loads,
+    // no branches)
+    dma_a(0, 0);
+    load_w<FMT>(w, wrow, 0, rw0);
+    {
+        const WScale sc = w_scales<FMT>(rw0, 0);
+        uint8_t *bn = lds + 256 * ROWB;
+#pragma unroll
+        for (int j = 0; j < 8; j++) *(u32x4 *)(bn + swz(tid, j)) = w_chunk<FMT>(rw0, sc, j, 0);
+    }
+    load_w<FMT>(w, wrow, (int64_t)min(1, KT - 1) * BK, rw0);
+    dma_a(1, (int64_t)min(1, KT - 1) * BK);
+    __builtin_amdgcn_s_waitcnt(WAIT_ALL_BUT_8);
+    __syncthreads();
+    // Steady state, one branch-free body. On entry to step kt, stage kt&1 holds
+    // A and W of step kt, rw0 holds the raw weights of step kt+1 and the A tile
+    // of step kt+1 is in flight to stage (kt+1)&1.
+    for (int kt = 0; kt < KT - 1; kt++) {
+        load_w<FMT>(w, wrow, (int64_t)min(kt + 2, KT - 1) * BK, rw1);
+        compute(kt & 1, rw0, (int64_t)(kt + 1) * BK, true);  // + W of step kt+1 into stage (kt+1)&1
+        rw0 = rw1;
+        __syncthreads();  // stage kt&1 is free; W of step kt+1 is staged
+        dma_a(kt & 1, (int64_t)min(kt + 2, KT - 1) * BK);
+        __builtin_amdgcn_s_waitcnt(WAIT_ALL_BUT_8);  // A of step kt+1 has landed
+        __syncthreads();
+    }
+    compute((KT - 1) & 1, rw0, 0, false);
+
+    // ---- epilogue, straight from the accumulators ----
+    // acc[i][j][r] holds row wm*128 + 32i + 8(r/4) + 4g + (r%4) and column
+    // wn*128 + 32j + l32 of the tile: each lane owns one column of 16 rows per
+    // (i, j), 32 lanes cover 32 consecutive columns.
+    const int64_t N = w.n;
+    const int64_t nw = n0 + wn * 128;  // first global column of this wave
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int64_t mi = m0 + wm * 128 + i * 32 + 4 * g;
+        if constexpr (EPI == EPI_F32 || EPI == EPI_BF16 || EPI == EPI_RESID) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int64_t m = mi + 8 * (r >> 2) + (r & 3);
+                if (m >= M) continue;
+                const float *grow = nullptr;
+                if constexpr (EPI == EPI_RESID) grow = ep.gvec + (int64_t)((int)m / (int)ep.g_rows_per) * ep.g_stride;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int64_t n = nw + j * 32 + l32;
+                    const float v = acc[i][j][r];
+                    if constexpr (EPI == EPI_F32) {
+                        ((float *)ep.out)[m * ep.ldo + n] = v;
+                    } else if constexpr (EPI == EPI_BF16) {
+                        ((uint16_t *)ep.out)[m * ep.ldo + n] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
+                    } else {
+                        ep.x_out[m * N + n] = ep.x_in[m * N + n] + grow[n] * v;
+                    }
+                }
+            }
+        } else if constexpr (EPI == EPI_SWIGLU) {
+            // columns 32j + l32 (j < 2) are gate, 64 + 32j + l32 the matching up
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int64_t m = mi + 8 * (r >> 2) + (r & 3);
+                if (m >= M) continue;
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const float h = silu(acc[i][j][r]) * acc[i][j + 2][r];
+                    ep.hmid[m * ep.ldh + nw / 2 + j * 32 + l32] = (uint16_t)(pack_bf16x2(h, 0.f) & 0xffffu);
+                }
+            }
+        }
+    }
+    if constexpr (EPI == EPI_QKV) {
+        // This wave's 128 columns are one head of q, k or v; its 128 rows are
+        // staged as bf16 in a private 32 KB LDS tile (q/k row-major [t][d], v
+        // transposed [d][t]) and then stored as whole 16 B chunks.
+        __syncthreads();  // every wave is done reading the last operand stage
+        uint16_t *tile = (uint16_t *)lds + wave * 128 * 128;
+        const int64_t nb = nw + ep.n_offset;
+        const int sec = (int)(nb / ep.hidden);
+        const int64_t head = (nb % ep.hidden) / 128;
+        const int S = (int)ep.seq;
+        const int64_t H = ep.heads;
+        const int64_t mw = m0 + wm * 128;  // first row of this wave
+        if (sec < 2) {
+            const float *nwt = sec == 0 ? ep.norm_q : ep.norm_k;
+            float wq[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) wq[j] = nwt[j * 32 + l32];
+            const bool odd = lane & 1;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int t = i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    const int s = (int)(min(mw + t, M - 1) % S);
+                    float ss = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) ss += acc[i][j][r] * acc[i][j][r];
+                    ss = group_sum(ss, 32);  // the 32 lanes holding this row
+                    const float rs = 1.0f / sqrtf(ss * (1.0f / 128.0f) + 1e-6f);
+                    const float *pr = ep.pe + (int64_t)s * 128;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int c = j * 32 + l32;
+                        const float x = acc[i][j][r] * rs * wq[j];
+                        const float xp = __shfl_xor(x, 1);  // RoPE partner column c ^ 1
+                        const float cs_ = pr[c & ~1], sn = pr[c | 1];
+                        // even column: x0 c - x1 s; odd column: x0 s + x1 c (x0 is the partner)
+                        const float y = odd ? xp * sn + x * cs_ : x * cs_ - xp * sn;
+                        tile[t * 128 + (c ^ ((t & 7) << 3))] = (uint16_t)(pack_bf16x2(y, 0.f) & 0xffffu);
+                    }
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes landed
+            __builtin_amdgcn_wave_barrier();
+            uint16_t *dst = sec == 0 ? ep.q : ep.k;
+            // 16 lanes per row (16 x 16 B = 256 B), 4 rows per pass
+#pragma unroll 4
+            for (int pass = 0; pass < 32; pass++) {
+                const int t = pass * 4 + (lane >> 4), ch = lane & 15;
+                const int64_t m = mw + t;
+                if (m >= M) continue;
+                const u32x4 v = *(const u32x4 *)(tile + t * 128 + ((ch * 8) ^ ((t & 7) << 3)));
+                const int64_t b = m / S, s = m % S;
+                *(u32x4 *)(dst + ((b * H + head) * S + s) * 128 + ch * 8) = v;
+            }
+        } else {
+            // V^T: tile[d][t], 8-token groups XOR-swizzled by d
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int d = j * 32 + l32;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int t = i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                        tile[d * 128 + (t ^ ((d & 15) << 3))] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.f) & 0xffffu);
+                    }
+                }
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_wave_barrier();
+            // one d row (128 tokens = 256 B) per 16 lanes, 16 B (8 tokens) per lane
+#pragma unroll 4
+            for (int pass = 0; pass < 32; pass++) {
+                const int d = pass * 4 + (lane >> 4), ch = lane & 15;
+                const int64_t m = mw + ch * 8;
+                if (m >= M) continue;
+                const u32x4 v = *(const u32x4 *)(tile + d * 128 + ((ch * 8) ^ ((d & 15) << 3)));
+                const int64_t b = m / S, s = m % S;
+                if ((S & 7) == 0 && m + 7 < M) {
+                    *(u32x4 *)(ep.vt + ((b * H + head) * 128 + d) * S + s) = v;
+                } else {
+                    for (int e = 0; e < 8; e++) {
+                        const int64_t me = m + e;
+                        if (me >= M) break;
+                        ep.vt[((me / S * H + head) * 128 + d) * S + me % S] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+                    }
+                }
+            }
+            if (ep.v_bhsd) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int64_t m = mw + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                        if (m >= M) continue;
+                        const int64_t b = m / S, s = m % S;
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            ep.v_bhsd[((b * H + head) * S + s) * 128 + j * 32 + l32] =
+                                (uint16_t)(pack_bf16x2(acc[i][j][r], 0.f) & 0xffffu);
+                    }
+            }
+        }
+    }
+}
+
+template <int FMT>
+hipError_t launch_fmt(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
+                      const EpiParams &ep, hipStream_t stream) {
+    const int mt = (int)((m + BM - 1) / BM), nt = (int)(w.n / BN);
+    dim3 grid((unsigned)(mt * nt)), block(256);
+    switch (epi) {
+    case EPI_F32: qgemm_large_kernel<FMT, EPI_F32><<<grid, block, 0, stream>>>(a, m, lda, w, ep, mt, nt); break;
+    case EPI_BF16: qgemm_large_kernel<FMT, EPI_BF16><<<grid, block, 0, stream>>>(a, m, lda, w, ep, mt, nt); break;
+    case EPI_QKV: qgemm_large_kernel<FMT, EPI_QKV><<<grid, block, 0, stream>>>(a, m, lda, w, ep, mt, nt); break;
+    case EPI_RESID: qgemm_large_kernel<FMT, EPI_RESID><<<grid, block, 0, stream>>>(a, m, lda, w, ep, mt, nt); break;
+    case EPI_SWIGLU: qgemm_large_kernel<FMT, EPI_SWIGLU><<<grid, block, 0, stream>>>(a, m, lda, w, ep, mt, nt); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool qgemm_large_fits(const GemmWeight &w, int64_t m) { return m >= 512 && w.n % BN == 0 && w.k % BK == 0; }
+
+hipError_t launch_qgemm_large(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
+                              const EpiParams &ep, hipStream_t stream) {
+    switch (w.fmt) {
+    case WF_Q8_0: return launch_fmt<WF_Q8_0>(w, a, m, lda, epi, ep, stream);
+    case WF_Q4_K: return launch_fmt<WF_Q4_K>(w, a, m, lda, epi, ep, stream);
+    case WF_Q6_K: return launch_fmt<WF_Q6_K>(w, a, m, lda, epi, ep, stream);
+    case WF_BF16: return launch_fmt<WF_BF16>(w, a, m, lda, epi, ep, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace qimm

@@ -70,7 +70,8 @@ def _gemm_case(torch, qctx, t, m, n, k, seed, out_type=synth.F32, std=0.02):
 
 
 @pytest.mark.parametrize("t", [synth.Q8_0, synth.Q4_K, synth.Q6_K, synth.BF16])
-@pytest.mark.parametrize("m,n,k", [(1, 128, 256), (17, 256, 512), (130, 384, 1024), (300, 128, 4096)])
+@pytest.mark.parametrize("m,n,k", [(1, 128, 256), (17, 256, 512), (130, 384, 1024), (300, 128, 4096),
+                                   (600, 512, 1024), (1024, 256, 768)])   # the last two: 256x256 kernel
 def test_qmatmul_matches_bf16_weight_products(torch_cuda, qctx, t, m, n, k):
     got, a, w = _gemm_case(torch_cuda, qctx, t, m, n, k, seed=m * 7 + n + k + t)
     Wd = O.dequantize(t, w, n * k).reshape(n, k)
@@ -86,8 +87,9 @@ def test_qmatmul_matches_bf16_weight_products(torch_cuda, qctx, t, m, n, k):
         assert cos_sim(got, yc) >= 0.9999 and max_abs_rel(got, yc) <= 2e-2
 
 
-def test_qmatmul_bf16_output(torch_cuda, qctx):
-    got, a, w = _gemm_case(torch_cuda, qctx, synth.Q4_K, 64, 256, 512, seed=5, out_type=synth.BF16)
+@pytest.mark.parametrize("m", [64, 700])
+def test_qmatmul_bf16_output(torch_cuda, qctx, m):
+    got, a, w = _gemm_case(torch_cuda, qctx, synth.Q4_K, m, 256, 512, seed=5, out_type=synth.BF16)
     want = O.qmatmul(synth.Q4_K, w, 256, 512, a, O.EXACT)
     assert cos_sim(got, want) >= 0.9999 and max_abs_rel(got, want) <= 2e-2
 

@@ -48,6 +48,9 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=16, help="steps timed stage by stage after the loop")
     ap.add_argument("--cpu-rows", type=int, default=4096, help="token rows in the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="first run one plain device copy of this many MiB, the known-size kernel that "
+                         "scales the FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc pass")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the block step is not sharded across GPUs "
@@ -64,6 +67,15 @@ def main():
     ctx = qimm.Context(0)
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib * (1 << 18)
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log(f"bench: calibration copy of {args.copy_calibration_mib} MiB done")
 
     # ---- weights: distinct blocks, Q4_K with a Q6_K down projection ----
     t0 = time.time()
@@ -145,6 +157,12 @@ def main():
         nprof += 1
     for blk in blocks:
         blk.profile(False)
+    if nprof == 0:
+        for blk in blocks:
+            blk.free()
+        kv.free()
+        log("bench: no profiled steps, stage report skipped")
+        return
     stages = {k: v / nprof for k, v in stage_sum.items()}
     log("bench: stages " + ", ".join(f"{k} {v:.3f}" for k, v in stages.items()) + " ms")
 
@@ -167,9 +185,12 @@ def main():
 
     dom_name = max(kernels, key=lambda n: kernels[n]["ms"])
     dom = kernels[dom_name]
+    traffic = measured_traffic(dom_name)
     roofline = {"kernel": dom_name, "bound": "mfma", "achieved": round(dom["tflops"], 2),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(dom["tflops"] / PEAK_BF16_TFLOPS, 4),
-                "traffic": None, "flop_per_launch": dom["gflop"] * 1e9}
+                "traffic": traffic["bytes"] if traffic else None, "flop_per_launch": dom["gflop"] * 1e9}
+    if traffic:
+        roofline["traffic_source"] = traffic["source"]
 
     block_flop = att_flop + 2.0 * S_IMG * HID * (3 * HID + HID + 2 * MLP) + 2.0 * S_IMG * MLP * HID
 
@@ -209,6 +230,22 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_block_q4km_1024.json")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE and WRITE_SIZE passes, each scaled by what the counter
+    reads for a plain copy of known size), or None when it holds no figure."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            data = json.load(f)
+        k = data["kernels"][kernel]
+        return {"bytes": int(k["traffic_bytes"]), "source": os.path.relpath(TRAFFIC_FILE, ROOT)}
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def cpu_baseline(rows, host_w):

@@ -157,7 +157,8 @@ int qimm_v_transpose(qimm_ctx *ctx, const float *x, int64_t batch, int64_t seq,
  * out [B,Sq,H*128] bf16. Replaces chunked_attention / flash_attention
  * (src/transformer.rs:246-296) on the cached step, where the mask is None
  * (src/quantized_transformer.rs:526-532) and the keys are
- * cat([from_cache_entry(prefix), own]) (143-146). scale = 1/sqrt(128) there. */
+ * cat([from_cache_entry(prefix), own]) (143-146). scale = 1/sqrt(128) there.
+ * q, k_own, vt_own and out must be 16-byte aligned. */
 int qimm_attention(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64_t heads,
                    int64_t sq, const qimm_kv *kv, int64_t layer, const uint16_t *k_own,
                    const uint16_t *vt_own, int64_t so, float scale, uint16_t *out,

@@ -217,6 +217,10 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     ep.seq = seq;
     ep.heads = H;
     ep.hidden = hid;
+    // q leaves the epilogue multiplied by the softmax scale and log2(e): the
+    // attention then works on scores in log2 units (transformer.rs:275 scales
+    // q by D^-1/2 before the product as well)
+    ep.q_scale = (1.0f / sqrtf(128.0f)) * 1.4426950408889634f;
     if (blk->qkv_fused) {
         ep.n_offset = 0;
         QIMM_HIP(ctx, qimm::launch_qgemm(blk->qkv->gw, xn, M, hid, qimm::EPI_QKV, ep, s));
@@ -229,9 +233,9 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     }
     STAGE_MARK(2);
     // attention over [prefix ; own]                            (:143-148)
-    QIMM_HIP(ctx, qimm::launch_attention(qb, kv ? kv->k + layer * kv->layer_elems() : nullptr,
-                                         kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, kb, vt, seq,
-                                         batch, H, seq, 1.0f / sqrtf(128.0f), att, s));
+    QIMM_HIP(ctx, qimm::launch_attention_log2(qb, kv ? kv->k + layer * kv->layer_elems() : nullptr,
+                                              kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, kb, vt, seq,
+                                              batch, H, seq, att, s));
     STAGE_MARK(3);
     // x1 = x + tanh(gate1) * to_out(attn)                       (:150-151, 271-273)
     qimm::EpiParams er{};
@@ -309,8 +313,8 @@ int qimm_attention(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64_t head
                    uint16_t *out, void *stream) {
     if (!ctx || !q || !out || (so > 0 && (!k_own || !vt_own))) return QIMM_ERR_ARG;
     if (batch <= 0 || heads <= 0 || sq < 0 || so < 0) return set_err(ctx, QIMM_ERR_SHAPE, "attention: bad sizes");
-    if (!aligned16(q) || !aligned16(out) || (k_own && !aligned16(k_own)))
-        return set_err(ctx, QIMM_ERR_ARG, "attention: q, k and out must be 16-byte aligned");
+    if (!aligned16(q) || !aligned16(out) || (k_own && !aligned16(k_own)) || (vt_own && !aligned16(vt_own)))
+        return set_err(ctx, QIMM_ERR_ARG, "attention: q, k, vt and out must be 16-byte aligned");
     int64_t P = 0;
     if (kv) {
         if (kv->batch != batch || kv->heads != heads)

@@ -6,19 +6,321 @@
 // (src/quantized_transformer.rs:143-148). The two key segments are read in
 // place (no concatenation copy, src/quantized_transformer.rs:143-146).
 //
-// Work split: one workgroup = 128 queries of one (batch, head), 4 waves x 32
-// queries. Each wave computes S^T = K_blk Q^T (64 keys x 32 queries) with
-// v_mfma_f32_32x32x16_bf16, so every lane owns one query column: the row max
-// and row sum need only the lane and its partner lane^32. The probabilities
-// stay in registers and are the B operand of O^T += V^T P^T; the 16-key
-// K-slots of that MFMA use the permuted key order the S^T accumulator layout
-// produces, and V^T is read from LDS in the same order. K and V^T tiles of 64
-// keys are double-buffered in LDS.
+// Common formulation: each wave computes S^T = K_blk Q^T for 32 queries with
+// v_mfma_f32_32x32x16_bf16, so every lane owns one query column and the row
+// max / row sum need only the lane and its partner lane^32. The probabilities
+// stay in registers and are the B operand of O^T += V^T P^T.
+//
+// Two kernels:
+//  - attn_fast_kernel (both segment lengths multiples of 8): 8 waves x 32
+//    queries per workgroup; 64-key K and V^T tiles copied HBM -> LDS with
+//    global_load_lds (no staging registers) into XOR-swizzled, conflict-free
+//    layouts, double-buffered; the K rows of a 32-key half are read in a
+//    bit-swapped order so that each lane's P^T registers hold 8 consecutive
+//    keys and every V^T fragment is one 16 B LDS read; the running maximum is
+//    folded into the S accumulator start (C = -m) and only moves when it grew
+//    by more than 2^8, so the common path is p = exp2(s) (q pre-scaled by
+//    scale*log2 e) and the rescale of O is a rare wave-uniform branch; row
+//    sums use v_dot2_f32_bf16 over the packed bf16 probabilities, the same
+//    values the PV product uses.
+//  - attn_any_kernel (any lengths): 4 waves x 32 queries, K/V^T staged through
+//    registers with per-element bounds, the reference shape for ragged tails.
 #include "device_common.h"
 #include "kernels.h"
 
 namespace qimm {
 namespace {
+
+struct Seg {
+    const uint16_t *k;   // [BH][len][128]
+    const uint16_t *vt;  // [BH][128][len]
+    int64_t len;
+};
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+// v_permlane32_swap exchanges the upper 32 lanes of its first operand with
+// the lower 32 lanes of its second; with both operands holding x, each lane
+// ends up with x and x of lane ^ 32 in the pair. Inline asm because the
+// compiler folds a max or sum over the builtin's two results when both
+// inputs are the same value.
+__device__ __forceinline__ void swap32(float &a, float &b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float xmax32(float x) {
+    float a = x, b = x;
+    swap32(a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float xsum32(float x) {
+    float a = x, b = x;
+    swap32(a, b);
+    return a + b;
+}
+// acc + lo + hi of a packed bf16 pair
+__device__ __forceinline__ float dot2_ones(uint32_t pair, float acc) {
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), one, acc, false);
+}
+
+namespace fast {
+
+constexpr int NW = 8;            // waves per workgroup
+constexpr int QB = 32 * NW;      // queries per workgroup
+constexpr int DI = 16 / NW;      // DMA instructions per wave per 16 KB tile
+constexpr int KB = 64;           // keys per block
+constexpr int HD = 128;
+constexpr int TILE = KB * HD * 2;     // 16 KB: K (64 rows x 256 B) or V^T (128 rows x 128 B)
+constexpr int STAGE = 2 * TILE;       // K tile then V^T tile
+constexpr int OP = 136;               // bf16 pitch of the output staging rows
+constexpr int LDS_BYTES = 2 * STAGE > NW * 32 * OP * 2 ? 2 * STAGE : NW * 32 * OP * 2;
+constexpr float RESCALE_TH = 8.0f;    // log2 units
+
+// K tile: key row r holds 16 B chunk c at slot c ^ (r % 16); V^T tile: d row
+// holds 8-key chunk c at slot c ^ ((d / 2) % 8). A 16-lane phase of b128 reads
+// (16 rows, one chunk) then covers all 64 banks once.
+template <bool PRE>
+__global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *__restrict__ q, Seg s0, Seg s1,
+                                                               int64_t H, int64_t Sq, int64_t nq, int64_t B,
+                                                               float sl2, uint16_t *__restrict__ out) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
+
+    // XCD-aware order: workgroups are dealt round-robin over 8 XCDs; each XCD
+    // gets a contiguous range of (batch, head, query tile) so the query tiles
+    // of one head share that XCD's L2 copy of its K/V.
+    const int64_t total = nq * H * B;
+    int64_t L = blockIdx.x;
+    if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
+    const int64_t qt = L % nq, hh = (L / nq) % H, bb = L / (nq * H);
+    const int64_t bh = bb * H + hh;
+    const int64_t q0 = qt * QB + wave * 32;
+
+    // Q^T fragments (B operand): lane holds query q0+l32, d = 16kk + 8g .. +8
+    bf16x8 qf[8];
+    {
+        const int64_t qi = q0 + l32;
+        const uint16_t *qr = q + (bh * Sq + (qi < Sq ? qi : 0)) * HD;
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+            u32x4 v = *(const u32x4 *)(qr + kk * 16 + g * 8);
+            if (qi >= Sq) v = u32x4{0u, 0u, 0u, 0u};
+            qf[kk] = __builtin_bit_cast(bf16x8, v);
+        }
+    }
+
+    const int len0 = (int)s0.len, len1 = (int)s1.len;
+    const int nb0 = (len0 + KB - 1) / KB, nb1 = (len1 + KB - 1) / KB;
+    const int nblk = nb0 + nb1;
+    const char *kb0 = (const char *)(s0.k + bh * (int64_t)len0 * HD);
+    const char *kb1 = (const char *)(s1.k + bh * (int64_t)len1 * HD);
+    const char *vb0 = (const char *)(s0.vt + bh * (int64_t)HD * len0);
+    const char *vb1 = (const char *)(s1.vt + bh * (int64_t)HD * len1);
+
+    // DMA roles: instruction t = wave + NW i fills K rows 4t .. 4t+3 (lane at
+    // row 4t + lane/16, slot lane%16) and V^T rows 8t .. 8t+7 (lane at row
+    // 8t + lane/8, slot lane%8); lane l lands at LDS base + 16 l.
+    uint32_t koff[DI], vrow[DI], vcol[DI];
+#pragma unroll
+    for (int i = 0; i < DI; i++) {
+        const int r = 4 * (wave + NW * i) + (lane >> 4);
+        koff[i] = (uint32_t)(r * 256 + (((lane & 15) ^ (r & 15)) << 4));
+        const int d = 8 * (wave + NW * i) + (lane >> 3);
+        vrow[i] = (uint32_t)d;
+        vcol[i] = (uint32_t)(((lane & 7) ^ ((d >> 1) & 7)) << 4);
+    }
+    // Block j covers keys [start, start + 64) of its segment. The last block of
+    // a segment of at least 64 keys slides back to end at len (window [kv0,
+    // kv0 + 64), keys before `lo` already seen); a shorter segment clamps its
+    // rows and masks keys from `hi` on. Every load stays inside the segment.
+    struct Blk {
+        const char *kb, *vb;
+        int len, kv0, lo, hi;
+    };
+    auto blk_of = [&](int j) {
+        Blk b;
+        const bool first = j < nb0;
+        b.len = first ? len0 : len1;
+        b.kb = first ? kb0 : kb1;
+        b.vb = first ? vb0 : vb1;
+        const int start = (first ? j : j - nb0) * KB;
+        if (b.len >= KB) {
+            b.kv0 = min(start, b.len - KB);
+            b.lo = start - b.kv0;
+            b.hi = KB;
+        } else {
+            b.kv0 = 0;
+            b.lo = 0;
+            b.hi = b.len;
+        }
+        return b;
+    };
+    auto dma = [&](const Blk &b, int stage) {
+        uint8_t *base = lds + stage * STAGE;
+        if (b.len >= KB) {
+            const char *kg = b.kb + (int64_t)b.kv0 * 256;
+            const char *vg = b.vb + (int64_t)b.kv0 * 2;
+#pragma unroll
+            for (int i = 0; i < DI; i++)
+                __builtin_amdgcn_global_load_lds((const void *)(kg + koff[i]),
+                                                 (lds_ptr_t)(base + (wave + NW * i) * 1024), 16, 0, 0);
+#pragma unroll
+            for (int i = 0; i < DI; i++)
+                __builtin_amdgcn_global_load_lds((const void *)(vg + (vrow[i] * (uint32_t)(2 * b.len) + vcol[i])),
+                                                 (lds_ptr_t)(base + TILE + (wave + NW * i) * 1024), 16, 0, 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < DI; i++) {
+                const int r = 4 * (wave + NW * i) + (lane >> 4);
+                const int gr = min(r, b.len - 1);
+                __builtin_amdgcn_global_load_lds((const void *)(b.kb + (koff[i] - r * 256) + gr * 256),
+                                                 (lds_ptr_t)(base + (wave + NW * i) * 1024), 16, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < DI; i++) {
+                const int gc = min((int)vcol[i] >> 1, b.len - 8);
+                __builtin_amdgcn_global_load_lds((const void *)(b.vb + vrow[i] * (uint32_t)(2 * b.len) + 2 * gc),
+                                                 (lds_ptr_t)(base + TILE + (wave + NW * i) * 1024), 16, 0, 0);
+            }
+        }
+    };
+
+    // S^T row m of a 32-key half is key pi(m) = m with bits 2 and 3 swapped,
+    // so accumulator register r of lane (l32, g) is key 16 (r / 8) + 8 g + r % 8
+    // and P^T register pairs map to consecutive keys. LDS read offsets are per
+    // lane; stage, half and d-tile parts are immediates.
+    const int krow = (l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
+    uint32_t kaddr[8], vaddr[2][2];
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++) kaddr[kk] = (uint32_t)(krow * 256 + (((2 * kk + g) ^ (krow & 15)) << 4));
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++)
+            vaddr[h][kk] = (uint32_t)(TILE + l32 * 128 + (((4 * h + 2 * kk + g) ^ ((l32 >> 1) & 7)) << 4));
+
+    f32x16 o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[dt][r] = 0.f;
+    // scores are kept relative to m_run (score units): the S accumulation
+    // starts at -m_run
+    float m_run = 0.f, l_run = 0.f;
+    f32x16 negm;
+#pragma unroll
+    for (int r = 0; r < 16; r++) negm[r] = 0.f;
+    bool first_half = true;
+
+    auto half_step = [&](const uint8_t *stg, int h, int lo, int hi) {
+        f32x16 st = negm;
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+            const bf16x8 a = *(const bf16x8 *)(stg + h * 32 * 256 + kaddr[kk]);
+            st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], st, 0, 0, 0);
+        }
+        if (lo > h * 32 || hi < h * 32 + 32) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int kv = h * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
+                if (kv < lo || kv >= hi) st[r] = -INFINITY;
+            }
+        }
+        float m0 = st[0], m1 = st[1];
+#pragma unroll
+        for (int r = 2; r < 16; r += 2) {
+            m0 = fmaxf(m0, st[r]);
+            m1 = fmaxf(m1, st[r + 1]);
+        }
+        float mx = xmax32(fmaxf(m0, m1));
+        if (!PRE) mx *= sl2;  // log2 units
+        if (first_half || __builtin_amdgcn_ballot_w64(mx > RESCALE_TH)) {
+            // move the reference point up by d (log2 units); the first half of
+            // a row has at least one unmasked key, so d is finite there
+            const float d = first_half ? mx : fmaxf(mx, 0.f);
+            const float alpha = first_half ? 0.f : __builtin_amdgcn_exp2f(-d);
+            first_half = false;
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[dt][r] *= alpha;
+            const float draw = PRE ? d : d / sl2;
+            m_run += draw;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                st[r] -= draw;
+                negm[r] = -m_run;
+            }
+        }
+        uint32_t pk[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float a = PRE ? st[2 * i] : st[2 * i] * sl2;
+            const float b = PRE ? st[2 * i + 1] : st[2 * i + 1] * sl2;
+            pk[i] = pack_bf16x2(__builtin_amdgcn_exp2f(a), __builtin_amdgcn_exp2f(b));
+            l_run = dot2_ones(pk[i], l_run);
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+            const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[4 * kk], pk[4 * kk + 1], pk[4 * kk + 2], pk[4 * kk + 3]});
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                const bf16x8 a = *(const bf16x8 *)(stg + dt * 32 * 128 + vaddr[h][kk]);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf, o[dt], 0, 0, 0);
+            }
+        }
+    };
+
+    // block j computes from stage cur while block j+1 streams into the other
+    auto step = [&](int j, int cur) {
+        if (j + 1 < nblk) dma(blk_of(j + 1), cur ^ 1);
+        const Blk b = blk_of(j);
+        const uint8_t *stg = lds + cur * STAGE;
+        half_step(stg, 0, b.lo, b.hi);
+        half_step(stg, 1, b.lo, b.hi);
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): block j+1 landed
+        __syncthreads();
+    };
+
+    if (nblk > 0) dma(blk_of(0), 0);
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();
+    int j = 0;
+    for (; j + 1 < nblk; j += 2) {
+        step(j, 0);
+        step(j + 1, 1);
+    }
+    if (j < nblk) step(j, 0);
+
+    // normalize and stage O [32 q x 128 d] per wave through LDS for row stores
+    const float l_tot = xsum32(l_run);
+    const float inv = 1.0f / l_tot;
+    uint16_t *os = (uint16_t *)lds + wave * 32 * OP;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+            const int d = dt * 32 + 8 * rq + 4 * g;
+            u32x2 w{pack_bf16x2(o[dt][4 * rq] * inv, o[dt][4 * rq + 1] * inv),
+                    pack_bf16x2(o[dt][4 * rq + 2] * inv, o[dt][4 * rq + 3] * inv)};
+            *(u32x2 *)(os + l32 * OP + d) = w;
+        }
+    __syncthreads();
+    const int64_t HDt = H * HD;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int r = i * 4 + (lane >> 4);
+        const int c = (lane & 15) * 8;
+        const int64_t qi = q0 + r;
+        if (qi < Sq)
+            *(u32x4 *)(out + (bb * Sq + qi) * HDt + hh * HD + c) = *(const u32x4 *)(os + r * OP + c);
+    }
+}
+
+}  // namespace fast
+
+namespace anylen {
 
 constexpr int QB = 128;     // queries per workgroup
 constexpr int KB = 64;      // keys per block
@@ -30,13 +332,10 @@ constexpr int VSTAGE = HD * VP;
 constexpr int STAGE = KSTAGE + VSTAGE;
 constexpr int OP = 136;     // bf16 pitch of the output staging rows
 
-struct Seg {
-    const uint16_t *k;   // [BH][len][128]
-    const uint16_t *vt;  // [BH][128][len]
-    int64_t len;
-};
-
-__global__ __launch_bounds__(256, 2) void attn_kernel(const uint16_t *__restrict__ q, Seg s0, Seg s1,
+// K and V^T tiles of 64 keys double-buffered in LDS through registers; the
+// 16-key K-slots of the PV MFMA use the key order of the S^T accumulator
+// layout, and V^T is read from LDS in the same order.
+__global__ __launch_bounds__(256, 2) void attn_any_kernel(const uint16_t *__restrict__ q, Seg s0, Seg s1,
                                                       int64_t H, int64_t Sq, int64_t nq, int64_t B,
                                                       float sl2, uint16_t *__restrict__ out) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
@@ -227,21 +526,45 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(const uint16_t *__restrict
     }
 }
 
-}  // namespace
+}  // namespace anylen
 
-hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
-                            const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
-                            int64_t sq, float scale, uint16_t *out, hipStream_t stream) {
+// sl2 = softmax scale * log2(e) applied to raw scores, or 1 when q already
+// carries it (PRE)
+template <bool PRE>
+hipError_t launch(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p, const uint16_t *ko,
+                  const uint16_t *vto, int64_t so, int64_t b, int64_t h, int64_t sq, float sl2, uint16_t *out,
+                  hipStream_t stream) {
     if (sq <= 0 || b <= 0 || h <= 0) return hipSuccess;
+    if (p < 0 || so < 0 || p + so <= 0) return hipErrorInvalidValue;
     Seg s0{kp, vtp, p}, s1{ko, vto, so};
     if (p <= 0) {
         s0 = s1;
         s1 = Seg{ko, vto, 0};
     }
-    const int64_t nq = (sq + QB - 1) / QB;
-    const float sl2 = scale * 1.4426950408889634f;
-    attn_kernel<<<dim3((unsigned)(nq * h * b)), dim3(256), 0, stream>>>(q, s0, s1, h, sq, nq, b, sl2, out);
+    if ((p & 7) == 0 && (so & 7) == 0) {
+        const int64_t nq = (sq + fast::QB - 1) / fast::QB;
+        fast::attn_fast_kernel<PRE><<<dim3((unsigned)(nq * h * b)), dim3(64 * fast::NW), 0, stream>>>(
+            q, s0, s1, h, sq, nq, b, sl2, out);
+    } else {
+        const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;
+        anylen::attn_any_kernel<<<dim3((unsigned)(nq * h * b)), dim3(256), 0, stream>>>(q, s0, s1, h, sq, nq, b,
+                                                                                       sl2, out);
+    }
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
+                            const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
+                            int64_t sq, float scale, uint16_t *out, hipStream_t stream) {
+    return launch<false>(q, kp, vtp, p, ko, vto, so, b, h, sq, scale * 1.4426950408889634f, out, stream);
+}
+
+hipError_t launch_attention_log2(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
+                                 const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
+                                 int64_t sq, uint16_t *out, hipStream_t stream) {
+    return launch<true>(q, kp, vtp, p, ko, vto, so, b, h, sq, 1.0f, out, stream);
 }
 
 }  // namespace qimm

@@ -40,6 +40,7 @@ struct EpiParams {
     int64_t heads;
     int64_t hidden;
     int64_t n_offset;
+    float q_scale = 1.0f;  // multiplies q after RoPE, before the bf16 rounding
     // EPI_SWIGLU: tile columns [0,64) gate, [64,128) up -> hmid[m*ldh + n/2 + j]
     uint16_t *hmid;
     int64_t ldh;
@@ -80,6 +81,11 @@ hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_
                             int64_t p, const uint16_t *ko, const uint16_t *vto, int64_t so,
                             int64_t b, int64_t h, int64_t sq, float scale, uint16_t *out,
                             hipStream_t stream);
+// The same with q already multiplied by scale * log2(e) (the QKV epilogue's
+// q_scale), so scores are in log2 units.
+hipError_t launch_attention_log2(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp,
+                                 int64_t p, const uint16_t *ko, const uint16_t *vto, int64_t so,
+                                 int64_t b, int64_t h, int64_t sq, uint16_t *out, hipStream_t stream);
 
 // Per-head RmsNorm + RoPE of raw projections x [B,S,H,128] (f32) into the
 // attention layouts; mode 0: q/k -> [B,H,S,128]; mode 1: v -> vt [B,H,128,S].

@@ -296,6 +296,7 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(const uint16_t *__restric
         if (sec < 2) {
             const float *nw = sec == 0 ? ep.norm_q : ep.norm_k;
             uint16_t *dst = sec == 0 ? ep.q : ep.k;
+            const float osc = sec == 0 ? ep.q_scale : 1.0f;
             const int cg = (tid & 15) * 8;
             float wv[8];
 #pragma unroll
@@ -321,7 +322,7 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(const uint16_t *__restric
                     const float x0 = v[2 * i] * rs * wv[2 * i];
                     const float x1 = v[2 * i + 1] * rs * wv[2 * i + 1];
                     const float c = pr[2 * i], sn = pr[2 * i + 1];
-                    pk[i] = pack_bf16x2(x0 * c - x1 * sn, x0 * sn + x1 * c);
+                    pk[i] = pack_bf16x2((x0 * c - x1 * sn) * osc, (x0 * sn + x1 * c) * osc);
                 }
                 *(u32x4 *)(dst + ((b * H + head) * S + s) * 128 + cg) = u32x4{pk[0], pk[1], pk[2], pk[3]};
             }

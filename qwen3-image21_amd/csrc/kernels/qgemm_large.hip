@@ -372,6 +372,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
         const int64_t mw = m0 + wm * 128;  // first row of this wave
         if (sec < 2) {
             const float *nwt = sec == 0 ? ep.norm_q : ep.norm_k;
+            const float osc = sec == 0 ? ep.q_scale : 1.0f;
             float wq[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) wq[j] = nwt[j * 32 + l32];
@@ -395,7 +396,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
                         const float xp = __shfl_xor(x, 1);  // RoPE partner column c ^ 1
                         const float cs_ = pr[c & ~1], sn = pr[c | 1];
                         // even column: x0 c - x1 s; odd column: x0 s + x1 c (x0 is the partner)
-                        const float y = odd ? xp * sn + x * cs_ : x * cs_ - xp * sn;
+                        const float y = (odd ? xp * sn + x * cs_ : x * cs_ - xp * sn) * osc;
                         tile[t * 128 + (c ^ ((t & 7) << 3))] = (uint16_t)(pack_bf16x2(y, 0.f) & 0xffffu);
                     }
                 }

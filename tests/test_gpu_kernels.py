@@ -128,9 +128,9 @@ def test_qmatmul_rejects_bad_shapes(torch_cuda, qctx):
 
 # ---------------------------------------------------------------- attention
 
-def _attention_case(torch, qctx, b, h, sq, p, so, seed):
+def _attention_case(torch, qctx, b, h, sq, p, so, seed, qmul=1.0):
     rng = np.random.default_rng(seed)
-    q_dev, q = bf16_dev(torch, rng.standard_normal((b, h, sq, 128)).astype(np.float32))
+    q_dev, q = bf16_dev(torch, (qmul * rng.standard_normal((b, h, sq, 128))).astype(np.float32))
     ko_dev, ko = bf16_dev(torch, rng.standard_normal((b, h, so, 128)).astype(np.float32))
     vo = O.bf16_round(rng.standard_normal((b, h, so, 128)).astype(np.float32))
     vt_dev, _ = bf16_dev(torch, np.ascontiguousarray(vo.transpose(0, 1, 3, 2)))
@@ -155,15 +155,20 @@ def _attention_case(torch, qctx, b, h, sq, p, so, seed):
     return got, q, ko, vo, kp, vp
 
 
-@pytest.mark.parametrize("b,h,sq,p,so", [
-    (1, 2, 128, 64, 128),     # aligned
-    (1, 2, 200, 70, 200),     # ragged query tile, unaligned prefix (scalar V^T path)
-    (2, 3, 64, 256, 96),      # batch 2, prefix longer than own
-    (1, 1, 33, 0, 45),        # no prefix, odd lengths
-    (1, 2, 16, 8, 8),         # tiny
+@pytest.mark.parametrize("b,h,sq,p,so,qmul", [
+    (1, 2, 128, 64, 128, 1.0),    # aligned
+    (1, 2, 200, 70, 200, 1.0),    # ragged query tile, unaligned prefix (per-element V^T path)
+    (2, 3, 64, 256, 96, 1.0),     # batch 2, prefix longer than own; own tail window slides back
+    (1, 1, 33, 0, 45, 1.0),       # no prefix, odd lengths
+    (1, 2, 16, 8, 8, 1.0),        # tiny: both segments shorter than one 64-key block
+    (1, 2, 300, 40, 520, 1.0),    # short prefix (clamped rows), own tail of 8 keys
+    (2, 4, 256, 0, 136, 1.0),     # no prefix, own tail window slides back
+    (1, 1, 513, 24, 64, 1.0),     # one query past a 256-query tile
+    (1, 2, 256, 64, 448, 4.0),    # large score range: the running maximum moves mid-row
 ])
-def test_attention_matches_oracle(torch_cuda, qctx, b, h, sq, p, so):
-    got, q, ko, vo, kp, vp = _attention_case(torch_cuda, qctx, b, h, sq, p, so, seed=b + h + sq + p + so)
+def test_attention_matches_oracle(torch_cuda, qctx, b, h, sq, p, so, qmul):
+    got, q, ko, vo, kp, vp = _attention_case(torch_cuda, qctx, b, h, sq, p, so, seed=b + h + sq + p + so,
+                                             qmul=qmul)
     want = O.attention(q, ko, vo, kp, vp, mode=O.EXACT)
     assert cos_sim(got, want) >= 0.9999, cos_sim(got, want)
     assert max_abs_rel(got, want) <= 2e-2, max_abs_rel(got, want)

@@ -3,6 +3,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
 #include <new>
 #include <vector>
 
@@ -196,6 +197,20 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     uint16_t *xn = (uint16_t *)(ws + o_xn), *qb = (uint16_t *)(ws + o_q);
     uint16_t *kb = k_out ? k_out : (uint16_t *)(ws + o_k);
     uint16_t *vt = (uint16_t *)(ws + o_vt), *att = (uint16_t *)(ws + o_att), *hm = (uint16_t *)(ws + o_h);
+    // split-K scratch of the short-M GEMM path, sized for the largest projection
+    size_t part_need = 0;
+    {
+        const qimm_weight *ws_list[] = {blk->qkv, blk->q, blk->k, blk->v, blk->out, blk->gate_up, blk->down};
+        for (const qimm_weight *wt : ws_list)
+            if (wt && qimm::qgemm_stream_fits(wt->gw, M))
+                part_need = std::max(part_need, qimm::qgemm_stream_workspace(wt->gw, M));
+    }
+    if (part_need) {
+        rc = ensure_part_workspace(ctx, part_need);
+        if (rc) return rc;
+    }
+    float *part_ws = part_need ? (float *)ctx->ws_part : nullptr;
+    const size_t part_bytes = part_need ? ctx->ws_part_bytes : 0;
 
 #define STAGE_MARK(i) \
     if (blk->profiling) QIMM_HIP(ctx, hipEventRecord(blk->ev[i], s))
@@ -207,6 +222,8 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     STAGE_MARK(1);
     // to_q/to_k/to_v + per-head RmsNorm + RoPE                 (:133-142)
     qimm::EpiParams ep{};
+    ep.part_ws = part_ws;
+    ep.part_ws_bytes = part_bytes;
     ep.q = qb;
     ep.k = kb;
     ep.vt = vt;
@@ -239,6 +256,8 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     STAGE_MARK(3);
     // x1 = x + tanh(gate1) * to_out(attn)                       (:150-151, 271-273)
     qimm::EpiParams er{};
+    er.part_ws = part_ws;
+    er.part_ws_bytes = part_bytes;
     er.x_in = x;
     er.x_out = x_out;
     er.gvec = modp + hid;
@@ -251,12 +270,16 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     STAGE_MARK(5);
     // silu(gate) * up                                          (:191-201)
     qimm::EpiParams eg{};
+    eg.part_ws = part_ws;
+    eg.part_ws_bytes = part_bytes;
     eg.hmid = hm;
     eg.ldh = F;
     QIMM_HIP(ctx, qimm::launch_qgemm(blk->gate_up->gw, xn, M, hid, qimm::EPI_SWIGLU, eg, s));
     STAGE_MARK(6);
     // x2 = x1 + tanh(gate2) * out(hidden)                       (:202, 280-282)
     qimm::EpiParams ed{};
+    ed.part_ws = part_ws;
+    ed.part_ws_bytes = part_bytes;
     ed.x_in = x_out;
     ed.x_out = x_out;
     ed.gvec = modp + 3 * hid;

@@ -33,6 +33,20 @@ int ensure_workspace(qimm_ctx *ctx, size_t bytes) {
     return QIMM_OK;
 }
 
+int ensure_part_workspace(qimm_ctx *ctx, size_t bytes) {
+    if (bytes <= ctx->ws_part_bytes) return QIMM_OK;
+    if (ctx->ws_part) {
+        QIMM_HIP(ctx, hipDeviceSynchronize());
+        QIMM_HIP(ctx, hipFree(ctx->ws_part));
+        ctx->ws_part = nullptr;
+        ctx->ws_part_bytes = 0;
+    }
+    bytes = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+    QIMM_HIP(ctx, hipMalloc(&ctx->ws_part, bytes));
+    ctx->ws_part_bytes = bytes;
+    return QIMM_OK;
+}
+
 }  // namespace qimm_host
 
 using namespace qimm_host;
@@ -69,10 +83,11 @@ int qimm_ctx_create(int device, qimm_ctx **out) {
 
 int qimm_ctx_destroy(qimm_ctx *ctx) {
     if (!ctx) return QIMM_ERR_ARG;
-    if (ctx->ws) {
+    if (ctx->ws || ctx->ws_part) {
         (void)hipSetDevice(ctx->device);
         (void)hipDeviceSynchronize();
-        (void)hipFree(ctx->ws);
+        if (ctx->ws) (void)hipFree(ctx->ws);
+        if (ctx->ws_part) (void)hipFree(ctx->ws_part);
     }
     delete ctx;
     return QIMM_OK;

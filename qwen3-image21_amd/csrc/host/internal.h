@@ -16,6 +16,9 @@ struct qimm_ctx {
     // context (calls on one context are serialized by the caller).
     void *ws = nullptr;
     size_t ws_bytes = 0;
+    // Growable f32 scratch for the split-K partial sums of the short-M GEMM.
+    void *ws_part = nullptr;
+    size_t ws_part_bytes = 0;
 };
 
 struct qimm_weight {
@@ -57,6 +60,7 @@ namespace qimm_host {
 int set_err(qimm_ctx *ctx, int status, const std::string &msg);
 int hip_err(qimm_ctx *ctx, hipError_t e, const char *what);
 int ensure_workspace(qimm_ctx *ctx, size_t bytes);
+int ensure_part_workspace(qimm_ctx *ctx, size_t bytes);
 int upload_weight_rows(qimm_ctx *ctx, int type, int64_t rows, int64_t cols, const uint8_t *bytes,
                        qimm_weight **out);
 int64_t row_bytes(int type, int64_t cols);

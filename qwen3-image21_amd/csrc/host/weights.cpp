@@ -189,6 +189,14 @@ int qimm_qmatmul(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_
     qimm::EpiParams ep{};
     ep.out = y;
     ep.ldo = w->rows;
+    if (qimm::qgemm_stream_fits(w->gw, m)) {
+        const size_t need = qimm::qgemm_stream_workspace(w->gw, m);
+        QIMM_HIP(ctx, hipSetDevice(ctx->device));
+        const int rc = qimm_host::ensure_part_workspace(ctx, need);
+        if (rc) return rc;
+        ep.part_ws = (float *)ctx->ws_part;
+        ep.part_ws_bytes = ctx->ws_part_bytes;
+    }
     QIMM_HIP(ctx, qimm::launch_qgemm(w->gw, (const uint16_t *)x_bf16, m, lda,
                                      out_type == QIMM_TYPE_F32 ? qimm::EPI_F32 : qimm::EPI_BF16, ep,
                                      (hipStream_t)stream));

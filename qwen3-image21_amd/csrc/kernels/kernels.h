@@ -44,6 +44,10 @@ struct EpiParams {
     // EPI_SWIGLU: tile columns [0,64) gate, [64,128) up -> hmid[m*ldh + n/2 + j]
     uint16_t *hmid;
     int64_t ldh;
+    // f32 scratch of part_ws_bytes for the short-M split-K path (optional;
+    // without it short M takes the 128x128 kernel)
+    float *part_ws = nullptr;
+    size_t part_ws_bytes = 0;
 };
 
 struct GemmWeight {
@@ -59,6 +63,15 @@ struct GemmWeight {
 hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda,
                         int epi, const EpiParams &ep, hipStream_t stream);
 bool qgemm_large_fits(const GemmWeight &w, int64_t m);
+
+// Short-M weight-streaming path (M <= 64): split-K partial sums into part
+// (qgemm_stream_workspace bytes), then a fixed-order reduction that applies
+// the epilogue.
+bool qgemm_stream_fits(const GemmWeight &w, int64_t m);
+size_t qgemm_stream_workspace(const GemmWeight &w, int64_t m);
+int qgemm_stream_splits(const GemmWeight &w, int64_t m);
+hipError_t launch_qgemm_stream(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
+                               const EpiParams &ep, float *part, hipStream_t stream);
 hipError_t launch_qgemm_large(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda,
                               int epi, const EpiParams &ep, hipStream_t stream);
 

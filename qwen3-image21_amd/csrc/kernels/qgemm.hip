@@ -392,6 +392,8 @@ hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64
                         const EpiParams &ep, hipStream_t stream) {
     if (m <= 0) return hipSuccess;
     if (qgemm_large_fits(w, m)) return launch_qgemm_large(w, a, m, lda, epi, ep, stream);
+    if (qgemm_stream_fits(w, m) && ep.part_ws && ep.part_ws_bytes >= qgemm_stream_workspace(w, m))
+        return launch_qgemm_stream(w, a, m, lda, epi, ep, ep.part_ws, stream);
     switch (w.fmt) {
     case WF_Q8_0: return launch_fmt<WF_Q8_0>(w, a, m, lda, epi, ep, stream);
     case WF_Q4_K: return launch_fmt<WF_Q4_K>(w, a, m, lda, epi, ep, stream);

@@ -70,7 +70,11 @@ def _gemm_case(torch, qctx, t, m, n, k, seed, out_type=synth.F32, std=0.02):
 
 
 @pytest.mark.parametrize("t", [synth.Q8_0, synth.Q4_K, synth.Q6_K, synth.BF16])
-@pytest.mark.parametrize("m,n,k", [(1, 128, 256), (17, 256, 512), (130, 384, 1024), (300, 128, 4096),
+@pytest.mark.parametrize("m,n,k", [(1, 128, 256), (17, 256, 512),
+                                   # M <= 64 with K % 256 == 0: split-K weight streaming (a short
+                                   # chunk, a partial 16-token tile, chunks longer than six stages)
+                                   (16, 384, 4096), (33, 256, 1024), (64, 128, 8192),
+                                   (130, 384, 1024), (300, 128, 4096),
                                    (600, 512, 1024), (1024, 256, 768)])   # the last two: 256x256 kernel
 def test_qmatmul_matches_bf16_weight_products(torch_cuda, qctx, t, m, n, k):
     got, a, w = _gemm_case(torch_cuda, qctx, t, m, n, k, seed=m * 7 + n + k + t)

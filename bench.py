@@ -194,6 +194,9 @@ def main():
 
     block_flop = att_flop + 2.0 * S_IMG * HID * (3 * HID + HID + 2 * MLP) + 2.0 * S_IMG * MLP * HID
 
+    # ---- weight streaming at short token counts (the HBM-bound regime) ----
+    streaming = weight_streaming(ctx, torch, np, qimm, synth, stream, host_w0)
+
     # ---- CPU baseline: the oracle in candle mode on a bounded sample ----
     cpu = None
     if not args.no_cpu_baseline:
@@ -227,9 +230,44 @@ def main():
         "stages_ms": {k: round(v, 4) for k, v in stages.items()},
         "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},
         "roofline": roofline,
+        "weight_streaming": streaming,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+
+
+def weight_streaming(ctx, torch, np, qimm, synth, stream, host_w, token_counts=(16, 64), iters=50):
+    """The block's Q4_K gate_up projection (24576 x 4096, 56.6 MB) and Q6_K
+    down projection (4096 x 12288, 41.3 MB) at short token counts, where the
+    time is the weight bytes over HBM bandwidth: device time per call (both
+    kernels of the split-K path) from HIP events on the launch stream."""
+    w, shapes, _, _ = host_w
+    out = {}
+    sh = stream.cuda_stream
+    for name in ("gate_up", "down"):
+        t, n, k = shapes[name]
+        W = ctx.upload(t, n, k, w[name].tobytes())
+        wbytes = synth.row_bytes(t, k) * n
+        for m in token_counts:
+            x = torch.randn((m, k), device="cuda").to(torch.bfloat16)
+            y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+            for _ in range(3):
+                ctx.qmatmul(W, x.data_ptr(), m, k, y.data_ptr(), synth.BF16, sh)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(iters):
+                ctx.qmatmul(W, x.data_ptr(), m, k, y.data_ptr(), synth.BF16, sh)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / iters * 1e3
+            gbps = wbytes / us / 1e3
+            out[f"{name}_m{m}"] = {"us": round(us, 2), "weight_mb": round(wbytes / 1e6, 1), "gbps": round(gbps, 1),
+                                   "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4)}
+            log(f"bench: {name} at {m} tokens: {us:.1f} us, {gbps:.0f} GB/s of weights "
+                f"({gbps / PEAK_HBM_GBPS:.2f} of HBM peak)")
+        W.free()
+    return out
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_block_q4km_1024.json")

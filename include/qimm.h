@@ -214,6 +214,43 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
                        int64_t seq, const float *mod, const float *pe, const qimm_kv *kv,
                        int64_t layer, uint16_t *k_out, uint16_t *v_out, void *stream);
 
+/* An attention mask, the product of build_block_causal_mask
+ * (src/attention_mask.rs:18-66) kept as its two inputs (device pointers):
+ *   image_ids  int32 [S]: JointLayout::image_ids of the call's tokens, -1 for
+ *              text; query i sees key j if i >= j or both lie in the same
+ *              image block. NULL: no block-causal term (every key visible).
+ *              Only for calls without a prefix cache, where queries and keys
+ *              are the same S tokens.
+ *   key_valid  uint8 [B][P+S] over the keys [prefix ; own], 0 = padding
+ *              (key_valid, src/quantized_transformer.rs:349-356). NULL: all
+ *              keys valid. */
+typedef struct {
+    const int32_t *image_ids;
+    const uint8_t *key_valid;
+} qimm_attn_mask;
+
+/* TransformerBlock::forward (src/quantized_transformer.rs:258-285) with
+ * Some(attention_mask) and modulation rows [B, mod_rows, 4*hidden]
+ * (mod_rows 1 broadcasts, mod_rows == S gives each token its own row).
+ * The prefix pass that fills the cache (prefix_kv,
+ * src/quantized_transformer.rs:359-392): kv NULL, mask = block-causal over the
+ * prefix tokens, the t=0 modulation row, k_out/v_out the layer's cache entry.
+ * The uncached full-sequence step (:508-543): kv NULL, mod_rows == S (t=0
+ * rows for the prefix, the step's row for the targets). The cached step with
+ * padded text: kv given, mask->key_valid only. */
+int qimm_block_forward_masked(qimm_block *blk, const float *x, float *x_out, int64_t batch,
+                              int64_t seq, const float *mod, int64_t mod_rows, const float *pe,
+                              const qimm_attn_mask *mask, const qimm_kv *kv, int64_t layer,
+                              uint16_t *k_out, uint16_t *v_out, void *stream);
+
+/* qimm_attention with a mask: chunked_attention (src/transformer.rs:259-296)
+ * called with Some(mask) (the masked branch adds -inf where the mask is 0).
+ * With mask->image_ids, kv must be NULL and so == sq. */
+int qimm_attention_masked(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64_t heads,
+                          int64_t sq, const qimm_kv *kv, int64_t layer, const uint16_t *k_own,
+                          const uint16_t *vt_own, int64_t so, float scale,
+                          const qimm_attn_mask *mask, uint16_t *out, void *stream);
+
 /* Stage timing of qimm_block_forward, the device-side counterpart of the
  * reference's per-phase wall-clock prints (src/service.rs:190-203). While
  * enabled, each forward records HIP events on its stream around its stages;

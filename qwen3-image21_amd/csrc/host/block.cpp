@@ -160,13 +160,26 @@ int qimm_block_destroy(qimm_block *blk) {
     return QIMM_OK;
 }
 
-int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t batch, int64_t seq,
-                       const float *mod, const float *pe, const qimm_kv *kv, int64_t layer, uint16_t *k_out,
-                       uint16_t *v_out, void *stream) {
+}  // extern "C"
+
+namespace {
+
+// TransformerBlock::forward (src/quantized_transformer.rs:258-285) with
+// modulation rows [B, mod_rows, 4 hidden] (mod_rows 1 broadcasts over the
+// tokens, mod_rows == seq gives one row per token) and an optional attention
+// mask; kv supplies the prefix K/V of the cached step.
+int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t batch, int64_t seq, const float *mod,
+                       int64_t mod_rows, const float *pe, const qimm_attn_mask *mask, const qimm_kv *kv,
+                       int64_t layer, uint16_t *k_out, uint16_t *v_out, void *stream) {
     if (!blk || !x || !x_out || !mod || !pe) return QIMM_ERR_ARG;
     qimm_ctx *ctx = blk->ctx;
     const int64_t hid = blk->cfg.hidden, H = blk->cfg.heads, F = blk->cfg.mlp;
     if (batch <= 0 || seq <= 0) return set_err(ctx, QIMM_ERR_SHAPE, "block forward: batch and seq must be positive");
+    if (mod_rows != 1 && mod_rows != seq)
+        return set_err(ctx, QIMM_ERR_SHAPE, "block forward: modulation needs 1 or seq rows per batch entry");
+    const int32_t *img = mask ? mask->image_ids : nullptr;
+    const uint8_t *kvalid = mask ? mask->key_valid : nullptr;
+    if (img && kv) return set_err(ctx, QIMM_ERR_SHAPE, "block forward: the block-causal mask has no prefix cache");
     if (!aligned16(x) || !aligned16(x_out) || !aligned16(mod) || !aligned16(pe) ||
         (k_out && !aligned16(k_out)) || (v_out && !aligned16(v_out)))
         return set_err(ctx, QIMM_ERR_ARG, "block forward: device pointers must be 16-byte aligned");
@@ -180,9 +193,9 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     const int64_t M = batch * seq;
     hipStream_t s = (hipStream_t)stream;
 
-    // workspace: modp [B,4h] f32 | xn [M,h] | q | k | vt | attn [M,h] | hmid [M,F] (bf16)
+    // workspace: modp [B*mod_rows,4h] f32 | xn [M,h] | q | k | vt | attn [M,h] | hmid [M,F] (bf16)
     size_t off = 0;
-    const size_t o_modp = off; off += align_up((size_t)(batch * 4 * hid) * 4);
+    const size_t o_modp = off; off += align_up((size_t)(batch * mod_rows * 4 * hid) * 4);
     const size_t o_xn = off; off += align_up((size_t)(M * hid) * 2);
     const size_t o_q = off; off += align_up((size_t)(M * hid) * 2);
     const size_t o_k = off; off += align_up((size_t)(M * hid) * 2);
@@ -216,9 +229,10 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     if (blk->profiling) QIMM_HIP(ctx, hipEventRecord(blk->ev[i], s))
     STAGE_MARK(0);
     // modulation.chunk(4) -> (1 + scale1, tanh gate1, 1 + scale2, tanh gate2)
-    QIMM_HIP(ctx, qimm::launch_mod_prep(mod, batch, hid, modp, s));
+    const int64_t rows_per = seq / mod_rows;  // tokens sharing one modulation row
+    QIMM_HIP(ctx, qimm::launch_mod_prep(mod, batch * mod_rows, hid, modp, s));
     // norm1(x) * (1 + scale1)                                  (:267-269)
-    QIMM_HIP(ctx, qimm::launch_ln_mod(x, M, hid, modp, 4 * hid, seq, xn, s));
+    QIMM_HIP(ctx, qimm::launch_ln_mod(x, M, hid, modp, 4 * hid, rows_per, xn, s));
     STAGE_MARK(1);
     // to_q/to_k/to_v + per-head RmsNorm + RoPE                 (:133-142)
     qimm::EpiParams ep{};
@@ -250,9 +264,14 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     }
     STAGE_MARK(2);
     // attention over [prefix ; own]                            (:143-148)
-    QIMM_HIP(ctx, qimm::launch_attention_log2(qb, kv ? kv->k + layer * kv->layer_elems() : nullptr,
-                                              kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, kb, vt, seq,
-                                              batch, H, seq, att, s));
+    if (img || kvalid)
+        QIMM_HIP(ctx, qimm::launch_attention_masked(qb, kv ? kv->k + layer * kv->layer_elems() : nullptr,
+                                                    kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, kb, vt,
+                                                    seq, batch, H, seq, 1.0f, img, kvalid, att, s));
+    else
+        QIMM_HIP(ctx, qimm::launch_attention_log2(qb, kv ? kv->k + layer * kv->layer_elems() : nullptr,
+                                                  kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, kb, vt,
+                                                  seq, batch, H, seq, att, s));
     STAGE_MARK(3);
     // x1 = x + tanh(gate1) * to_out(attn)                       (:150-151, 271-273)
     qimm::EpiParams er{};
@@ -262,11 +281,11 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     er.x_out = x_out;
     er.gvec = modp + hid;
     er.g_stride = 4 * hid;
-    er.g_rows_per = seq;
+    er.g_rows_per = rows_per;
     QIMM_HIP(ctx, qimm::launch_qgemm(blk->out->gw, att, M, hid, qimm::EPI_RESID, er, s));
     STAGE_MARK(4);
     // norm2(x1) * (1 + scale2)                                 (:276-278)
-    QIMM_HIP(ctx, qimm::launch_ln_mod(x_out, M, hid, modp + 2 * hid, 4 * hid, seq, xn, s));
+    QIMM_HIP(ctx, qimm::launch_ln_mod(x_out, M, hid, modp + 2 * hid, 4 * hid, rows_per, xn, s));
     STAGE_MARK(5);
     // silu(gate) * up                                          (:191-201)
     qimm::EpiParams eg{};
@@ -284,12 +303,28 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
     ed.x_out = x_out;
     ed.gvec = modp + 3 * hid;
     ed.g_stride = 4 * hid;
-    ed.g_rows_per = seq;
+    ed.g_rows_per = rows_per;
     QIMM_HIP(ctx, qimm::launch_qgemm(blk->down->gw, hm, M, F, qimm::EPI_RESID, ed, s));
     STAGE_MARK(7);
 #undef STAGE_MARK
     if (blk->profiling) blk->profiled_once = true;
     return QIMM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t batch, int64_t seq,
+                       const float *mod, const float *pe, const qimm_kv *kv, int64_t layer, uint16_t *k_out,
+                       uint16_t *v_out, void *stream) {
+    return block_forward_impl(blk, x, x_out, batch, seq, mod, 1, pe, nullptr, kv, layer, k_out, v_out, stream);
+}
+
+int qimm_block_forward_masked(qimm_block *blk, const float *x, float *x_out, int64_t batch, int64_t seq,
+                              const float *mod, int64_t mod_rows, const float *pe, const qimm_attn_mask *mask,
+                              const qimm_kv *kv, int64_t layer, uint16_t *k_out, uint16_t *v_out, void *stream) {
+    return block_forward_impl(blk, x, x_out, batch, seq, mod, mod_rows, pe, mask, kv, layer, k_out, v_out, stream);
 }
 
 int qimm_block_profile(qimm_block *blk, int enable) {
@@ -349,6 +384,32 @@ int qimm_attention(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64_t head
     QIMM_HIP(ctx, qimm::launch_attention(q, kv ? kv->k + layer * kv->layer_elems() : nullptr,
                                          kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, k_own, vt_own, so,
                                          batch, heads, sq, scale, out, (hipStream_t)stream));
+    return QIMM_OK;
+}
+
+int qimm_attention_masked(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64_t heads, int64_t sq,
+                          const qimm_kv *kv, int64_t layer, const uint16_t *k_own, const uint16_t *vt_own,
+                          int64_t so, float scale, const qimm_attn_mask *mask, uint16_t *out, void *stream) {
+    if (!mask || (!mask->image_ids && !mask->key_valid))
+        return qimm_attention(ctx, q, batch, heads, sq, kv, layer, k_own, vt_own, so, scale, out, stream);
+    if (!ctx || !q || !out || (so > 0 && (!k_own || !vt_own))) return QIMM_ERR_ARG;
+    if (batch <= 0 || heads <= 0 || sq < 0 || so < 0) return set_err(ctx, QIMM_ERR_SHAPE, "attention: bad sizes");
+    if (!aligned16(q) || !aligned16(out) || (k_own && !aligned16(k_own)) || (vt_own && !aligned16(vt_own)))
+        return set_err(ctx, QIMM_ERR_ARG, "attention: q, k, vt and out must be 16-byte aligned");
+    int64_t P = 0;
+    if (kv) {
+        if (kv->batch != batch || kv->heads != heads)
+            return set_err(ctx, QIMM_ERR_SHAPE, "attention: cache batch/heads differ");
+        if (layer < 0 || layer >= kv->layers) return set_err(ctx, QIMM_ERR_SHAPE, "attention: cache layer out of range");
+        P = kv->prefix;
+    }
+    if (P + so == 0) return set_err(ctx, QIMM_ERR_SHAPE, "attention: no keys");
+    if (mask->image_ids && (P != 0 || so != sq))
+        return set_err(ctx, QIMM_ERR_SHAPE, "attention: the block-causal mask needs no prefix and so == sq");
+    QIMM_HIP(ctx, qimm::launch_attention_masked(q, kv ? kv->k + layer * kv->layer_elems() : nullptr,
+                                                kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, k_own, vt_own,
+                                                so, batch, heads, sq, scale * 1.4426950408889634f, mask->image_ids,
+                                                mask->key_valid, out, (hipStream_t)stream));
     return QIMM_OK;
 }
 

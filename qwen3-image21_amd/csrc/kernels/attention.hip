@@ -37,6 +37,16 @@ struct Seg {
     int64_t len;
 };
 
+// Key mask of build_block_causal_mask (src/attention_mask.rs:18-66): query i
+// sees key j when key_valid[b][j] and (i >= j or i and j lie in the same
+// image block, img >= 0). img indexes the one sequence that queries and keys
+// share (no prefix); key_valid indexes the concatenated [prefix ; own] keys.
+struct KeyMask {
+    const int32_t *img;     // [Sq] image block id, -1 for text; null: no block-causal term
+    const uint8_t *kvalid;  // [B][kv_len]; null: every key valid
+    int64_t kv_len;
+};
+
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
 // v_permlane32_swap exchanges the upper 32 lanes of its first operand with
@@ -335,9 +345,10 @@ constexpr int OP = 136;     // bf16 pitch of the output staging rows
 // K and V^T tiles of 64 keys double-buffered in LDS through registers; the
 // 16-key K-slots of the PV MFMA use the key order of the S^T accumulator
 // layout, and V^T is read from LDS in the same order.
+template <bool MASKED>
 __global__ __launch_bounds__(256, 2) void attn_any_kernel(const uint16_t *__restrict__ q, Seg s0, Seg s1,
                                                       int64_t H, int64_t Sq, int64_t nq, int64_t B,
-                                                      float sl2, uint16_t *__restrict__ out) {
+                                                      float sl2, uint16_t *__restrict__ out, KeyMask km) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
 
@@ -459,6 +470,20 @@ __global__ __launch_bounds__(256, 2) void attn_any_kernel(const uint16_t *__rest
                     if (kv >= valid) st[r] = -INFINITY;
                 }
             }
+            if constexpr (MASKED) {
+                // key index in the concatenated [prefix ; own] sequence
+                const int64_t kb = (j < nb0 ? j * KB : s0.len + (j - nb0) * KB) + half * 32;
+                const int64_t qi = min(q0 + l32, Sq - 1);
+                const int32_t qimg = km.img ? km.img[qi] : -1;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int64_t kidx = kb + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (kidx >= km.kv_len) continue;  // beyond the keys: masked above
+                    bool ok = km.kvalid ? km.kvalid[bb * km.kv_len + kidx] != 0 : true;
+                    if (km.img) ok = ok && (qi >= kidx || (qimg >= 0 && km.img[kidx] == qimg));
+                    if (!ok) st[r] = -INFINITY;
+                }
+            }
             // online softmax in the log2 domain
             float mx = st[0];
 #pragma unroll
@@ -547,8 +572,8 @@ hipError_t launch(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, in
             q, s0, s1, h, sq, nq, b, sl2, out);
     } else {
         const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;
-        anylen::attn_any_kernel<<<dim3((unsigned)(nq * h * b)), dim3(256), 0, stream>>>(q, s0, s1, h, sq, nq, b,
-                                                                                       sl2, out);
+        anylen::attn_any_kernel<false><<<dim3((unsigned)(nq * h * b)), dim3(256), 0, stream>>>(
+            q, s0, s1, h, sq, nq, b, sl2, out, KeyMask{nullptr, nullptr, p + so});
     }
     return hipGetLastError();
 }
@@ -559,6 +584,24 @@ hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_
                             const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
                             int64_t sq, float scale, uint16_t *out, hipStream_t stream) {
     return launch<false>(q, kp, vtp, p, ko, vto, so, b, h, sq, scale * 1.4426950408889634f, out, stream);
+}
+
+hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
+                                   const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
+                                   int64_t sq, float sl2, const int32_t *img, const uint8_t *kvalid,
+                                   uint16_t *out, hipStream_t stream) {
+    if (sq <= 0 || b <= 0 || h <= 0) return hipSuccess;
+    if (p < 0 || so < 0 || p + so <= 0) return hipErrorInvalidValue;
+    if (img && (p != 0 || so != sq)) return hipErrorInvalidValue;  // block-causal: one shared sequence
+    Seg s0{kp, vtp, p}, s1{ko, vto, so};
+    if (p <= 0) {
+        s0 = s1;
+        s1 = Seg{ko, vto, 0};
+    }
+    const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;
+    anylen::attn_any_kernel<true><<<dim3((unsigned)(nq * h * b)), dim3(256), 0, stream>>>(
+        q, s0, s1, h, sq, nq, b, sl2, out, KeyMask{img, kvalid, p + so});
+    return hipGetLastError();
 }
 
 hipError_t launch_attention_log2(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,

@@ -94,6 +94,14 @@ hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_
                             int64_t p, const uint16_t *ko, const uint16_t *vto, int64_t so,
                             int64_t b, int64_t h, int64_t sq, float scale, uint16_t *out,
                             hipStream_t stream);
+// Masked attention (build_block_causal_mask semantics): img [sq] image block
+// ids (-1 text) for a prefix-less call where queries and keys are one
+// sequence (so == sq), kvalid [b][p + so] key validity; either may be null.
+// sl2 = softmax scale * log2(e), or 1 when q already carries it.
+hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
+                                   const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
+                                   int64_t sq, float sl2, const int32_t *img, const uint8_t *kvalid,
+                                   uint16_t *out, hipStream_t stream);
 // The same with q already multiplied by scale * log2(e) (the QKV epilogue's
 // q_scale), so scores are in log2 units.
 hipError_t launch_attention_log2(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp,

@@ -56,9 +56,12 @@ SIGNATURES = [
     ("qimm_qk_norm_rope", _i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     ("qimm_v_transpose", _i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     ("qimm_attention", _i32, [_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _f32, _vp, _vp]),
+    ("qimm_attention_masked", _i32, [_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _f32, _vp, _vp, _vp]),
     ("qimm_block_create", _i32, [_vp, _vp, _vp, C.POINTER(_vp)]),
     ("qimm_block_destroy", _i32, [_vp]),
     ("qimm_block_forward", _i32, [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp]),
+    ("qimm_block_forward_masked", _i32, [_vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp,
+                                         _vp]),
     ("qimm_block_profile", _i32, [_vp, _i32]),
     ("qimm_block_stage_times", _i32, [_vp, C.POINTER(C.c_float), _i32]),
 ]
@@ -78,6 +81,11 @@ class Tensor(C.Structure):
 class BlockTensors(C.Structure):
     _fields_ = [(n, Tensor) for n in ("to_q", "to_k", "to_v", "to_out", "norm_q", "norm_k",
                                       "gate_up", "proj", "gate_layer", "mlp_out")]
+
+
+class AttnMask(C.Structure):
+    """qimm_attn_mask: image_ids int32 [seq] (-1 = text), key_valid uint8 [batch][keys]."""
+    _fields_ = [("image_ids", _vp), ("key_valid", _vp)]
 
 
 class QimmError(RuntimeError):
@@ -171,6 +179,13 @@ class Context:
         self.check(self.lib.qimm_attention(self.h, q_dev, batch, heads, sq, kv.h if kv else None, layer,
                                            k_own, vt_own, so, scale, out_dev, stream), "qimm_attention")
 
+    def attention_masked(self, q_dev, batch, heads, sq, kv, layer, k_own, vt_own, so, scale, out_dev,
+                         image_ids=None, key_valid=None, stream=0):
+        m = AttnMask(image_ids, key_valid)
+        self.check(self.lib.qimm_attention_masked(self.h, q_dev, batch, heads, sq, kv.h if kv else None, layer,
+                                                  k_own, vt_own, so, scale, C.byref(m), out_dev, stream),
+                   "qimm_attention_masked")
+
     # -- block --
     def block_create(self, cfg: BlockConfig, tensors: BlockTensors) -> "Block":
         h = C.c_void_p()
@@ -218,6 +233,15 @@ class Block:
         self.ctx.check(self.ctx.lib.qimm_block_forward(self.h, x_dev, x_out_dev, batch, seq, mod_dev, pe_dev,
                                                        kv.h if kv else None, layer, k_out, v_out, stream),
                        "qimm_block_forward")
+
+    def forward_masked(self, x_dev, x_out_dev, batch, seq, mod_dev, mod_rows, pe_dev, image_ids=None,
+                       key_valid=None, kv=None, layer=0, k_out=None, v_out=None, stream=0):
+        """Prefix pass: per-token modulation rows (mod_rows 1 or seq) and the block-causal / key mask."""
+        m = AttnMask(image_ids, key_valid)
+        self.ctx.check(self.ctx.lib.qimm_block_forward_masked(self.h, x_dev, x_out_dev, batch, seq, mod_dev,
+                                                              mod_rows, pe_dev, C.byref(m), kv.h if kv else None,
+                                                              layer, k_out, v_out, stream),
+                       "qimm_block_forward_masked")
 
     def profile(self, enable: bool = True):
         self.ctx.check(self.ctx.lib.qimm_block_profile(self.h, 1 if enable else 0), "qimm_block_profile")

@@ -87,8 +87,19 @@ int upload_weight_rows(qimm_ctx *ctx, int type, int64_t rows, int64_t cols, cons
                     memcpy(&main_bytes[(size_t)(r * cols + b * 32)], blk + 2, 32);
                 }
         } else if (type == QIMM_TYPE_Q4_K) {
+            // 16-row groups, interleaved per super-block (the byte order the
+            // short-M kernel streams; every kernel addresses blocks the same way)
             fmt = qimm::WF_Q4_K;
-            main_bytes.assign(src, src + rows * rb);
+            if (rows % 16) {
+                delete w;
+                return set_err(ctx, QIMM_ERR_SHAPE, "weight: Q4_K tensors need rows % 16 == 0");
+            }
+            const int64_t sbs = cols / 256;
+            main_bytes.resize((size_t)(rows * rb));
+            for (int64_t r = 0; r < rows; r++)
+                for (int64_t sb = 0; sb < sbs; sb++)
+                    memcpy(&main_bytes[(size_t)((((r / 16) * sbs + sb) * 16 + r % 16) * 144)], src + r * rb + sb * 144,
+                           144);
         } else if (type == QIMM_TYPE_Q6_K) {
             fmt = qimm::WF_Q6_K;
             const int64_t nb = rows * (cols / 256);

@@ -37,6 +37,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
+// Q4_K device layout: the 144 B GGUF blocks of 16 consecutive rows are
+// interleaved per super-block, so one super-block column of a 16-row group is
+// 2304 contiguous bytes: block (n, sb) at ((n / 16) * sbs + sb) * 16 + n % 16.
+__device__ __forceinline__ const uint8_t *q4k_block(const uint8_t *q, int64_t n, int64_t sb, int64_t sbs) {
+    return q + (((n >> 4) * sbs + sb) * 16 + (n & 15)) * 144;
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
     return __uint_as_float(b << 16);
 }

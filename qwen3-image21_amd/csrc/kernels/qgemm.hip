@@ -72,7 +72,7 @@ __device__ __forceinline__ void load_w(const GemmWeight &w, int64_t n, int64_t k
         r.v[1] = *(const u32x4 *)(p + 16);
         r.s = w.scales[n * (K / 32) + k0 / 32 + h];
     } else if constexpr (FMT == WF_Q4_K) {
-        const uint8_t *blk = w.q + (n * (K / 256) + k0 / 256) * 144;
+        const uint8_t *blk = q4k_block(w.q, n, k0 / 256, K / 256);
         const int c = (int)((k0 & 255) >> 6);
         r.v[0] = *(const u32x4 *)blk;
         r.v[1] = *(const u32x4 *)(blk + 16 + 32 * c + 16 * h);

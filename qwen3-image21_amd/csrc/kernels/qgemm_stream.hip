@@ -68,7 +68,7 @@ template <int FMT>
 __device__ __forceinline__ void load_step(const GemmWeight &w, int64_t n, int64_t k0, int kg, WStep &r) {
     const int64_t K = w.k;
     if constexpr (FMT == WF_Q4_K) {
-        const uint8_t *blk = w.q + (n * (K / 256) + k0 / 256) * 144;
+        const uint8_t *blk = q4k_block(w.q, n, k0 / 256, K / 256);
         const int c = (int)((k0 & 255) >> 6);
         r.a = *(const u32x4 *)blk;
         r.c = *(const u32x2 *)(blk + 16 + 32 * c + 8 * kg);
@@ -251,6 +251,222 @@ __global__ __launch_bounds__(256) void qgemm_stream_kernel(const uint16_t *__res
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K at M <= 16: MFMA on the raw 4-bit codes, scales applied afterwards.
+//
+// For sub-block j (32 values) of row n: w = ds_j q - dm_j with ds_j = d sc_j,
+// dm_j = dmin m_j. The B operand is the exact bf16 of 128 + q (bits 0x4300 |
+// q), so one v_mfma_f32_16x16x32_bf16 gives S'_j = sum x (128 + q) for 16
+// tokens x 16 rows, and
+//     sum_k x w = sum_j ds_j S'_j - sum_j (128 ds_j + dm_j) X_j,
+// X_j = sum of x over the sub-block. The first sum is 4 FMAs per lane per
+// sub-block; the second is an f32 MFMA (16x16x4) per four sub-blocks, its
+// A operand X from a bf16 MFMA with row-selector ones, so no per-value
+// dequantization runs at all. The result is the exact product of the bf16
+// activations and the exact Q4_K weights up to f32 summation order.
+//
+// One workgroup per CU (8 waves, 131 KB LDS holding x[16][4096] bf16): x is
+// copied to LDS once by direct loads, then each wave streams its share of the
+// (16-row group, super-block) tiles -- 2304 contiguous bytes in the device
+// layout -- through a register ring four tiles deep. Waves split the
+// workgroup's tiles evenly; the partial tile sums of a wave are reduced in LDS
+// in wave order (deterministic) and written to part[c][m][n] for the
+// split-K epilogue.
+namespace m16 {
+
+constexpr int NW = 8;       // waves per workgroup
+constexpr int KC = 4096;    // k per workgroup (x[16][KC] in LDS)
+constexpr int SBC = KC / 256;
+constexpr int ROWB = KC * 2 + 16;  // padded row: the 16 rows of a fragment read hit distinct banks
+constexpr int DEPTH = 4;    // tiles in flight per wave
+
+struct Raw {
+    u32x4 h;
+    u32x2 q[4];
+};
+
+// B fragments of 8 consecutive codes (two words): bf16 128 + q of the low and
+// of the high nibbles, by byte permutes against a 0x43 source register.
+__device__ __forceinline__ void codes8(uint32_t w0, uint32_t w1, u32x4 &lo, u32x4 &hi) {
+    const uint32_t C43 = 0x43434343u;
+    const uint32_t l0 = w0 & 0x0F0F0F0Fu, l1 = w1 & 0x0F0F0F0Fu;
+    const uint32_t h0 = (w0 >> 4) & 0x0F0F0F0Fu, h1 = (w1 >> 4) & 0x0F0F0F0Fu;
+    lo = u32x4{__builtin_amdgcn_perm(C43, l0, 0x04010400u), __builtin_amdgcn_perm(C43, l0, 0x04030402u),
+               __builtin_amdgcn_perm(C43, l1, 0x04010400u), __builtin_amdgcn_perm(C43, l1, 0x04030402u)};
+    hi = u32x4{__builtin_amdgcn_perm(C43, h0, 0x04010400u), __builtin_amdgcn_perm(C43, h0, 0x04030402u),
+               __builtin_amdgcn_perm(C43, h1, 0x04010400u), __builtin_amdgcn_perm(C43, h1, 0x04030402u)};
+}
+
+__device__ __forceinline__ float cvt_f16_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu)); }
+__device__ __forceinline__ float cvt_f16_hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
+
+// PER tiles per wave (compile time, so every wait on the ring is exact).
+// Grid: NG n-groups x C k-chunks; group g holds T 16-row tiles.
+template <int PER>
+__global__ __launch_bounds__(512) void q4k_m16_kernel(const uint16_t *__restrict__ A, int M, int64_t lda,
+                                                      GemmWeight w, int C, int T, float *__restrict__ part) {
+    __shared__ __attribute__((aligned(16))) uint8_t xs[16 * ROWB];
+    __shared__ __attribute__((aligned(16))) float red[NW][2][256];
+    __shared__ int tags[NW][2];
+    constexpr int D = DEPTH < PER ? DEPTH : PER;
+    constexpr int R = D + 1;  // ring slots: tile u + D is requested before tile u is computed
+    const int lane = threadIdx.x & 63, l16 = lane & 15, kg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t N = w.n, SB = w.k / 256;
+    const int NG = (int)((N / 16) / T);
+    const int ng = blockIdx.x % NG, c = blockIdx.x / NG;
+    const int64_t k0 = (int64_t)c * KC;
+    const int t0 = wave * PER;
+
+    // x chunk -> LDS by direct loads (instruction i of wave w fills 64
+    // consecutive 16 B chunks of one row); rows past M repeat row M - 1
+    {
+        constexpr int NI = 16 * KC / 8 / 64 / NW;
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int q0 = (i * NW + wave) * 64;
+            const int m = q0 / (KC / 8), s0 = q0 % (KC / 8);
+            const uint16_t *src = A + (int64_t)min(m, M - 1) * lda + k0 + 8 * (s0 + lane);
+            __builtin_amdgcn_global_load_lds((const void *)src, (lds_ptr_t)(xs + m * ROWB + 16 * s0), 16, 0, 0);
+        }
+    }
+    // the wave's tiles in (n-tile, super-block) order
+    Raw ring[R];
+    const int nt0 = t0 / SBC, sb0 = t0 % SBC;
+    auto load_tile = [&](Raw &r, int u) {
+        const int ntl = nt0 + (sb0 + u) / SBC, sbl = (sb0 + u) % SBC;
+        const int64_t n = (int64_t)(ng * T + ntl) * 16 + l16;
+        const uint8_t *b = q4k_block(w.q, n, (int64_t)c * SBC + sbl, SB);
+        r.h = *(const u32x4 *)b;
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) r.q[cc] = *(const u32x2 *)(b + 16 + 32 * cc + 8 * kg);
+    };
+#pragma unroll
+    for (int u = 0; u < D; u++) load_tile(ring[u], u);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(5 * D) : "memory");
+
+    // A operands of the sub-block sums: rows 4 s .. 4 s + 3 of ones[s] are 1
+    bf16x8 ones[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const uint32_t v = (l16 >> 2) == s ? 0x3F803F80u : 0u;
+        ones[s] = __builtin_bit_cast(bf16x8, u32x4{v, v, v, v});
+    }
+    f32x4 accA = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
+    int seg = 0;
+    const uint8_t *xlane = xs + l16 * ROWB + 16 * kg;
+    auto tile = [&](const Raw &r, int u) {
+        const int ntl = nt0 + (sb0 + u) / SBC, sbl = (sb0 + u) % SBC;
+        const uint32_t hx = r.h[0], hy = r.h[1], hz = r.h[2], hw = r.h[3];
+        const float d = cvt_f16_lo(hx), dmin = cvt_f16_hi(hx);
+        // 6-bit scales / mins of sub-blocks 0..3 (lo) and 4..7 (hi), one per byte
+        const uint32_t sc_lo = hy & 0x3F3F3F3Fu, m_lo = hz & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (hw & 0x0F0F0F0Fu) | ((hy >> 2) & 0x30303030u);
+        const uint32_t m_hi = ((hw >> 4) & 0x0F0F0F0Fu) | ((hz >> 2) & 0x30303030u);
+        // f32-MFMA B operand: 128 ds_j + dm_j of sub-blocks kg and 4 + kg
+        const uint32_t sh = 8u * (uint32_t)kg;
+        const float cc0 = fmaf(128.f, d * (float)((sc_lo >> sh) & 0xffu), dmin * (float)((m_lo >> sh) & 0xffu));
+        const float cc1 = fmaf(128.f, d * (float)((sc_hi >> sh) & 0xffu), dmin * (float)((m_hi >> sh) & 0xffu));
+        const uint8_t *xt = xlane + sbl * 512;
+        bf16x8 af[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) af[j] = *(const bf16x8 *)(xt + 64 * j);
+        // X[m][j0 + kg] in the A layout of the f32 MFMA (all four registers)
+        f32x4 xq0 = {0.f, 0.f, 0.f, 0.f}, xq1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            xq0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], af[j], xq0, 0, 0, 0);
+            xq1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], af[4 + j], xq1, 0, 0, 0);
+        }
+        accM = __builtin_amdgcn_mfma_f32_16x16x4f32(xq0[0], cc0, accM, 0, 0, 0);
+        accM = __builtin_amdgcn_mfma_f32_16x16x4f32(xq1[0], cc1, accM, 0, 0, 0);
+        // the eight code products (independent accumulators), then the scales
+        u32x4 bq[8];
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) codes8(r.q[cc][0], r.q[cc][1], bq[2 * cc], bq[2 * cc + 1]);
+        f32x4 tv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            tv[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[j], __builtin_bit_cast(bf16x8, bq[j]),
+                                                            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float ds = d * (float)(((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3))) & 0xffu);
+#pragma unroll
+            for (int e = 0; e < 4; e++) accA[e] = fmaf(ds, tv[j][e], accA[e]);
+        }
+        if (sbl == SBC - 1 || u == PER - 1) {  // end of this n-tile's part in the wave
+#pragma unroll
+            for (int e = 0; e < 4; e++) red[wave][seg][(4 * kg + e) * 16 + l16] = accA[e] - accM[e];
+            if (lane == 0) tags[wave][seg] = ntl;
+            seg++;
+            accA = f32x4{0.f, 0.f, 0.f, 0.f};
+            accM = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        if (u + D < PER) load_tile(ring[(u + D) % R], u + D);
+        tile(ring[u % R], u);
+    }
+    if (lane == 0 && seg < 2) tags[wave][1] = -1;
+    __syncthreads();
+    // per-tile sums over the waves that covered it, in wave order
+    for (int p = threadIdx.x; p < T * 256; p += 64 * NW) {
+        const int tt = p >> 8, e = p & 255, m = e >> 4, nl = e & 15;
+        float s = 0.f;
+        for (int wv = 0; wv < NW; wv++)
+            for (int sg = 0; sg < 2; sg++)
+                if (tags[wv][sg] == tt) s += red[wv][sg][e];
+        if (m < M) part[((int64_t)c * M + m) * N + (int64_t)(ng * T + tt) * 16 + nl] = s;
+    }
+}
+
+// Grid of the M <= 16 kernel, or false when the shape does not tile exactly:
+// K a multiple of 4096 (C chunks), NG n-groups of T 16-row tiles with
+// NG * C equal to the CU count, each wave covering at most two n-tiles.
+bool plan(const GemmWeight &w, int64_t m, int cus, int &C, int &T, int &NG) {
+    if (w.fmt != WF_Q4_K || m < 1 || m > 16 || w.k % KC || w.n % 16 || cus <= 0) return false;
+    C = (int)(w.k / KC);
+    const int64_t tiles16 = w.n / 16;
+    if ((tiles16 * C) % cus) return false;
+    T = (int)(tiles16 * C / cus);
+    if (T < 1 || T > 8 || tiles16 % T) return false;
+    NG = (int)(tiles16 / T);
+    return (int64_t)NG * C == cus;
+}
+
+int device_cus() {
+    static int cus = -1;
+    if (cus < 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+            cus = v;
+        else
+            cus = 0;
+    }
+    return cus;
+}
+
+hipError_t launch(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, float *part, int C, int T, int NG,
+                  hipStream_t stream) {
+    const dim3 grid((unsigned)(NG * C)), block(64 * NW);
+    switch (2 * T) {
+    case 2: q4k_m16_kernel<2><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
+    case 4: q4k_m16_kernel<4><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
+    case 6: q4k_m16_kernel<6><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
+    case 8: q4k_m16_kernel<8><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
+    case 10: q4k_m16_kernel<10><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
+    case 12: q4k_m16_kernel<12><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
+    case 14: q4k_m16_kernel<14><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
+    case 16: q4k_m16_kernel<16><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace m16
+
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
 // Sum of the split-K partials of C[m][n], in split order.
@@ -343,6 +559,8 @@ hipError_t launch_fmt(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t
 // chunks stay whole 256-value groups and the partial sums (written and read
 // once each) stay under half the weight bytes.
 int qgemm_stream_splits(const GemmWeight &w, int64_t m) {
+    int C, T, NG;
+    if (m16::plan(w, m, m16::device_cus(), C, T, NG)) return C;
     const int64_t nt = w.n / 64, kst = w.k / 256;
     const double wbytes = (double)w.n * (double)w.k * (w.fmt == WF_Q4_K ? 0.5625 : w.fmt == WF_Q6_K ? 0.875
                                                        : w.fmt == WF_Q8_0 ? 1.0625 : 2.0);
@@ -362,11 +580,19 @@ size_t qgemm_stream_workspace(const GemmWeight &w, int64_t m) {
 
 hipError_t launch_qgemm_stream(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
                                const EpiParams &ep, float *part, hipStream_t stream) {
-    const int splits = qgemm_stream_splits(w, m);
+    int splits = qgemm_stream_splits(w, m);
     hipError_t e;
+    int C, T, NG;
     switch (w.fmt) {
     case WF_Q8_0: e = launch_fmt<WF_Q8_0>(w, a, m, lda, part, splits, stream); break;
-    case WF_Q4_K: e = launch_fmt<WF_Q4_K>(w, a, m, lda, part, splits, stream); break;
+    case WF_Q4_K:
+        if (m16::plan(w, m, m16::device_cus(), C, T, NG)) {
+            splits = C;
+            e = m16::launch(w, a, m, lda, part, C, T, NG, stream);
+        } else {
+            e = launch_fmt<WF_Q4_K>(w, a, m, lda, part, splits, stream);
+        }
+        break;
     case WF_Q6_K: e = launch_fmt<WF_Q6_K>(w, a, m, lda, part, splits, stream); break;
     case WF_BF16: e = launch_fmt<WF_BF16>(w, a, m, lda, part, splits, stream); break;
     default: return hipErrorInvalidValue;

@@ -150,6 +150,24 @@ def test_block_config1_shape(torch_cuda, qctx):
     check(got, ref_e, x, exact=True)
 
 
+@pytest.mark.parametrize("b,s,p", [(1, 8, 16), (2, 6, 0)])
+def test_block_hidden4096_short_m(torch_cuda, qctx, b, s, p):
+    """Hidden 4096 (32 heads) at M <= 16 tokens: the fused QKV (12288 x 4096)
+    and output (4096 x 4096) projections take the Q4_K code-product kernel,
+    with the QKV and residual epilogues; a short MLP (512) keeps the oracle
+    quick and runs on the split-K dequantizing kernel."""
+    cfg = dict(hidden=4096, heads=32, head_dim=128, mlp=512)
+    w, x, mod, pe, kpre, vpre = make_case(21 + b + s, cfg, b, s, p, synth.Q4_K, synth.Q6_K)
+    got, (k, v) = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)
+    ref, kr, vr = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
+    check(got, ref, x)
+    ref_e, kre, vre = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
+    check(got, ref_e, x, exact=True)
+    for kk, vv in ((kr, vr), (kre, vre)):
+        assert cos_sim(k, kk) >= 0.9999 and max_abs_rel(k, kk) <= 2e-2
+        assert cos_sim(v, vv) >= 0.9999 and max_abs_rel(v, vv) <= 2e-2
+
+
 def test_block_rejects_bad_config(torch_cuda, qctx):
     keep = []
     w = synth.block_weights(1, 256, 2, 768, synth.Q8_0)

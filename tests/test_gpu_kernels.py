@@ -91,6 +91,25 @@ def test_qmatmul_matches_bf16_weight_products(torch_cuda, qctx, t, m, n, k):
         assert cos_sim(got, yc) >= 0.9999 and max_abs_rel(got, yc) <= 2e-2
 
 
+@pytest.mark.parametrize("m,n,k", [(16, 4096, 4096),    # one 16-row tile per workgroup
+                                   (1, 8192, 4096),     # a single token, two tiles per workgroup
+                                   (7, 12288, 4096),    # three tiles: a wave spans two n-tiles
+                                   (5, 4096, 8192)])    # two 4096-k chunks
+def test_qmatmul_q4k_short_m_exact_weights(torch_cuda, qctx, m, n, k):
+    """Q4_K at M <= 16 and K % 4096 == 0 multiplies the raw codes and applies the
+    scales afterwards: the product of the bf16 activations and the exact
+    (not bf16-rounded) Q4_K weights, up to f32 summation order."""
+    got, a, w = _gemm_case(torch_cuda, qctx, synth.Q4_K, m, n, k, seed=m + n + k)
+    Wd = O.dequantize(synth.Q4_K, w, n * k).reshape(n, k).astype(np.float64)
+    want = a.astype(np.float64) @ Wd.T
+    scale = np.abs(a).astype(np.float64) @ np.abs(Wd).T
+    assert np.all(np.abs(got - want) <= 2e-5 * scale + 1e-6), np.max(np.abs(got - want) / (scale + 1e-9))
+    ye = O.qmatmul(synth.Q4_K, w, n, k, a, O.EXACT)
+    assert cos_sim(got, ye) >= 0.9999 and max_abs_rel(got, ye) <= 2e-2
+    yc = O.qmatmul(synth.Q4_K, w, n, k, a, O.CANDLE)
+    assert cos_sim(got, yc) >= 0.9999 and max_abs_rel(got, yc) <= 2e-2
+
+
 @pytest.mark.parametrize("m", [64, 700])
 def test_qmatmul_bf16_output(torch_cuda, qctx, m):
     got, a, w = _gemm_case(torch_cuda, qctx, synth.Q4_K, m, 256, 512, seed=5, out_type=synth.BF16)

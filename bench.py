@@ -48,6 +48,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=16, help="steps timed stage by stage after the loop")
     ap.add_argument("--cpu-rows", type=int, default=4096, help="token rows in the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-weight-streaming", action="store_true",
+                    help="skip the short-token weight-streaming measurements")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB, the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc pass")
@@ -195,7 +197,7 @@ def main():
     block_flop = att_flop + 2.0 * S_IMG * HID * (3 * HID + HID + 2 * MLP) + 2.0 * S_IMG * MLP * HID
 
     # ---- weight streaming at short token counts (the HBM-bound regime) ----
-    streaming = weight_streaming(ctx, torch, np, qimm, synth, stream, host_w0)
+    streaming = None if args.no_weight_streaming else weight_streaming(ctx, torch, np, qimm, synth, stream, host_w0)
 
     # ---- CPU baseline: the oracle in candle mode on a bounded sample ----
     cpu = None

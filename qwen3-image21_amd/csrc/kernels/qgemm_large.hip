@@ -10,13 +10,17 @@
 // for 16 MFMAs, half the LDS traffic per flop of a 64x64 wave tile. LDS rows
 // are dense 128 B with the 16 B chunk index XOR-swizzled by (row & 7), so both
 // the staging writes and the MFMA operand reads are bank-conflict free.
-// The A tile goes global->LDS directly (no registers), one k step ahead; the
-// raw weights of step k+2 are loaded while step k computes and the weights of
-// step k+1 are dequantized into the other LDS stage between its MFMAs. The q/k/v epilogue stages its outputs
-// through LDS; the others work on the accumulators in place.
+// The A tile goes global->LDS directly (no registers); the raw weights are
+// loaded two steps ahead and those of step k+1 are dequantized into the other
+// LDS stage between the MFMAs of step k. One barrier per 64-wide k step; the
+// operand fragments of the next 16-wide slice are read while the current
+// slice's MFMAs run. The q/k/v epilogue stages its outputs through LDS; the
+// others work on the accumulators in place.
 // Tiles are ordered XCD-aware: each XCD gets a contiguous range of tiles,
 // grouped 4 M-tiles at a time so concurrently resident tiles share A rows and
 // W columns in that XCD's L2.
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -234,9 +238,10 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
             __builtin_amdgcn_global_load_lds((const void *)(asrc[i] + k0), (lds_ptr_t)(base + (8 * wave + i) * 8 * ROWB),
                                              16, 0, 0);
     };
-    // W staging: row n0 + tid, all 8 chunks, through registers (dequantized)
+    // W staging: row n0 + tid, all 8 chunks, through registers (dequantized);
+    // raw weights double-buffered two steps ahead
     const int64_t wrow = n0 + tid;
-    WRaw rw0, rw1;
+    WRaw rw[2];
 
     f32x16 acc[4][4];
 #pragma unroll
@@ -246,74 +251,84 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-    // MFMAs of one stage; with `store`, the weights in rw (step at knext) are
-    // dequantized into the other stage, two 8-wide chunks after each group of
-    // eight MFMAs so the VALU work overlaps the matrix pipe.
-    auto compute = [&](int stage, const WRaw &rw, int64_t knext, bool store) {
+    // operand fragments of one 16-wide k slice, double-buffered across slices
+    // (buffer and slice indices are compile-time after unrolling)
+    bf16x8 fa[2][4], fb[2][4];
+    auto rd = [&](int buf, int stage, int kk) __attribute__((always_inline)) {
         const uint8_t *as = lds + stage * STAGE;
         const uint8_t *bs = as + 256 * ROWB;
-        uint8_t *bn = lds + (stage ^ 1) * STAGE + 256 * ROWB;
-        WScale sc{};
-        if (store) sc = w_scales<FMT>(rw, knext);
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            bf16x8 af[4], bfr[4];
+        for (int i = 0; i < 4; i++) fa[buf][i] = *(const bf16x8 *)(as + swz(wm * 128 + i * 32 + l32, 2 * kk + g));
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = wm * 128 + i * 32 + l32;
-                af[i] = *(const bf16x8 *)(as + swz(r, 2 * kk + g));
-            }
+        for (int j = 0; j < 4; j++) fb[buf][j] = *(const bf16x8 *)(bs + swz(wn * 128 + j * 32 + l32, 2 * kk + g));
+    };
+    auto mm = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int r = wn * 128 + j * 32 + l32;
-                bfr[j] = *(const bf16x8 *)(bs + swz(r, 2 * kk + g));
-            }
-#pragma unroll
-            for (int half = 0; half < 2; half++) {
-#pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    const int i = 2 * half + (q >> 2), j = q & 3;
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-                }
-                if (store) {
-                    const int c = 2 * kk + half;
-                    *(u32x4 *)(bn + swz(tid, c)) = w_chunk<FMT>(rw, sc, c, knext);
-                }
-            }
+        for (int q = 0; q < 16; q++) {
+            const int i = q >> 2, j = q & 3;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[buf][i], fb[buf][j], acc[i][j], 0, 0, 0);
         }
     };
 
-    // vmcnt(8): every vector-memory op older than the 8 A-tile loads just
-    // issued has completed (loads complete in issue order).
-    constexpr int WAIT_ALL_BUT_8 = 0x0f70 | 8;
-    // prologue: A and W of step 0 into stage 0; W of step 1 in registers; A of
-    // step 1 in flight (step indices clamped to the last step: redundant loads,
-    // no branches)
+    // prologue: step 0 staged in stage 0; raw weights of steps 1 and 2 and the
+    // A tile of step 1 loaded (step indices clamped to the last step: redundant
+    // loads, no branches)
+    load_w<FMT>(w, wrow, 0, rw[0]);
     dma_a(0, 0);
-    load_w<FMT>(w, wrow, 0, rw0);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     {
-        const WScale sc = w_scales<FMT>(rw0, 0);
+        const WScale sc = w_scales<FMT>(rw[0], 0);
         uint8_t *bn = lds + 256 * ROWB;
 #pragma unroll
-        for (int j = 0; j < 8; j++) *(u32x4 *)(bn + swz(tid, j)) = w_chunk<FMT>(rw0, sc, j, 0);
+        for (int j = 0; j < 8; j++) *(u32x4 *)(bn + swz(tid, j)) = w_chunk<FMT>(rw[0], sc, j, 0);
     }
-    load_w<FMT>(w, wrow, (int64_t)min(1, KT - 1) * BK, rw0);
+    load_w<FMT>(w, wrow, (int64_t)min(1, KT - 1) * BK, rw[1]);
     dma_a(1, (int64_t)min(1, KT - 1) * BK);
-    __builtin_amdgcn_s_waitcnt(WAIT_ALL_BUT_8);
+    load_w<FMT>(w, wrow, (int64_t)min(2, KT - 1) * BK, rw[0]);
+    __builtin_amdgcn_s_waitcnt(0xc070);  // vmcnt(0) lgkmcnt(0)
     __syncthreads();
-    // Steady state, one branch-free body. On entry to step kt, stage kt&1 holds
-    // A and W of step kt, rw0 holds the raw weights of step kt+1 and the A tile
-    // of step kt+1 is in flight to stage (kt+1)&1.
-    for (int kt = 0; kt < KT - 1; kt++) {
-        load_w<FMT>(w, wrow, (int64_t)min(kt + 2, KT - 1) * BK, rw1);
-        compute(kt & 1, rw0, (int64_t)(kt + 1) * BK, true);  // + W of step kt+1 into stage (kt+1)&1
-        rw0 = rw1;
-        __syncthreads();  // stage kt&1 is free; W of step kt+1 is staged
-        dma_a(kt & 1, (int64_t)min(kt + 2, KT - 1) * BK);
-        __builtin_amdgcn_s_waitcnt(WAIT_ALL_BUT_8);  // A of step kt+1 has landed
+    rd(0, 0, 0);
+
+    // Step kt, stage s = kt & 1, t = s ^ 1. On entry fa/fb[0] hold slice 0 of
+    // step kt, rw[t] holds the raw weights of step kt+1, rw[s] those of step
+    // kt+2 and stage t holds the A tile of step kt+1. Slices 0-2 dequantize step
+    // kt+1 into stage t while their MFMAs run; then ONE barrier per step: stage t
+    // is complete, and every wave is done reading stage s (its last slice sits
+    // in registers). After it, stage s receives the A tile of step kt+2 and
+    // rw[t] the raw weights of step kt+3 while slice 3 computes and slice 0 of
+    // step kt+1 is read. The vmcnt(0) before the barrier covers loads issued a
+    // whole step earlier.
+    auto step = [&](int kt, auto sc_) __attribute__((always_inline)) {
+        constexpr int s = decltype(sc_)::value, t = s ^ 1;
+        const int64_t knext = (int64_t)min(kt + 1, KT - 1) * BK;
+        uint8_t *bn = lds + t * STAGE + 256 * ROWB;
+        const WScale sc = w_scales<FMT>(rw[t], knext);
+        rd(1, s, 1);
+        mm(0);
+#pragma unroll
+        for (int c = 0; c < 3; c++) *(u32x4 *)(bn + swz(tid, c)) = w_chunk<FMT>(rw[t], sc, c, knext);
+        rd(0, s, 2);
+        mm(1);
+#pragma unroll
+        for (int c = 3; c < 6; c++) *(u32x4 *)(bn + swz(tid, c)) = w_chunk<FMT>(rw[t], sc, c, knext);
+        rd(1, s, 3);
+        mm(0);
+#pragma unroll
+        for (int c = 6; c < 8; c++) *(u32x4 *)(bn + swz(tid, c)) = w_chunk<FMT>(rw[t], sc, c, knext);
+        __builtin_amdgcn_s_waitcnt(0xc070);  // vmcnt(0) lgkmcnt(0)
         __syncthreads();
+        dma_a(s, (int64_t)min(kt + 2, KT - 1) * BK);
+        load_w<FMT>(w, wrow, (int64_t)min(kt + 3, KT - 1) * BK, rw[t]);
+        rd(0, t, 0);
+        mm(1);
+    };
+    int kt = 0;
+    for (; kt + 1 < KT; kt += 2) {
+        step(kt, std::integral_constant<int, 0>{});
+        step(kt + 1, std::integral_constant<int, 1>{});
     }
-    compute((KT - 1) & 1, rw0, 0, false);
+    if (kt < KT) step(kt, std::integral_constant<int, 0>{});
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): no load into LDS still in flight
 
     // ---- epilogue, straight from the accumulators ----
     // acc[i][j][r] holds row wm*128 + 32i + 8(r/4) + 4g + (r%4) and column

@@ -78,6 +78,20 @@ __device__ __forceinline__ u32x4 cvt8(uint32_t x0, uint32_t x1, float ds, float 
                  pack_bf16x2(f(x1, 0), f(x1, 1)), pack_bf16x2(f(x1, 2), f(x1, 3))};
 }
 
+// f32 fma with src0 read as f16 from the low / high half of x: a code q held
+// as the f16 subnormal q * 2^-24 (exact) times a scale pre-multiplied by 2^24
+// gives q*scale + off with a single rounding, no separate integer convert.
+__device__ __forceinline__ float mix_lo(uint32_t x, float s, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(s), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float mix_hi(uint32_t x, float s, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(s), "v"(c));
+    return r;
+}
+
 __device__ __forceinline__ uint32_t word(const u32x4 *v, int byte_off) {
     return v[byte_off >> 4][(byte_off >> 2) & 3];
 }
@@ -138,9 +152,11 @@ __device__ __forceinline__ WScale w_scales(const WRaw &r, int64_t k0) {
         float sc0, m0, sc1, m1;
         q4k_sc_m(r.v[0], 2 * c, sc0, m0);
         q4k_sc_m(r.v[0], 2 * c + 1, sc1, m1);
-        s.a0 = d * sc0;
+        // low nibbles (sub-block 2c) sit at f16 bits 0-3, high nibbles
+        // (sub-block 2c+1) at bits 4-7: the scales carry 2^24 and 2^20
+        s.a0 = d * sc0 * 0x1p24f;
         s.b0 = -(dmin * m0);
-        s.a1 = d * sc1;
+        s.a1 = d * sc1 * 0x1p20f;
         s.b1 = -(dmin * m1);
     } else if constexpr (FMT == WF_Q6_K) {
         // values 32 r + l of half hh, r in {2o, 2o+1}; scale index 8hh + 2r + l/16
@@ -166,11 +182,16 @@ __device__ __forceinline__ u32x4 w_chunk(const WRaw &r, const WScale &s, int j, 
         const uint32_t x0 = opaque(word(r.v, 8 * j) ^ 0x80808080u), x1 = opaque(word(r.v, 8 * j + 4) ^ 0x80808080u);
         return j < 4 ? cvt8(x0, x1, s.a0, s.b0) : cvt8(x0, x1, s.a1, s.b1);
     } else if constexpr (FMT == WF_Q4_K) {
-        // k < 32: low nibbles of qs bytes [8j, 8j+8); k >= 32: high nibbles of bytes [8(j-4), ...)
+        // k < 32: low nibbles of qs bytes [8j, 8j+8); k >= 32: high nibbles of
+        // bytes [8(j-4), ...). The halves of (y & m) hold bytes 0 and 2, those
+        // of ((y >> 8) & m) bytes 1 and 3.
         const int jb = j & 3;
         const uint32_t y0 = word(r.v + 1, 8 * jb), y1 = word(r.v + 1, 8 * jb + 4);
-        if (j < 4) return cvt8(opaque(y0 & 0x0F0F0F0Fu), opaque(y1 & 0x0F0F0F0Fu), s.a0, s.b0);
-        return cvt8(opaque((y0 >> 4) & 0x0F0F0F0Fu), opaque((y1 >> 4) & 0x0F0F0F0Fu), s.a1, s.b1);
+        const uint32_t m = j < 4 ? 0x000F000Fu : 0x00F000F0u;
+        const float a = j < 4 ? s.a0 : s.a1, b = j < 4 ? s.b0 : s.b1;
+        const uint32_t p0 = y0 & m, p1 = (y0 >> 8) & m, p2 = y1 & m, p3 = (y1 >> 8) & m;
+        return u32x4{pack_bf16x2(mix_lo(p0, a, b), mix_lo(p1, a, b)), pack_bf16x2(mix_hi(p0, a, b), mix_hi(p1, a, b)),
+                     pack_bf16x2(mix_lo(p2, a, b), mix_lo(p3, a, b)), pack_bf16x2(mix_hi(p2, a, b), mix_hi(p3, a, b))};
     } else if constexpr (FMT == WF_Q6_K) {
         // k = 32 rl + l with rl = j/4, l in [8(j%4), +8): low 4 bits from ql byte
         // 32 rl + l (low nibble when o == 0, else high), high 2 bits from qh byte l

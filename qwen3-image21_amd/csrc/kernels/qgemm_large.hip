@@ -360,25 +360,45 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int64_t mi = m0 + wm * 128 + i * 32 + 4 * g;
-        if constexpr (EPI == EPI_F32 || EPI == EPI_BF16 || EPI == EPI_RESID) {
+        if constexpr (EPI == EPI_F32 || EPI == EPI_BF16) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int64_t m = mi + 8 * (r >> 2) + (r & 3);
                 if (m >= M) continue;
-                const float *grow = nullptr;
-                if constexpr (EPI == EPI_RESID) grow = ep.gvec + (int64_t)((int)m / (int)ep.g_rows_per) * ep.g_stride;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const int64_t n = nw + j * 32 + l32;
                     const float v = acc[i][j][r];
                     if constexpr (EPI == EPI_F32) {
                         ((float *)ep.out)[m * ep.ldo + n] = v;
-                    } else if constexpr (EPI == EPI_BF16) {
-                        ((uint16_t *)ep.out)[m * ep.ldo + n] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
                     } else {
-                        ep.x_out[m * N + n] = ep.x_in[m * N + n] + grow[n] * v;
+                        ((uint16_t *)ep.out)[m * ep.ldo + n] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
                     }
                 }
+            }
+        } else if constexpr (EPI == EPI_RESID) {
+            // Every load of the 16 rows x 4 columns first (rows past M clamped
+            // to M-1), then the stores: one memory round trip per 32 rows
+            // instead of one per row. x_out may alias x_in: each element is read
+            // and written by the same lane, loads before stores.
+            float xv[16][4], gv[16][4];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int64_t m = min(mi + 8 * (r >> 2) + (r & 3), M - 1);
+                const float *grow = ep.gvec + (int64_t)((int)m / (int)ep.g_rows_per) * ep.g_stride;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int64_t n = nw + j * 32 + l32;
+                    xv[r][j] = ep.x_in[m * N + n];
+                    gv[r][j] = grow[n];
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int64_t m = mi + 8 * (r >> 2) + (r & 3);
+                if (m >= M) continue;
+#pragma unroll
+                for (int j = 0; j < 4; j++) ep.x_out[m * N + nw + j * 32 + l32] = xv[r][j] + gv[r][j] * acc[i][j][r];
             }
         } else if constexpr (EPI == EPI_SWIGLU) {
             // columns 32j + l32 (j < 2) are gate, 64 + 32j + l32 the matching up

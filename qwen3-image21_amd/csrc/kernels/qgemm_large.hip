@@ -433,24 +433,44 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
 #pragma unroll
             for (int j = 0; j < 4; j++) wq[j] = nwt[j * 32 + l32];
             const bool odd = lane & 1;
+            const uint32_t Su = (uint32_t)S, Mlast = (uint32_t)(M - 1);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
+                // per 32 rows: the RoPE (cos, sin) pairs of all 16 x 4 elements
+                // first, then the 16 sums of squares reduced over their 32
+                // lanes together, so loads and cross-lane steps overlap
+                float2 cs[16][4];
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const uint32_t t = (uint32_t)(i * 32 + 8 * (r >> 2) + 4 * g + (r & 3));
+                    const uint32_t s = min((uint32_t)mw + t, Mlast) % Su;
+                    const float *pr = ep.pe + (int64_t)s * 128;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) cs[r][j] = *(const float2 *)(pr + ((j * 32 + l32) & ~1));
+                }
+                float ss[16];
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    ss[r] = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) ss[r] += acc[i][j][r] * acc[i][j][r];
+                }
+#pragma unroll
+                for (int o = 16; o > 0; o >>= 1)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) ss[r] += __shfl_xor(ss[r], o);
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int t = i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    const int s = (int)(min(mw + t, M - 1) % S);
-                    float ss = 0.f;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) ss += acc[i][j][r] * acc[i][j][r];
-                    ss = group_sum(ss, 32);  // the 32 lanes holding this row
-                    const float rs = 1.0f / sqrtf(ss * (1.0f / 128.0f) + 1e-6f);
-                    const float *pr = ep.pe + (int64_t)s * 128;
+                    const float rs = 1.0f / sqrtf(ss[r] * (1.0f / 128.0f) + 1e-6f);
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         const int c = j * 32 + l32;
                         const float x = acc[i][j][r] * rs * wq[j];
-                        const float xp = __shfl_xor(x, 1);  // RoPE partner column c ^ 1
-                        const float cs_ = pr[c & ~1], sn = pr[c | 1];
+                        // RoPE partner column c ^ 1 = lane ^ 1 (DPP quad_perm [1,0,3,2])
+                        const float xp = __builtin_bit_cast(
+                            float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+                        const float cs_ = cs[r][j].x, sn = cs[r][j].y;
                         // even column: x0 c - x1 s; odd column: x0 s + x1 c (x0 is the partner)
                         const float y = (odd ? xp * sn + x * cs_ : x * cs_ - xp * sn) * osc;
                         tile[t * 128 + (c ^ ((t & 7) << 3))] = (uint16_t)(pack_bf16x2(y, 0.f) & 0xffffu);
@@ -471,16 +491,20 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
                 *(u32x4 *)(dst + ((b * H + head) * S + s) * 128 + ch * 8) = v;
             }
         } else {
-            // V^T: tile[d][t], 8-token groups XOR-swizzled by d
+            // V^T: tile[d][t], 8-token groups XOR-swizzled by d. Registers
+            // 4q .. 4q+3 hold 4 consecutive tokens (4-aligned; the swizzle
+            // only flips bits 3-6): one 8 B write each.
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const int d = j * 32 + l32;
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int t = i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                        tile[d * 128 + (t ^ ((d & 15) << 3))] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.f) & 0xffffu);
+                    for (int q = 0; q < 4; q++) {
+                        const int t = i * 32 + 8 * q + 4 * g;
+                        *(u32x2 *)(tile + d * 128 + (t ^ ((d & 15) << 3))) =
+                            u32x2{pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                                  pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])};
                     }
                 }
             __builtin_amdgcn_s_waitcnt(0xc07f);

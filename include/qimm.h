@@ -34,7 +34,9 @@ typedef enum {
     QIMM_ERR_TYPE = 3,     /* GGML type not supported for this use */
     QIMM_ERR_OOM = 4,      /* device or host allocation failed */
     QIMM_ERR_HIP = 5,      /* a HIP runtime call failed */
-    QIMM_ERR_STATE = 6     /* object used in the wrong state (e.g. missing cache) */
+    QIMM_ERR_STATE = 6,    /* object used in the wrong state (e.g. missing cache) */
+    QIMM_ERR_NOT_FOUND = 7,/* named tensor or metadata key absent */
+    QIMM_ERR_FORMAT = 8    /* file malformed or truncated (GGUF reader) */
 } qimm_status;
 
 /* GGML tensor type ids as stored in GGUF files (GGML spec; the values
@@ -137,6 +139,24 @@ int qimm_kv_store_layer(qimm_kv *kv, int64_t layer, const uint16_t *k_bhpd,
 int qimm_kv_load_layer(const qimm_kv *kv, int64_t layer, uint16_t *k_bhpd, uint16_t *v_bhpd,
                        void *stream);
 int64_t qimm_kv_prefix_len(const qimm_kv *kv);
+
+/* The host-resident cache of set_kv_cache_offload / --kv-cache-cpu
+ * (src/transformer.rs:26-41, src/main.rs:169-172): the same object, but the
+ * layers live in pinned host memory and a layer is copied to the device only
+ * while it is used. Two device slots of one layer each stage the copies.
+ * Every call that takes a qimm_kv works on both kinds; on a host cache, a call
+ * that needs a layer not staged copies it first on its own stream. */
+int qimm_kv_create_host(qimm_ctx *ctx, int64_t layers, int64_t batch, int64_t heads,
+                        int64_t prefix_len, int64_t head_dim, qimm_kv **out);
+int qimm_kv_is_host(const qimm_kv *kv);
+/* Starts copying one layer of a host cache into a device slot on `stream`
+ * (a copy stream, so that layer l+1 moves while layer l computes); the next
+ * call using that layer, on any stream, waits for the copy on the device. A
+ * slot is reused only after the kernels reading it have finished (events), so
+ * at most the layer in use and one prefetched layer are resident. No-op on a
+ * device cache. (The reference copies synchronously inside from_cache_entry,
+ * src/transformer.rs:43-45; the prefetch is this library's overlap of it.) */
+int qimm_kv_prefetch(qimm_kv *kv, int64_t layer, void *stream);
 
 /* ---------------- attention ---------------- */
 
@@ -263,6 +283,73 @@ int qimm_attention_masked(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64
 #define QIMM_BLOCK_STAGES 7
 int qimm_block_profile(qimm_block *blk, int enable);
 int qimm_block_stage_times(qimm_block *blk, float *ms_out, int n);
+
+/* ---------------- GGUF files (host only, no device needed) ---------------- */
+
+/* A memory-mapped, parsed GGUF file (format versions 2 and 3). Stands in for
+ * candle's gguf_file::Content::read + Content::tensor as used by the quantized
+ * VarBuilder in load_transformer (src/service.rs:246-258) and by
+ * load_gguf_as_safetensors (src/gguf_loader.rs:15-40). Tensor data pointers
+ * stay valid until qimm_gguf_close. */
+typedef struct qimm_gguf qimm_gguf;
+
+typedef struct {
+    const char *name;  /* NUL-terminated, owned by the file handle */
+    int ggml_type;     /* GGML type id (any; sizes known for the non-IQ types) */
+    int32_t n_dims;    /* 1..4 */
+    int64_t ne[4];     /* ne[0] innermost: in features of a weight, 1 past n_dims */
+    const void *data;  /* host pointer into the mapping; NULL if the type's size is unknown */
+    size_t nbytes;     /* 0 if the type's size is unknown */
+    uint64_t offset;   /* byte offset of the data from the start of the file */
+} qimm_gguf_tensor_info;
+
+/* Opens and validates the whole file: magic "GGUF", version 2 or 3, every
+ * metadata value, every tensor info, general.alignment (default 32), and that
+ * every tensor of known type lies inside the file at an aligned offset.
+ * QIMM_ERR_ARG: cannot open/map; QIMM_ERR_FORMAT: malformed (err gets the
+ * reason when err_len > 0). */
+int qimm_gguf_open(const char *path, qimm_gguf **out, char *err, size_t err_len);
+int qimm_gguf_close(qimm_gguf *g);
+/* Format version, tensor count, metadata count, alignment, data-section offset. */
+int qimm_gguf_header(const qimm_gguf *g, uint32_t *version, int64_t *n_tensors, int64_t *n_kv,
+                     uint32_t *alignment, uint64_t *data_offset);
+
+int qimm_gguf_tensor_at(const qimm_gguf *g, int64_t i, qimm_gguf_tensor_info *info);
+/* By exact name, else under the ComfyUI prefix "model.diffusion_model." that
+ * load_transformer strips (src/service.rs:250-256). QIMM_ERR_NOT_FOUND if absent. */
+int qimm_gguf_find(const qimm_gguf *g, const char *name, qimm_gguf_tensor_info *info);
+
+/* GGUF metadata value types (GGUF spec). */
+typedef enum {
+    QIMM_GGUF_U8 = 0, QIMM_GGUF_I8 = 1, QIMM_GGUF_U16 = 2, QIMM_GGUF_I16 = 3,
+    QIMM_GGUF_U32 = 4, QIMM_GGUF_I32 = 5, QIMM_GGUF_F32 = 6, QIMM_GGUF_BOOL = 7,
+    QIMM_GGUF_STRING = 8, QIMM_GGUF_ARRAY = 9, QIMM_GGUF_U64 = 10, QIMM_GGUF_I64 = 11,
+    QIMM_GGUF_F64 = 12
+} qimm_gguf_value_type;
+
+/* Metadata entry i: its key (NUL-terminated, owned by the handle), value type
+ * and, for arrays, the element type and count (else elem_type = -1, count 1). */
+int qimm_gguf_meta_at(const qimm_gguf *g, int64_t i, const char **key, int *type, int *elem_type,
+                      uint64_t *count);
+/* Scalar metadata by key: integers and bools widen to int64 (u64 above
+ * INT64_MAX is QIMM_ERR_TYPE), floats to double; arrays/strings are QIMM_ERR_TYPE. */
+int qimm_gguf_meta_int(const qimm_gguf *g, const char *key, int64_t *out);
+int qimm_gguf_meta_float(const qimm_gguf *g, const char *key, double *out);
+/* String metadata: pointer into the mapping plus length (not NUL-terminated). */
+int qimm_gguf_meta_string(const qimm_gguf *g, const char *key, const char **str, uint64_t *len);
+
+/* 1 if the name is one the model loads (map_gguf_name / is_mappable,
+ * src/gguf_mapping.rs:13-60, plus the fused img_mlp.gate_up.weight of
+ * src/quantized_transformer.rs:181), after stripping the ComfyUI prefix; else 0. */
+int qimm_gguf_is_known_name(const char *name);
+
+/* The tensors of transformer_blocks.{layer} as qimm_block_create takes them
+ * (host pointers into the mapping): attn.to_q/k/v/out.0, attn.norm_q/norm_k,
+ * img_mlp.gate_up when present else img_mlp.proj + img_mlp.gate_layer
+ * (src/quantized_transformer.rs:173-188), img_mlp.out. Each weight's rows =
+ * ne[1], cols = ne[0]. QIMM_ERR_NOT_FOUND names the first missing tensor. */
+int qimm_gguf_block_tensors(const qimm_gguf *g, int64_t layer, qimm_block_tensors *out, char *err,
+                            size_t err_len);
 
 #ifdef __cplusplus
 }

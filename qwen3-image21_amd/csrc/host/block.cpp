@@ -264,14 +264,20 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
     }
     STAGE_MARK(2);
     // attention over [prefix ; own]                            (:143-148)
+    const uint16_t *pk = nullptr, *pvt = nullptr;
+    if (kv) {
+        const int rc = kv_layer(kv, layer, s, &pk, &pvt);
+        if (rc) return rc;
+    }
     if (img || kvalid)
-        QIMM_HIP(ctx, qimm::launch_attention_masked(qb, kv ? kv->k + layer * kv->layer_elems() : nullptr,
-                                                    kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, kb, vt,
-                                                    seq, batch, H, seq, 1.0f, img, kvalid, att, s));
+        QIMM_HIP(ctx, qimm::launch_attention_masked(qb, pk, pvt, P, kb, vt, seq, batch, H, seq, 1.0f, img, kvalid,
+                                                    att, s));
     else
-        QIMM_HIP(ctx, qimm::launch_attention_log2(qb, kv ? kv->k + layer * kv->layer_elems() : nullptr,
-                                                  kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, kb, vt,
-                                                  seq, batch, H, seq, att, s));
+        QIMM_HIP(ctx, qimm::launch_attention_log2(qb, pk, pvt, P, kb, vt, seq, batch, H, seq, att, s));
+    if (kv) {
+        const int rc = kv_release(kv, layer, s);
+        if (rc) return rc;
+    }
     STAGE_MARK(3);
     // x1 = x + tanh(gate1) * to_out(attn)                       (:150-151, 271-273)
     qimm::EpiParams er{};
@@ -381,10 +387,14 @@ int qimm_attention(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64_t head
         P = kv->prefix;
     }
     if (P + so == 0) return set_err(ctx, QIMM_ERR_SHAPE, "attention: no keys");
-    QIMM_HIP(ctx, qimm::launch_attention(q, kv ? kv->k + layer * kv->layer_elems() : nullptr,
-                                         kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, k_own, vt_own, so,
-                                         batch, heads, sq, scale, out, (hipStream_t)stream));
-    return QIMM_OK;
+    const hipStream_t s = (hipStream_t)stream;
+    const uint16_t *pk = nullptr, *pvt = nullptr;
+    if (kv) {
+        const int rc = kv_layer(kv, layer, s, &pk, &pvt);
+        if (rc) return rc;
+    }
+    QIMM_HIP(ctx, qimm::launch_attention(q, pk, pvt, P, k_own, vt_own, so, batch, heads, sq, scale, out, s));
+    return kv ? kv_release(kv, layer, s) : QIMM_OK;
 }
 
 int qimm_attention_masked(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64_t heads, int64_t sq,
@@ -406,11 +416,16 @@ int qimm_attention_masked(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64
     if (P + so == 0) return set_err(ctx, QIMM_ERR_SHAPE, "attention: no keys");
     if (mask->image_ids && (P != 0 || so != sq))
         return set_err(ctx, QIMM_ERR_SHAPE, "attention: the block-causal mask needs no prefix and so == sq");
-    QIMM_HIP(ctx, qimm::launch_attention_masked(q, kv ? kv->k + layer * kv->layer_elems() : nullptr,
-                                                kv ? kv->vt + layer * kv->layer_elems() : nullptr, P, k_own, vt_own,
-                                                so, batch, heads, sq, scale * 1.4426950408889634f, mask->image_ids,
-                                                mask->key_valid, out, (hipStream_t)stream));
-    return QIMM_OK;
+    const hipStream_t s = (hipStream_t)stream;
+    const uint16_t *pk = nullptr, *pvt = nullptr;
+    if (kv) {
+        const int rc = kv_layer(kv, layer, s, &pk, &pvt);
+        if (rc) return rc;
+    }
+    QIMM_HIP(ctx, qimm::launch_attention_masked(q, pk, pvt, P, k_own, vt_own, so, batch, heads, sq,
+                                                scale * 1.4426950408889634f, mask->image_ids, mask->key_valid, out,
+                                                s));
+    return kv ? kv_release(kv, layer, s) : QIMM_OK;
 }
 
 }  // extern "C"

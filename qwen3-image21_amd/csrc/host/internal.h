@@ -34,8 +34,23 @@ struct qimm_weight {
 struct qimm_kv {
     qimm_ctx *ctx = nullptr;
     int64_t layers = 0, batch = 0, heads = 0, prefix = 0, head_dim = 0;
-    uint16_t *k = nullptr;   // [L][B][H][P][128]
-    uint16_t *vt = nullptr;  // [L][B][H][128][P]
+    // device cache: k [L][B][H][P][128], vt [L][B][H][128][P]; host cache: the
+    // same layout in pinned host memory, staged one layer at a time into slots
+    uint16_t *k = nullptr;
+    uint16_t *vt = nullptr;
+    bool host = false;
+    // Host cache: two device slots of one layer each. `ready` is recorded after
+    // the copy into the slot, `released` after the last kernel reading it; a
+    // copy into a slot waits for both, a reader waits for `ready`. `written` is
+    // recorded after each store into host memory; every staging copy waits on it.
+    struct Slot {
+        uint16_t *k = nullptr, *vt = nullptr;
+        int64_t layer = -1;
+        hipEvent_t ready = nullptr, released = nullptr;
+    };
+    mutable Slot slot[2];
+    mutable int next = 0;
+    hipEvent_t written = nullptr;
     int64_t layer_elems() const { return batch * heads * prefix * head_dim; }
 };
 
@@ -65,6 +80,12 @@ int upload_weight_rows(qimm_ctx *ctx, int type, int64_t rows, int64_t cols, cons
                        qimm_weight **out);
 int64_t row_bytes(int type, int64_t cols);
 int block_values(int type);
+
+// Device pointers of cache layer `layer` for kernels launched on stream s. A
+// host cache stages the layer into a slot first (or waits for a prefetch);
+// kv_release must follow the last kernel that reads the pointers.
+int kv_layer(const qimm_kv *kv, int64_t layer, hipStream_t s, const uint16_t **k, const uint16_t **vt);
+int kv_release(const qimm_kv *kv, int64_t layer, hipStream_t s);
 
 }  // namespace qimm_host
 

@@ -25,7 +25,8 @@ F32, F16, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 8, 12, 14, 30
 
 OK = 0
 STATUS = {0: "QIMM_OK", 1: "QIMM_ERR_ARG", 2: "QIMM_ERR_SHAPE", 3: "QIMM_ERR_TYPE",
-          4: "QIMM_ERR_OOM", 5: "QIMM_ERR_HIP", 6: "QIMM_ERR_STATE"}
+          4: "QIMM_ERR_OOM", 5: "QIMM_ERR_HIP", 6: "QIMM_ERR_STATE", 7: "QIMM_ERR_NOT_FOUND",
+          8: "QIMM_ERR_FORMAT"}
 
 # Every symbol include/qimm.h declares: (name, restype, argtypes)
 _vp, _i64, _i32, _f32 = C.c_void_p, C.c_int64, C.c_int, C.c_float
@@ -53,6 +54,9 @@ SIGNATURES = [
     ("qimm_kv_store_layer", _i32, [_vp, _i64, _vp, _vp, _vp]),
     ("qimm_kv_load_layer", _i32, [_vp, _i64, _vp, _vp, _vp]),
     ("qimm_kv_prefix_len", _i64, [_vp]),
+    ("qimm_kv_create_host", _i32, [_vp, _i64, _i64, _i64, _i64, _i64, C.POINTER(_vp)]),
+    ("qimm_kv_is_host", _i32, [_vp]),
+    ("qimm_kv_prefetch", _i32, [_vp, _i64, _vp]),
     ("qimm_qk_norm_rope", _i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     ("qimm_v_transpose", _i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     ("qimm_attention", _i32, [_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _f32, _vp, _vp]),
@@ -64,6 +68,19 @@ SIGNATURES = [
                                          _vp]),
     ("qimm_block_profile", _i32, [_vp, _i32]),
     ("qimm_block_stage_times", _i32, [_vp, C.POINTER(C.c_float), _i32]),
+    ("qimm_gguf_open", _i32, [C.c_char_p, C.POINTER(_vp), C.c_char_p, C.c_size_t]),
+    ("qimm_gguf_close", _i32, [_vp]),
+    ("qimm_gguf_header", _i32, [_vp, C.POINTER(C.c_uint32), C.POINTER(_i64), C.POINTER(_i64),
+                                C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]),
+    ("qimm_gguf_tensor_at", _i32, [_vp, _i64, _vp]),
+    ("qimm_gguf_find", _i32, [_vp, C.c_char_p, _vp]),
+    ("qimm_gguf_meta_at", _i32, [_vp, _i64, C.POINTER(C.c_char_p), C.POINTER(_i32), C.POINTER(_i32),
+                                 C.POINTER(C.c_uint64)]),
+    ("qimm_gguf_meta_int", _i32, [_vp, C.c_char_p, C.POINTER(_i64)]),
+    ("qimm_gguf_meta_float", _i32, [_vp, C.c_char_p, C.POINTER(C.c_double)]),
+    ("qimm_gguf_meta_string", _i32, [_vp, C.c_char_p, C.POINTER(_vp), C.POINTER(C.c_uint64)]),
+    ("qimm_gguf_is_known_name", _i32, [C.c_char_p]),
+    ("qimm_gguf_block_tensors", _i32, [_vp, _i64, _vp, C.c_char_p, C.c_size_t]),
 ]
 BLOCK_STAGES = ("norm1", "qkv", "attention", "out_proj", "norm2", "gate_up", "down")
 
@@ -88,8 +105,16 @@ class AttnMask(C.Structure):
     _fields_ = [("image_ids", _vp), ("key_valid", _vp)]
 
 
+class GgufTensorInfo(C.Structure):
+    """qimm_gguf_tensor_info."""
+    _fields_ = [("name", C.c_char_p), ("ggml_type", _i32), ("n_dims", C.c_int32), ("ne", _i64 * 4),
+                ("data", _vp), ("nbytes", C.c_size_t), ("offset", C.c_uint64)]
+
+
 class QimmError(RuntimeError):
-    pass
+    def __init__(self, msg, status=None):
+        super().__init__(msg)
+        self.status = status
 
 
 _lib = None
@@ -167,6 +192,14 @@ class Context:
                    "qimm_kv_create")
         return KvCache(self, h, layers, batch, heads, prefix_len)
 
+    def kv_create_host(self, layers: int, batch: int, heads: int, prefix_len: int,
+                       head_dim: int = 128) -> "KvCache":
+        """The host-resident cache (pinned host memory, two device staging slots)."""
+        h = C.c_void_p()
+        self.check(self.lib.qimm_kv_create_host(self.h, layers, batch, heads, prefix_len, head_dim, C.byref(h)),
+                   "qimm_kv_create_host")
+        return KvCache(self, h, layers, batch, heads, prefix_len)
+
     # -- attention --
     def qk_norm_rope(self, x_dev, batch, seq, heads, norm_w_dev, pe_dev, out_dev, stream=0):
         self.check(self.lib.qimm_qk_norm_rope(self.h, x_dev, batch, seq, heads, norm_w_dev, pe_dev, out_dev,
@@ -217,6 +250,13 @@ class KvCache:
 
     def load(self, layer, k_dev, v_dev, stream=0):
         self.ctx.check(self.ctx.lib.qimm_kv_load_layer(self.h, layer, k_dev, v_dev, stream), "qimm_kv_load_layer")
+
+    def prefetch(self, layer, stream=0):
+        self.ctx.check(self.ctx.lib.qimm_kv_prefetch(self.h, layer, stream), "qimm_kv_prefetch")
+
+    @property
+    def is_host(self) -> bool:
+        return bool(self.ctx.lib.qimm_kv_is_host(self.h))
 
     def free(self):
         if self.h:
@@ -301,3 +341,101 @@ def rope_table(shapes, image_mask, axes=(16, 56, 56), theta=10000.0):
     if rc != OK:
         raise QimmError(f"qimm_rope_table -> {status_name(rc)}")
     return pe
+
+
+class GGUF:
+    """A GGUF v2/v3 file opened through the library's reader (qimm_gguf_*):
+    memory-mapped, validated at open, tensor data exposed as host pointers."""
+
+    def __init__(self, path: str):
+        self.lib = load()
+        h = C.c_void_p()
+        err = C.create_string_buffer(512)
+        rc = self.lib.qimm_gguf_open(path.encode(), C.byref(h), err, len(err))
+        if rc != OK:
+            raise QimmError(f"qimm_gguf_open({path}) -> {status_name(rc)}: {err.value.decode()}", rc)
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.qimm_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def header(self) -> dict:
+        v, a = C.c_uint32(), C.c_uint32()
+        nt, nkv, off = C.c_int64(), C.c_int64(), C.c_uint64()
+        self._ok(self.lib.qimm_gguf_header(self.h, C.byref(v), C.byref(nt), C.byref(nkv), C.byref(a), C.byref(off)),
+                 "qimm_gguf_header")
+        return {"version": v.value, "n_tensors": nt.value, "n_kv": nkv.value, "alignment": a.value,
+                "data_offset": off.value}
+
+    @staticmethod
+    def _info(ti: GgufTensorInfo) -> dict:
+        raw = C.string_at(ti.data, ti.nbytes) if ti.data else None
+        return {"name": ti.name.decode(), "ggml_type": ti.ggml_type, "ne": tuple(ti.ne[:ti.n_dims]),
+                "offset": ti.offset, "nbytes": ti.nbytes, "data": raw, "ptr": ti.data}
+
+    def tensors(self) -> list:
+        out = []
+        for i in range(self.header()["n_tensors"]):
+            ti = GgufTensorInfo()
+            self._ok(self.lib.qimm_gguf_tensor_at(self.h, i, C.byref(ti)), "qimm_gguf_tensor_at")
+            out.append(self._info(ti))
+        return out
+
+    def find(self, name: str):
+        ti = GgufTensorInfo()
+        rc = self.lib.qimm_gguf_find(self.h, name.encode(), C.byref(ti))
+        if rc == 7:
+            return None
+        self._ok(rc, f"qimm_gguf_find({name})")
+        return self._info(ti)
+
+    def metadata(self) -> list:
+        """[(key, value_type, element_type, count)] in file order."""
+        out = []
+        for i in range(self.header()["n_kv"]):
+            k, t, et, n = C.c_char_p(), C.c_int(), C.c_int(), C.c_uint64()
+            self._ok(self.lib.qimm_gguf_meta_at(self.h, i, C.byref(k), C.byref(t), C.byref(et), C.byref(n)),
+                     "qimm_gguf_meta_at")
+            out.append((k.value.decode(), t.value, et.value, n.value))
+        return out
+
+    def meta_int(self, key: str) -> int:
+        v = C.c_int64()
+        self._ok(self.lib.qimm_gguf_meta_int(self.h, key.encode(), C.byref(v)), f"qimm_gguf_meta_int({key})")
+        return v.value
+
+    def meta_float(self, key: str) -> float:
+        v = C.c_double()
+        self._ok(self.lib.qimm_gguf_meta_float(self.h, key.encode(), C.byref(v)), f"qimm_gguf_meta_float({key})")
+        return v.value
+
+    def meta_string(self, key: str) -> str:
+        p, n = C.c_void_p(), C.c_uint64()
+        self._ok(self.lib.qimm_gguf_meta_string(self.h, key.encode(), C.byref(p), C.byref(n)),
+                 f"qimm_gguf_meta_string({key})")
+        return C.string_at(p, n.value).decode()
+
+    def block_tensors(self, layer: int) -> BlockTensors:
+        """transformer_blocks.{layer} for Context.block_create; pointers stay
+        valid while this file is open."""
+        T = BlockTensors()
+        err = C.create_string_buffer(512)
+        rc = self.lib.qimm_gguf_block_tensors(self.h, layer, C.byref(T), err, len(err))
+        self._ok(rc, f"qimm_gguf_block_tensors({layer})", err.value.decode())
+        return T
+
+    def _ok(self, rc, what, detail=""):
+        if rc != OK:
+            raise QimmError(f"{what} -> {status_name(rc)} {detail}".rstrip(), rc)
+
+
+def gguf_is_known_name(name: str) -> bool:
+    return bool(load().qimm_gguf_is_known_name(name.encode()))

@@ -284,6 +284,88 @@ int qimm_attention_masked(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64
 int qimm_block_profile(qimm_block *blk, int enable);
 int qimm_block_stage_times(qimm_block *blk, float *ms_out, int n);
 
+/* ---------------- the denoising step around the blocks ---------------- */
+
+/* The whole quantized transformer: the global layers around the blocks plus
+ * the caller's blocks (QwenImageTransformerQuantized, src/quantized_transformer.rs:311-331,
+ * 399-427). The global linears run in f32 over weights dequantized once at
+ * creation (exact), as the reference runs its unquantized ones in F32. */
+typedef struct qimm_model qimm_model;
+
+typedef struct {
+    int64_t in_channels; /* latent channels (Config::in_channels = 64, src/transformer.rs:67) */
+    int64_t joint_dim;   /* txt_in input width (Config::joint_attention_dim); 0 = no txt_in */
+    int64_t hidden;      /* must equal the blocks' hidden */
+    int64_t layers;      /* number of blocks */
+} qimm_model_config;
+
+/* Global tensors, each [out, in] as in GGUF (rows = out, cols = in):
+ * img_in [hidden, in_channels]; time_text_embed.timestep_embedder.linear_1
+ * [hidden, 256] and linear_2 [hidden, hidden]; modulation.1 [4 hidden, hidden];
+ * norm_out.linear [hidden, hidden]; proj_out [in_channels, hidden];
+ * txt_in.text_norm [joint_dim] as stored (scale - 1, src/quantized_transformer.rs:65-68),
+ * txt_in.in_layer [hidden, joint_dim], txt_in.out_layer [hidden, hidden]
+ * (the txt_in three may be absent: data NULL). Types F32, F16, BF16, Q8_0,
+ * Q4_K, Q6_K. */
+typedef struct {
+    qimm_tensor img_in, t_linear_1, t_linear_2, modulation, norm_out, proj_out;
+    qimm_tensor txt_norm, txt_in, txt_out;
+} qimm_model_tensors;
+
+/* QwenImageTransformerQuantized::new_with_dtype (src/quantized_transformer.rs:399-427).
+ * blocks: cfg->layers blocks made by qimm_block_create, not owned; they must
+ * outlive the model. */
+int qimm_model_create(qimm_ctx *ctx, const qimm_model_config *cfg, const qimm_model_tensors *t,
+                      qimm_block *const *blocks, qimm_model **out);
+int qimm_model_destroy(qimm_model *m);
+
+/* timestep_embedding(t, 256) (src/scheduler.rs:101-126): cos | sin of
+ * 1000 t exp(-ln(1e4) i / 128), i < 128, for batch timesteps t (host),
+ * written as f32 [batch][256] to out (device). */
+int qimm_timestep_embedding(qimm_ctx *ctx, const float *t, int64_t batch, float *out, void *stream);
+
+/* The cached step of forward_conditioned (src/quantized_transformer.rs:471-551
+ * with a filled prefix cache): t_emb = linear_2(silu(linear_1(t_sin))),
+ * modulation = modulation.1(silu(t_emb)), h = img_in(latents), the blocks over
+ * [prefix ; h] (qimm_block_forward, or the key-validity form when key_valid is
+ * given), pred = proj_out(LayerNorm(h) * (1 + norm_out.linear(silu(t_emb)))).
+ * latents, pred: [batch, seq, in_channels] f32 (device); t_sin [batch, 256]
+ * f32 from qimm_timestep_embedding; pe [seq, 128] f32 (the target rows of the
+ * joint table); kv: the prefix cache (or NULL without prefix); key_valid
+ * uint8 [batch][P + seq] or NULL. */
+int qimm_model_forward(qimm_model *m, const float *latents, int64_t batch, int64_t seq, const float *t_sin,
+                       const float *pe, const qimm_kv *kv, const uint8_t *key_valid, float *pred, void *stream);
+
+/* prefix_kv (src/quantized_transformer.rs:359-392): runs the prefix through
+ * every block under the t = 0 modulation (zero_modulation, :334-343) and the
+ * block-causal mask, storing each layer's k, v into kv.
+ * txt [batch, text_len, joint_dim] f32 (before txt_in); cond [batch,
+ * cond_len, in_channels] f32 condition latents (before img_in) or NULL;
+ * pieces: npieces (kind, start, len) triples in layout order, kind 0 = text
+ * rows, 1 = condition rows (JointLayout::assemble, src/joint_layout.rs:112-126;
+ * qimm_joint_layout_pieces); image_ids int32 [P] and key_valid uint8
+ * [batch][P] (or NULL) on the device; pe [P, 128] f32. P = kv's prefix_len. */
+int qimm_model_prefix_fill(qimm_model *m, const float *txt, int64_t text_len, const float *cond, int64_t cond_len,
+                           int64_t batch, const int64_t *pieces, int64_t npieces, const int32_t *image_ids,
+                           const uint8_t *key_valid, const float *pe, qimm_kv *kv, void *stream);
+
+/* The prefix pieces of JointLayout::new (src/joint_layout.rs:52-103): writes
+ * (kind, start, len) triples, kind 0 = Text { start, len } over prompt rows,
+ * 1 = Condition { index } as (1, cond_offsets[index], h*w); the target piece
+ * is not listed. cap = capacity in triples. */
+int qimm_joint_layout_pieces(int64_t text_len, const uint8_t *text_image_mask, const int64_t *cond_shapes,
+                             int64_t ncond, int64_t *pieces, int64_t cap, int64_t *npieces);
+
+/* FlowMatchEuler::new (src/scheduler.rs:24-37): the shifted sigma schedule,
+ * f32 arithmetic in the reference's order; sigmas gets steps values. */
+int qimm_flow_match_sigmas(int64_t steps, int64_t image_seq_len, float *sigmas);
+/* FlowMatchEuler::step (src/scheduler.rs:54-66): latents += dt * pred over n
+ * f32 values, dt = sigmas[i+1] - sigmas[i] (or -sigmas[i] at the last step). */
+int qimm_euler_step(qimm_ctx *ctx, float *latents, const float *pred, int64_t n, float dt, void *stream);
+/* Classifier-free guidance (src/pipeline.rs:180-186): out = neg + scale * (cond - neg). */
+int qimm_cfg_combine(qimm_ctx *ctx, const float *cond, const float *neg, int64_t n, float scale, float *out,
+                     void *stream);
+
 /* ---------------- GGUF files (host only, no device needed) ---------------- */
 
 /* A memory-mapped, parsed GGUF file (format versions 2 and 3). Stands in for
@@ -350,6 +432,11 @@ int qimm_gguf_is_known_name(const char *name);
  * ne[1], cols = ne[0]. QIMM_ERR_NOT_FOUND names the first missing tensor. */
 int qimm_gguf_block_tensors(const qimm_gguf *g, int64_t layer, qimm_block_tensors *out, char *err,
                             size_t err_len);
+/* The global tensors for qimm_model_create (QwenImageTransformerQuantized::new_with_dtype,
+ * src/quantized_transformer.rs:399-427): img_in, time_text_embed.timestep_embedder.linear_1/2,
+ * modulation.1, norm_out.linear, proj_out, and txt_in.text_norm / in_layer /
+ * out_layer when txt_in.in_layer.weight exists (:406-411). */
+int qimm_gguf_model_tensors(const qimm_gguf *g, qimm_model_tensors *out, char *err, size_t err_len);
 
 #ifdef __cplusplus
 }

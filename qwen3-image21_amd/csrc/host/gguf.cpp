@@ -501,4 +501,43 @@ int qimm_gguf_block_tensors(const qimm_gguf *g, int64_t layer, qimm_block_tensor
     return get("img_mlp.out.weight", out->mlp_out, true);
 }
 
+int qimm_gguf_model_tensors(const qimm_gguf *g, qimm_model_tensors *out, char *err, size_t err_len) {
+    if (!g || !out) {
+        put_err(err, err_len, "null argument");
+        return QIMM_ERR_ARG;
+    }
+    memset(out, 0, sizeof(*out));
+    auto get = [&](const char *name, qimm_tensor &dst, bool required) -> int {
+        const Tensor *t = g->find_tensor(name);
+        if (!t) {
+            if (!required) return QIMM_OK;
+            put_err(err, err_len, std::string("missing tensor ") + name);
+            return QIMM_ERR_NOT_FOUND;
+        }
+        if (!t->nbytes) {
+            put_err(err, err_len, std::string(name) + ": GGML type " + std::to_string(t->type) + " has no known layout");
+            return QIMM_ERR_TYPE;
+        }
+        dst.ggml_type = t->type;
+        dst.rows = t->ne[1] * t->ne[2] * t->ne[3];
+        dst.cols = t->ne[0];
+        dst.data = g->map + t->abs_off;
+        dst.nbytes = (size_t)t->nbytes;
+        return QIMM_OK;
+    };
+    int st;
+    if ((st = get("img_in.weight", out->img_in, true))) return st;
+    if ((st = get("time_text_embed.timestep_embedder.linear_1.weight", out->t_linear_1, true))) return st;
+    if ((st = get("time_text_embed.timestep_embedder.linear_2.weight", out->t_linear_2, true))) return st;
+    if ((st = get("modulation.1.weight", out->modulation, true))) return st;
+    if ((st = get("norm_out.linear.weight", out->norm_out, true))) return st;
+    if ((st = get("proj_out.weight", out->proj_out, true))) return st;
+    if (g->find_tensor("txt_in.in_layer.weight")) {  // src/quantized_transformer.rs:406-411
+        if ((st = get("txt_in.text_norm.weight", out->txt_norm, true))) return st;
+        if ((st = get("txt_in.in_layer.weight", out->txt_in, true))) return st;
+        if ((st = get("txt_in.out_layer.weight", out->txt_out, true))) return st;
+    }
+    return QIMM_OK;
+}
+
 }  // extern "C"

@@ -118,4 +118,20 @@ hipError_t launch_qk_prep(const float *x, int64_t b, int64_t s, int64_t h, const
 hipError_t launch_transpose_sd(const uint16_t *in, int64_t bh, int64_t s, uint16_t *out,
                                int inverse, hipStream_t stream);
 
+// ---- the denoising step around the blocks (step.hip), all f32 ----
+enum : int { ACT_NONE = 0, ACT_SILU = 1, ACT_GELU_TANH = 2 };
+// y[m][n] (row stride ldy) = sum_k act(x[m][k]) * w[n][k]; x row stride ldx, w [n][k] dense.
+hipError_t launch_linear_f32(const float *x, int64_t ldx, const float *w, int64_t m, int64_t n, int64_t k,
+                             int act_in, float *y, int64_t ldy, hipStream_t stream);
+// y = x / sqrt(mean(x^2) + eps) * w, per row of d values
+hipError_t launch_rows_rmsnorm(const float *x, const float *w, int64_t rows, int64_t d, float eps, float *y,
+                               hipStream_t stream);
+// y = LayerNorm(x) * (1 + scale[row / rows_per][:]), per row of d values
+hipError_t launch_rows_ln_scale(const float *x, const float *scale, int64_t rows, int64_t d, int64_t rows_per,
+                                float eps, float *y, hipStream_t stream);
+// x += dt * v
+hipError_t launch_euler(float *x, const float *v, int64_t n, float dt, hipStream_t stream);
+// out = neg + scale * (cond - neg)
+hipError_t launch_cfg(const float *cond, const float *neg, int64_t n, float scale, float *out, hipStream_t stream);
+
 }  // namespace qimm

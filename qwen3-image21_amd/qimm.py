@@ -68,6 +68,15 @@ SIGNATURES = [
                                          _vp]),
     ("qimm_block_profile", _i32, [_vp, _i32]),
     ("qimm_block_stage_times", _i32, [_vp, C.POINTER(C.c_float), _i32]),
+    ("qimm_model_create", _i32, [_vp, _vp, _vp, _vp, C.POINTER(_vp)]),
+    ("qimm_model_destroy", _i32, [_vp]),
+    ("qimm_timestep_embedding", _i32, [_vp, _vp, _i64, _vp, _vp]),
+    ("qimm_model_forward", _i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
+    ("qimm_model_prefix_fill", _i32, [_vp, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp]),
+    ("qimm_joint_layout_pieces", _i32, [_i64, _vp, _vp, _i64, _vp, _i64, C.POINTER(_i64)]),
+    ("qimm_flow_match_sigmas", _i32, [_i64, _i64, _vp]),
+    ("qimm_euler_step", _i32, [_vp, _vp, _vp, _i64, _f32, _vp]),
+    ("qimm_cfg_combine", _i32, [_vp, _vp, _vp, _i64, _f32, _vp, _vp]),
     ("qimm_gguf_open", _i32, [C.c_char_p, C.POINTER(_vp), C.c_char_p, C.c_size_t]),
     ("qimm_gguf_close", _i32, [_vp]),
     ("qimm_gguf_header", _i32, [_vp, C.POINTER(C.c_uint32), C.POINTER(_i64), C.POINTER(_i64),
@@ -81,6 +90,7 @@ SIGNATURES = [
     ("qimm_gguf_meta_string", _i32, [_vp, C.c_char_p, C.POINTER(_vp), C.POINTER(C.c_uint64)]),
     ("qimm_gguf_is_known_name", _i32, [C.c_char_p]),
     ("qimm_gguf_block_tensors", _i32, [_vp, _i64, _vp, C.c_char_p, C.c_size_t]),
+    ("qimm_gguf_model_tensors", _i32, [_vp, _vp, C.c_char_p, C.c_size_t]),
 ]
 BLOCK_STAGES = ("norm1", "qkv", "attention", "out_proj", "norm2", "gate_up", "down")
 
@@ -98,6 +108,15 @@ class Tensor(C.Structure):
 class BlockTensors(C.Structure):
     _fields_ = [(n, Tensor) for n in ("to_q", "to_k", "to_v", "to_out", "norm_q", "norm_k",
                                       "gate_up", "proj", "gate_layer", "mlp_out")]
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [("in_channels", _i64), ("joint_dim", _i64), ("hidden", _i64), ("layers", _i64)]
+
+
+class ModelTensors(C.Structure):
+    _fields_ = [(n, Tensor) for n in ("img_in", "t_linear_1", "t_linear_2", "modulation", "norm_out", "proj_out",
+                                      "txt_norm", "txt_in", "txt_out")]
 
 
 class AttnMask(C.Structure):
@@ -191,6 +210,26 @@ class Context:
         self.check(self.lib.qimm_kv_create(self.h, layers, batch, heads, prefix_len, head_dim, C.byref(h)),
                    "qimm_kv_create")
         return KvCache(self, h, layers, batch, heads, prefix_len)
+
+    # -- the denoising step around the blocks --
+    def model_create(self, cfg: ModelConfig, tensors: ModelTensors, blocks) -> "Model":
+        arr = (C.c_void_p * max(1, len(blocks)))(*[b.h for b in blocks])
+        h = C.c_void_p()
+        self.check(self.lib.qimm_model_create(self.h, C.byref(cfg), C.byref(tensors), arr, C.byref(h)),
+                   "qimm_model_create")
+        return Model(self, h, list(blocks))
+
+    def timestep_embedding(self, t, out_dev, stream=0):
+        """t: sequence of floats (one per batch row) -> out_dev f32 [len(t), 256]."""
+        arr = (C.c_float * len(t))(*t)
+        self.check(self.lib.qimm_timestep_embedding(self.h, arr, len(t), out_dev, stream), "qimm_timestep_embedding")
+
+    def euler_step(self, latents_dev, pred_dev, n, dt, stream=0):
+        self.check(self.lib.qimm_euler_step(self.h, latents_dev, pred_dev, n, dt, stream), "qimm_euler_step")
+
+    def cfg_combine(self, cond_dev, neg_dev, n, scale, out_dev, stream=0):
+        self.check(self.lib.qimm_cfg_combine(self.h, cond_dev, neg_dev, n, scale, out_dev, stream),
+                   "qimm_cfg_combine")
 
     def kv_create_host(self, layers: int, batch: int, heads: int, prefix_len: int,
                        head_dim: int = 128) -> "KvCache":
@@ -423,6 +462,14 @@ class GGUF:
                  f"qimm_gguf_meta_string({key})")
         return C.string_at(p, n.value).decode()
 
+    def model_tensors(self) -> ModelTensors:
+        """The global tensors for Context.model_create (pointers valid while open)."""
+        T = ModelTensors()
+        err = C.create_string_buffer(512)
+        rc = self.lib.qimm_gguf_model_tensors(self.h, C.byref(T), err, len(err))
+        self._ok(rc, "qimm_gguf_model_tensors", err.value.decode())
+        return T
+
     def block_tensors(self, layer: int) -> BlockTensors:
         """transformer_blocks.{layer} for Context.block_create; pointers stay
         valid while this file is open."""
@@ -439,3 +486,52 @@ class GGUF:
 
 def gguf_is_known_name(name: str) -> bool:
     return bool(load().qimm_gguf_is_known_name(name.encode()))
+
+
+class Model:
+    """The transformer around the blocks (qimm_model)."""
+
+    def __init__(self, ctx, h, blocks):
+        self.ctx, self.h, self.blocks = ctx, h, blocks  # blocks kept alive: the model does not own them
+
+    def forward(self, latents_dev, batch, seq, t_sin_dev, pe_dev, kv, pred_dev, key_valid_dev=None, stream=0):
+        self.ctx.check(self.ctx.lib.qimm_model_forward(self.h, latents_dev, batch, seq, t_sin_dev, pe_dev,
+                                                       kv.h if kv else None, key_valid_dev, pred_dev, stream),
+                       "qimm_model_forward")
+
+    def prefix_fill(self, txt_dev, text_len, cond_dev, cond_len, batch, pieces, image_ids_dev, key_valid_dev, pe_dev,
+                    kv, stream=0):
+        flat = [v for p in pieces for v in p]
+        arr = (C.c_int64 * max(1, len(flat)))(*flat)
+        self.ctx.check(self.ctx.lib.qimm_model_prefix_fill(self.h, txt_dev, text_len, cond_dev, cond_len, batch, arr,
+                                                           len(pieces), image_ids_dev, key_valid_dev, pe_dev, kv.h,
+                                                           stream), "qimm_model_prefix_fill")
+
+    def free(self):
+        if self.h:
+            self.ctx.lib.qimm_model_destroy(self.h)
+            self.h = None
+
+
+def flow_match_sigmas(steps: int, image_seq_len: int) -> list:
+    out = (C.c_float * steps)()
+    rc = load().qimm_flow_match_sigmas(steps, image_seq_len, out)
+    if rc != OK:
+        raise QimmError(f"qimm_flow_match_sigmas -> {status_name(rc)}", rc)
+    return list(out)
+
+
+def joint_layout_pieces(text_len: int, text_image_mask=None, cond_shapes=()) -> list:
+    """(kind, start, len) triples of the prefix: 0 = prompt rows, 1 = condition rows."""
+    mask = None
+    if text_image_mask is not None:
+        mask = (C.c_uint8 * text_len)(*[1 if v else 0 for v in text_image_mask])
+    flat = [v for hw in cond_shapes for v in hw]
+    shp = (C.c_int64 * max(1, len(flat)))(*flat)
+    cap = text_len + len(cond_shapes) + 1
+    out = (C.c_int64 * (3 * cap))()
+    n = C.c_int64()
+    rc = load().qimm_joint_layout_pieces(text_len, mask, shp if flat else None, len(cond_shapes), out, cap, C.byref(n))
+    if rc != OK:
+        raise QimmError(f"qimm_joint_layout_pieces -> {status_name(rc)}", rc)
+    return [tuple(out[3 * i:3 * i + 3]) for i in range(n.value)]

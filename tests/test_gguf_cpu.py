@@ -147,7 +147,8 @@ def test_tensor_past_end_rejected(tmp_path):
     assert e.value.status == 1
 
 
-def random_file(path, seed, alignment=32, prefix="", fused=True, layers=2, hidden=256, mlp=512):
+def random_file(path, seed, alignment=32, prefix="", fused=True, layers=2, hidden=256, mlp=512, globals_=False,
+                txt_in=False):
     rng = np.random.default_rng(seed)
     meta = [("general.architecture", G.STRING, "qwen_image"),
             ("general.name", G.STRING, "synthetic é"),
@@ -175,8 +176,23 @@ def random_file(path, seed, alignment=32, prefix="", fused=True, layers=2, hidde
             for sub in ("img_mlp.proj.weight", "img_mlp.gate_layer.weight"):
                 _, data, r, c = synth.weight(rng, synth.Q4_K, mlp, hidden)
                 tensors.append((pre + sub, synth.Q4_K, (c, r), data.tobytes()))
-    tensors.append((prefix + "img_in.weight", 30, (64, hidden), rng.integers(0, 1 << 16, 64 * hidden,
-                                                                             dtype=np.uint16).tobytes()))
+    _, data, r, c = synth.weight(rng, synth.BF16, hidden, 64, std=0.2)  # finite bf16 values
+    tensors.append((prefix + "img_in.weight", synth.BF16, (c, r), data.tobytes()))
+    if globals_:
+        # the model's global tensors (src/gguf_mapping.rs:27-37), [out, in] as ne = (in, out)
+        for name, t, rows, cols in (("time_text_embed.timestep_embedder.linear_1.weight", synth.Q8_0, hidden, 256),
+                                    ("time_text_embed.timestep_embedder.linear_2.weight", synth.Q4_K, hidden, hidden),
+                                    ("modulation.1.weight", synth.Q4_K, 4 * hidden, hidden),
+                                    ("norm_out.linear.weight", synth.BF16, hidden, hidden),
+                                    ("proj_out.weight", synth.Q6_K, 64, hidden)):
+            _, data, r, c = synth.weight(rng, t, rows, cols, std=0.05)
+            tensors.append((prefix + name, t, (c, r), data.tobytes()))
+        if txt_in:
+            tensors.append((prefix + "txt_in.text_norm.weight", 0, (128,),
+                            (0.1 * rng.standard_normal(128)).astype(np.float32).tobytes()))
+            for name, rows, cols in (("txt_in.in_layer.weight", hidden, 128), ("txt_in.out_layer.weight", hidden, hidden)):
+                _, data, r, c = synth.weight(rng, synth.F32, rows, cols, std=0.05)
+                tensors.append((prefix + name, 0, (c, r), data.tobytes()))
     G.write(str(path), meta, tensors, alignment=alignment)
     return meta, tensors
 
@@ -256,3 +272,33 @@ def test_round_trip_against_oracle(tmp_path, seed, alignment, prefix, fused):
 def test_name_mapping(name, known):
     assert G.is_known_name(name) == known
     assert qimm.gguf_is_known_name(name) == known
+
+
+@pytest.mark.parametrize("prefix,txt_in", [("", True), ("model.diffusion_model.", False)])
+def test_model_tensors(tmp_path, prefix, txt_in):
+    p = tmp_path / "g.gguf"
+    _, tensors = random_file(p, 9, 32, prefix, True, layers=1, globals_=True, txt_in=txt_in)
+    by = {name[len(prefix):]: (gt, ne, data) for name, gt, ne, data in tensors}
+    with qimm.GGUF(str(p)) as g:
+        T = g.model_tensors()
+        for field, name in (("img_in", "img_in.weight"),
+                            ("t_linear_1", "time_text_embed.timestep_embedder.linear_1.weight"),
+                            ("t_linear_2", "time_text_embed.timestep_embedder.linear_2.weight"),
+                            ("modulation", "modulation.1.weight"), ("norm_out", "norm_out.linear.weight"),
+                            ("proj_out", "proj_out.weight"), ("txt_norm", "txt_in.text_norm.weight"),
+                            ("txt_in", "txt_in.in_layer.weight"), ("txt_out", "txt_in.out_layer.weight")):
+            ft = getattr(T, field)
+            if name not in by:
+                assert not ft.data and field.startswith("txt")
+                continue
+            gt, ne, data = by[name]
+            rows = ne[1] if len(ne) > 1 else 1
+            assert (ft.ggml_type, ft.cols, ft.rows, ft.nbytes) == (gt, ne[0], rows, len(data))
+            assert qimm.C.string_at(ft.data, ft.nbytes) == data
+    # a file without the globals names the first missing one
+    q = tmp_path / "blocks_only.gguf"
+    random_file(q, 10, layers=1)
+    with qimm.GGUF(str(q)) as g:
+        with pytest.raises(qimm.QimmError) as e:
+            g.model_tensors()
+        assert e.value.status == 7 and "time_text_embed.timestep_embedder.linear_1.weight" in str(e.value)

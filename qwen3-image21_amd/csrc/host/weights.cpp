@@ -101,10 +101,20 @@ int upload_weight_rows(qimm_ctx *ctx, int type, int64_t rows, int64_t cols, cons
                     memcpy(&main_bytes[(size_t)((((r / 16) * sbs + sb) * 16 + r % 16) * 144)], src + r * rb + sb * 144,
                            144);
         } else if (type == QIMM_TYPE_Q6_K) {
+            // 210 B blocks padded to 224 B (16 B aligned), 16-row groups
+            // interleaved per super-block like Q4_K, so a wave's rows load from
+            // one contiguous run
             fmt = qimm::WF_Q6_K;
-            const int64_t nb = rows * (cols / 256);
-            main_bytes.assign((size_t)nb * 224, 0);
-            for (int64_t b = 0; b < nb; b++) memcpy(&main_bytes[(size_t)b * 224], src + b * 210, 210);
+            if (rows % 16) {
+                delete w;
+                return set_err(ctx, QIMM_ERR_SHAPE, "weight: Q6_K tensors need rows % 16 == 0");
+            }
+            const int64_t sbs = cols / 256;
+            main_bytes.assign((size_t)(rows * sbs) * 224, 0);
+            for (int64_t r = 0; r < rows; r++)
+                for (int64_t sb = 0; sb < sbs; sb++)
+                    memcpy(&main_bytes[(size_t)((((r / 16) * sbs + sb) * 16 + r % 16) * 224)], src + r * rb + sb * 210,
+                           210);
         } else {
             // Float-stored weights feed the bf16 MFMA path: BF16 as is, F16 and
             // F32 rounded to bf16 (nearest even).

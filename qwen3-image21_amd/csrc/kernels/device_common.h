@@ -44,6 +44,11 @@ __device__ __forceinline__ const uint8_t *q4k_block(const uint8_t *q, int64_t n,
     return q + (((n >> 4) * sbs + sb) * 16 + (n & 15)) * 144;
 }
 
+// Q6_K device layout, the same interleave with blocks padded to 224 B.
+__device__ __forceinline__ const uint8_t *q6k_block(const uint8_t *q, int64_t n, int64_t sb, int64_t sbs) {
+    return q + (((n >> 4) * sbs + sb) * 16 + (n & 15)) * 224;
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
     return __uint_as_float(b << 16);
 }

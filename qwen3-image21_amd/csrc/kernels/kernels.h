@@ -11,7 +11,8 @@ namespace qimm {
 //   WF_Q8_0  codes int8 [N][K] + f16 scales [N][K/32]      (34 B blocks split)
 //   WF_Q4_K  GGUF 144 B blocks, 16-row groups interleaved per super-block:
 //            [N/16][K/256][16] x 144 B (q4k_block in device_common.h)
-//   WF_Q6_K  GGUF blocks re-strided to 224 B, [N][K/256]      (210 B + 14 B pad)
+//   WF_Q6_K  GGUF blocks padded to 224 B, the same 16-row interleave:
+//            [N/16][K/256][16] x 224 B (q6k_block)
 //   WF_BF16  bf16 [N][K]
 enum : int { WF_Q8_0 = 0, WF_Q4_K = 1, WF_Q6_K = 2, WF_BF16 = 3 };
 

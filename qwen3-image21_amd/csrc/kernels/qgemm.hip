@@ -77,7 +77,7 @@ __device__ __forceinline__ void load_w(const GemmWeight &w, int64_t n, int64_t k
         r.v[0] = *(const u32x4 *)blk;
         r.v[1] = *(const u32x4 *)(blk + 16 + 32 * c + 16 * h);
     } else if constexpr (FMT == WF_Q6_K) {
-        const uint8_t *blk = w.q + (n * (K / 256) + k0 / 256) * 224;
+        const uint8_t *blk = q6k_block(w.q, n, k0 / 256, K / 256);
         const int hh = (int)((k0 & 255) >> 7);
         r.v[0] = *(const u32x4 *)(blk + 64 * hh + 16 * h);
         r.v[1] = *(const u32x4 *)(blk + 64 * hh + 32 + 16 * h);

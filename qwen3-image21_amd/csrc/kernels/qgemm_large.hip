@@ -117,7 +117,7 @@ __device__ __forceinline__ void load_w(const GemmWeight &w, int64_t n, int64_t k
         r.v[1] = *(const u32x4 *)(blk + 16 + 32 * c);
         r.v[2] = *(const u32x4 *)(blk + 32 + 32 * c);
     } else if constexpr (FMT == WF_Q6_K) {
-        const uint8_t *blk = w.q + (n * (K / 256) + k0 / 256) * 224;
+        const uint8_t *blk = q6k_block(w.q, n, k0 / 256, K / 256);
         const int hh = (int)((k0 & 255) >> 7);
 #pragma unroll
         for (int i = 0; i < 4; i++) r.v[i] = *(const u32x4 *)(blk + 64 * hh + 16 * i);
@@ -163,14 +163,20 @@ __device__ __forceinline__ WScale w_scales(const WRaw &r, int64_t k0) {
         const int hh = (int)((k0 & 255) >> 7), o = (int)((k0 & 127) >> 6);
         const float d = f16_bits_to_f32(r.s);
         const int base = 8 * hh + 4 * o;
-        s.a0 = d * (float)(int8_t)byte_of(r.v[6], base + 0);
-        s.a1 = d * (float)(int8_t)byte_of(r.v[6], base + 1);
-        s.a2 = d * (float)(int8_t)byte_of(r.v[6], base + 2);
-        s.a3 = d * (float)(int8_t)byte_of(r.v[6], base + 3);
-        s.b0 = -32.f * s.a0;  // (q+32)*ds - 32*ds, exact
-        s.b1 = -32.f * s.a1;
-        s.b2 = -32.f * s.a2;
-        s.b3 = -32.f * s.a3;
+        const float d0 = d * (float)(int8_t)byte_of(r.v[6], base + 0);
+        const float d1 = d * (float)(int8_t)byte_of(r.v[6], base + 1);
+        const float d2 = d * (float)(int8_t)byte_of(r.v[6], base + 2);
+        const float d3 = d * (float)(int8_t)byte_of(r.v[6], base + 3);
+        // codes sit at f16 bits 0-5 (the subnormal q * 2^-24), so the scales carry
+        // 2^24; q*ds - 32*ds with both products exact and one rounding
+        s.a0 = d0 * 0x1p24f;
+        s.a1 = d1 * 0x1p24f;
+        s.a2 = d2 * 0x1p24f;
+        s.a3 = d3 * 0x1p24f;
+        s.b0 = -32.f * d0;
+        s.b1 = -32.f * d1;
+        s.b2 = -32.f * d2;
+        s.b3 = -32.f * d3;
     }
     return s;
 }
@@ -210,7 +216,12 @@ __device__ __forceinline__ u32x4 w_chunk(const WRaw &r, const WScale &s, int j, 
         const int si = 2 * rl + (l0 >> 4);
         const float a = si == 0 ? s.a0 : (si == 1 ? s.a1 : (si == 2 ? s.a2 : s.a3));
         const float b = si == 0 ? s.b0 : (si == 1 ? s.b1 : (si == 2 ? s.b2 : s.b3));
-        return cvt8(c0, c1, a, b);
+        // the 6-bit codes fill whole bytes (<= 63): the halves of (c & 0x00FF00FF)
+        // hold bytes 0 and 2, those of perm(c) bytes 1 and 3
+        const uint32_t p0 = c0 & 0x00FF00FFu, p1 = __builtin_amdgcn_perm(0u, c0, 0x0C030C01u);
+        const uint32_t p2 = c1 & 0x00FF00FFu, p3 = __builtin_amdgcn_perm(0u, c1, 0x0C030C01u);
+        return u32x4{pack_bf16x2(mix_lo(p0, a, b), mix_lo(p1, a, b)), pack_bf16x2(mix_hi(p0, a, b), mix_hi(p1, a, b)),
+                     pack_bf16x2(mix_lo(p2, a, b), mix_lo(p3, a, b)), pack_bf16x2(mix_hi(p2, a, b), mix_hi(p3, a, b))};
     } else {
         return r.v[j];
     }

@@ -73,7 +73,7 @@ __device__ __forceinline__ void load_step(const GemmWeight &w, int64_t n, int64_
         r.a = *(const u32x4 *)blk;
         r.c = *(const u32x2 *)(blk + 16 + 32 * c + 8 * kg);
     } else if constexpr (FMT == WF_Q6_K) {
-        const uint8_t *blk = w.q + (n * (K / 256) + k0 / 256) * 224;
+        const uint8_t *blk = q6k_block(w.q, n, k0 / 256, K / 256);
         const int hh = (int)((k0 & 255) >> 7);
         const u32x2 l0 = *(const u32x2 *)(blk + 64 * hh + 8 * kg);
         const u32x2 l1 = *(const u32x2 *)(blk + 64 * hh + 32 + 8 * kg);

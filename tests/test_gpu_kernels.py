@@ -147,6 +147,11 @@ def test_qmatmul_rejects_bad_shapes(torch_cuda, qctx):
     W.free()
     with pytest.raises(qimm.QimmError, match="QIMM_ERR_SHAPE"):
         qctx.upload(synth.Q4_K, 128, 100, b"\0" * 10)
+    # the K-quant device layouts interleave 16-row groups
+    with pytest.raises(qimm.QimmError, match="rows % 16"):
+        qctx.upload(synth.Q6_K, 24, 256, b"\0" * (24 * 210))
+    with pytest.raises(qimm.QimmError, match="rows % 16"):
+        qctx.upload(synth.Q4_K, 24, 256, b"\0" * (24 * 144))
 
 
 # ---------------------------------------------------------------- attention

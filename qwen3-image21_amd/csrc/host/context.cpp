@@ -2,6 +2,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <new>
 
 #include "internal.h"
@@ -44,6 +45,9 @@ int ensure_part_workspace(qimm_ctx *ctx, size_t bytes) {
     bytes = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
     QIMM_HIP(ctx, hipMalloc(&ctx->ws_part, bytes));
     ctx->ws_part_bytes = bytes;
+    // the arrival counters at the front of the short-M GEMM scratch start at
+    // zero; the kernels leave them zero after every call
+    QIMM_HIP(ctx, hipMemset(ctx->ws_part, 0, std::min(bytes, qimm::STREAM_COUNTER_BYTES)));
     return QIMM_OK;
 }
 

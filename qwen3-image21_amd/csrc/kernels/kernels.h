@@ -66,14 +66,17 @@ hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64
                         int epi, const EpiParams &ep, hipStream_t stream);
 bool qgemm_large_fits(const GemmWeight &w, int64_t m);
 
-// Short-M weight-streaming path (M <= 64): split-K partial sums into part
-// (qgemm_stream_workspace bytes), then a fixed-order reduction that applies
-// the epilogue.
+// Short-M weight-streaming path (M <= 64): split-K partial sums, added in a
+// fixed order by the epilogue (in the same launch for Q4_K / Q6_K at M <= 16).
+// work (qgemm_stream_workspace bytes) starts with STREAM_COUNTER_BYTES of
+// arrival counters that must be zero before the first call; every call leaves
+// them zero again. The partial sums follow.
+constexpr size_t STREAM_COUNTER_BYTES = 64 * 1024;
 bool qgemm_stream_fits(const GemmWeight &w, int64_t m);
 size_t qgemm_stream_workspace(const GemmWeight &w, int64_t m);
 int qgemm_stream_splits(const GemmWeight &w, int64_t m);
 hipError_t launch_qgemm_stream(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
-                               const EpiParams &ep, float *part, hipStream_t stream);
+                               const EpiParams &ep, float *work, hipStream_t stream);
 hipError_t launch_qgemm_large(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda,
                               int epi, const EpiParams &ep, hipStream_t stream);
 

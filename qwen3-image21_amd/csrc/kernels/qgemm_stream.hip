@@ -1,7 +1,10 @@
 // Weight-streaming dequant-GEMM for gfx950 at small token counts (M <= 64):
 // C = A (bf16, M x K) x W^T (GGUF blocks, N x K). At these sizes the time is
-// the weight bytes over HBM bandwidth, so the kernel is shaped for streaming:
+// the weight bytes over HBM bandwidth, so the kernels are shaped for streaming.
 //
+// Q4_K and Q6_K at M <= 16 with K % 1024 == 0 take the one-launch kernel in
+// namespace ws (its description is there). Everything else takes the split-K
+// kernel:
 //  - 64 weight rows x one K chunk per workgroup (4 waves x 16 rows), the K
 //    range split over workgroups so that the grid holds several workgroups per
 //    CU; partial sums go to an f32 workspace [split][M][N] and a second kernel
@@ -16,6 +19,9 @@
 //
 // Replaces candle's QMatMul::forward (src/quantized_transformer.rs:19-33) for
 // short token counts: the per-row vec-dot regime of the reference CPU path.
+#include <algorithm>
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -252,7 +258,7 @@ __global__ __launch_bounds__(256) void qgemm_stream_kernel(const uint16_t *__res
 }
 
 // ---------------------------------------------------------------------------
-// Q4_K at M <= 16: MFMA on the raw 4-bit codes, scales applied afterwards.
+// Q4_K code products (used by the M <= 16 kernel below).
 //
 // For sub-block j (32 values) of row n: w = ds_j q - dm_j with ds_j = d sc_j,
 // dm_j = dmin m_j. The B operand is the exact bf16 of 128 + q (bits 0x4300 |
@@ -264,26 +270,7 @@ __global__ __launch_bounds__(256) void qgemm_stream_kernel(const uint16_t *__res
 // A operand X from a bf16 MFMA with row-selector ones, so no per-value
 // dequantization runs at all. The result is the exact product of the bf16
 // activations and the exact Q4_K weights up to f32 summation order.
-//
-// One workgroup per CU (8 waves, 131 KB LDS holding x[16][4096] bf16): x is
-// copied to LDS once by direct loads, then each wave streams its share of the
-// (16-row group, super-block) tiles -- 2304 contiguous bytes in the device
-// layout -- through a register ring four tiles deep. Waves split the
-// workgroup's tiles evenly; the partial tile sums of a wave are reduced in LDS
-// in wave order (deterministic) and written to part[c][m][n] for the
-// split-K epilogue.
 namespace m16 {
-
-constexpr int NW = 8;       // waves per workgroup
-constexpr int KC = 4096;    // k per workgroup (x[16][KC] in LDS)
-constexpr int SBC = KC / 256;
-constexpr int ROWB = KC * 2 + 16;  // padded row: the 16 rows of a fragment read hit distinct banks
-constexpr int DEPTH = 4;    // tiles in flight per wave
-
-struct Raw {
-    u32x4 h;
-    u32x2 q[4];
-};
 
 // B fragments of 8 consecutive codes (two words): bf16 128 + q of the low and
 // of the high nibbles, by byte permutes against a 0x43 source register.
@@ -300,142 +287,6 @@ __device__ __forceinline__ void codes8(uint32_t w0, uint32_t w1, u32x4 &lo, u32x
 __device__ __forceinline__ float cvt_f16_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu)); }
 __device__ __forceinline__ float cvt_f16_hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
 
-// PER tiles per wave (compile time, so every wait on the ring is exact).
-// Grid: NG n-groups x C k-chunks; group g holds T 16-row tiles.
-template <int PER>
-__global__ __launch_bounds__(512) void q4k_m16_kernel(const uint16_t *__restrict__ A, int M, int64_t lda,
-                                                      GemmWeight w, int C, int T, float *__restrict__ part) {
-    __shared__ __attribute__((aligned(16))) uint8_t xs[16 * ROWB];
-    __shared__ __attribute__((aligned(16))) float red[NW][2][256];
-    __shared__ int tags[NW][2];
-    constexpr int D = DEPTH < PER ? DEPTH : PER;
-    constexpr int R = D + 1;  // ring slots: tile u + D is requested before tile u is computed
-    const int lane = threadIdx.x & 63, l16 = lane & 15, kg = lane >> 4;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t N = w.n, SB = w.k / 256;
-    const int NG = (int)((N / 16) / T);
-    const int ng = blockIdx.x % NG, c = blockIdx.x / NG;
-    const int64_t k0 = (int64_t)c * KC;
-    const int t0 = wave * PER;
-
-    // x chunk -> LDS by direct loads (instruction i of wave w fills 64
-    // consecutive 16 B chunks of one row); rows past M repeat row M - 1
-    {
-        constexpr int NI = 16 * KC / 8 / 64 / NW;
-#pragma unroll
-        for (int i = 0; i < NI; i++) {
-            const int q0 = (i * NW + wave) * 64;
-            const int m = q0 / (KC / 8), s0 = q0 % (KC / 8);
-            const uint16_t *src = A + (int64_t)min(m, M - 1) * lda + k0 + 8 * (s0 + lane);
-            __builtin_amdgcn_global_load_lds((const void *)src, (lds_ptr_t)(xs + m * ROWB + 16 * s0), 16, 0, 0);
-        }
-    }
-    // the wave's tiles in (n-tile, super-block) order
-    Raw ring[R];
-    const int nt0 = t0 / SBC, sb0 = t0 % SBC;
-    auto load_tile = [&](Raw &r, int u) {
-        const int ntl = nt0 + (sb0 + u) / SBC, sbl = (sb0 + u) % SBC;
-        const int64_t n = (int64_t)(ng * T + ntl) * 16 + l16;
-        const uint8_t *b = q4k_block(w.q, n, (int64_t)c * SBC + sbl, SB);
-        r.h = *(const u32x4 *)b;
-#pragma unroll
-        for (int cc = 0; cc < 4; cc++) r.q[cc] = *(const u32x2 *)(b + 16 + 32 * cc + 8 * kg);
-    };
-#pragma unroll
-    for (int u = 0; u < D; u++) load_tile(ring[u], u);
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(5 * D) : "memory");
-
-    // A operands of the sub-block sums: rows 4 s .. 4 s + 3 of ones[s] are 1
-    bf16x8 ones[4];
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-        const uint32_t v = (l16 >> 2) == s ? 0x3F803F80u : 0u;
-        ones[s] = __builtin_bit_cast(bf16x8, u32x4{v, v, v, v});
-    }
-    f32x4 accA = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
-    int seg = 0;
-    const uint8_t *xlane = xs + l16 * ROWB + 16 * kg;
-    auto tile = [&](const Raw &r, int u) {
-        const int ntl = nt0 + (sb0 + u) / SBC, sbl = (sb0 + u) % SBC;
-        const uint32_t hx = r.h[0], hy = r.h[1], hz = r.h[2], hw = r.h[3];
-        const float d = cvt_f16_lo(hx), dmin = cvt_f16_hi(hx);
-        // 6-bit scales / mins of sub-blocks 0..3 (lo) and 4..7 (hi), one per byte
-        const uint32_t sc_lo = hy & 0x3F3F3F3Fu, m_lo = hz & 0x3F3F3F3Fu;
-        const uint32_t sc_hi = (hw & 0x0F0F0F0Fu) | ((hy >> 2) & 0x30303030u);
-        const uint32_t m_hi = ((hw >> 4) & 0x0F0F0F0Fu) | ((hz >> 2) & 0x30303030u);
-        // f32-MFMA B operand: 128 ds_j + dm_j of sub-blocks kg and 4 + kg
-        const uint32_t sh = 8u * (uint32_t)kg;
-        const float cc0 = fmaf(128.f, d * (float)((sc_lo >> sh) & 0xffu), dmin * (float)((m_lo >> sh) & 0xffu));
-        const float cc1 = fmaf(128.f, d * (float)((sc_hi >> sh) & 0xffu), dmin * (float)((m_hi >> sh) & 0xffu));
-        const uint8_t *xt = xlane + sbl * 512;
-        bf16x8 af[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) af[j] = *(const bf16x8 *)(xt + 64 * j);
-        // X[m][j0 + kg] in the A layout of the f32 MFMA (all four registers)
-        f32x4 xq0 = {0.f, 0.f, 0.f, 0.f}, xq1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            xq0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], af[j], xq0, 0, 0, 0);
-            xq1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], af[4 + j], xq1, 0, 0, 0);
-        }
-        accM = __builtin_amdgcn_mfma_f32_16x16x4f32(xq0[0], cc0, accM, 0, 0, 0);
-        accM = __builtin_amdgcn_mfma_f32_16x16x4f32(xq1[0], cc1, accM, 0, 0, 0);
-        // the eight code products (independent accumulators), then the scales
-        u32x4 bq[8];
-#pragma unroll
-        for (int cc = 0; cc < 4; cc++) codes8(r.q[cc][0], r.q[cc][1], bq[2 * cc], bq[2 * cc + 1]);
-        f32x4 tv[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            tv[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[j], __builtin_bit_cast(bf16x8, bq[j]),
-                                                            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float ds = d * (float)(((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3))) & 0xffu);
-#pragma unroll
-            for (int e = 0; e < 4; e++) accA[e] = fmaf(ds, tv[j][e], accA[e]);
-        }
-        if (sbl == SBC - 1 || u == PER - 1) {  // end of this n-tile's part in the wave
-#pragma unroll
-            for (int e = 0; e < 4; e++) red[wave][seg][(4 * kg + e) * 16 + l16] = accA[e] - accM[e];
-            if (lane == 0) tags[wave][seg] = ntl;
-            seg++;
-            accA = f32x4{0.f, 0.f, 0.f, 0.f};
-            accM = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    };
-#pragma unroll
-    for (int u = 0; u < PER; u++) {
-        if (u + D < PER) load_tile(ring[(u + D) % R], u + D);
-        tile(ring[u % R], u);
-    }
-    if (lane == 0 && seg < 2) tags[wave][1] = -1;
-    __syncthreads();
-    // per-tile sums over the waves that covered it, in wave order
-    for (int p = threadIdx.x; p < T * 256; p += 64 * NW) {
-        const int tt = p >> 8, e = p & 255, m = e >> 4, nl = e & 15;
-        float s = 0.f;
-        for (int wv = 0; wv < NW; wv++)
-            for (int sg = 0; sg < 2; sg++)
-                if (tags[wv][sg] == tt) s += red[wv][sg][e];
-        if (m < M) part[((int64_t)c * M + m) * N + (int64_t)(ng * T + tt) * 16 + nl] = s;
-    }
-}
-
-// Grid of the M <= 16 kernel, or false when the shape does not tile exactly:
-// K a multiple of 4096 (C chunks), NG n-groups of T 16-row tiles with
-// NG * C equal to the CU count, each wave covering at most two n-tiles.
-bool plan(const GemmWeight &w, int64_t m, int cus, int &C, int &T, int &NG) {
-    if (w.fmt != WF_Q4_K || m < 1 || m > 16 || w.k % KC || w.n % 16 || cus <= 0) return false;
-    C = (int)(w.k / KC);
-    const int64_t tiles16 = w.n / 16;
-    if ((tiles16 * C) % cus) return false;
-    T = (int)(tiles16 * C / cus);
-    if (T < 1 || T > 8 || tiles16 % T) return false;
-    NG = (int)(tiles16 / T);
-    return (int64_t)NG * C == cus;
-}
-
 int device_cus() {
     static int cus = -1;
     if (cus < 0) {
@@ -448,26 +299,474 @@ int device_cus() {
     return cus;
 }
 
-hipError_t launch(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, float *part, int C, int T, int NG,
-                  hipStream_t stream) {
-    const dim3 grid((unsigned)(NG * C)), block(64 * NW);
-    switch (2 * T) {
-    case 2: q4k_m16_kernel<2><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
-    case 4: q4k_m16_kernel<4><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
-    case 6: q4k_m16_kernel<6><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
-    case 8: q4k_m16_kernel<8><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
-    case 10: q4k_m16_kernel<10><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
-    case 12: q4k_m16_kernel<12><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
-    case 14: q4k_m16_kernel<14><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
-    case 16: q4k_m16_kernel<16><<<grid, block, 0, stream>>>(a, (int)m, lda, w, C, T, part); break;
+}  // namespace m16
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// ---------------------------------------------------------------------------
+// M <= 16, Q4_K / Q6_K, K % 1024 == 0: one launch per product.
+//
+// Work item = (16-row weight group g, 1024-wide k chunk c) = four (group,
+// super-block) tiles, contiguous in the device layout. Workgroup b keeps chunk
+// c = b % C of the activations in LDS (x[16][1024] bf16, loaded once by direct
+// loads) and its four waves grid-stride over the groups: at step t wave v
+// takes group (t * WPC + b / C) * 4 + v. Workgroups with neighbouring ids read
+// neighbouring groups, so the bytes in flight at any time are one compact
+// window of the weight matrix (the pattern of a plain streaming read). Raw
+// tiles go straight to registers, four in flight per wave, one item ahead.
+//
+// Q4_K uses the exact code products of the M <= 16 kernel above (the
+// sub-block sums X_j of the chunk are computed once per wave). Q6_K
+// dequantizes each lane's 8 values of a step with v_fma_mix (the 6-bit codes
+// as f16 subnormals, scales carrying 2^24; RNE to bf16); a lane's 8 values of
+// a step are 8 consecutive k of one 16-value sub-block and the matching
+// activations are one 16 B LDS read, so the lane reads its ql / qh bytes as
+// 16 B pieces.
+//
+// The partial sums of an item, [16 tokens][16 rows] f32, go to
+// part[c][g]; the wave that completes the last item of an epilogue unit
+// (counter per unit, device-scope fences around it) adds the C partials of the
+// unit in chunk order -- deterministic -- applies the epilogue and resets the
+// counter for the next launch. Units: a group (F32, BF16, residual), the
+// gate and up groups of 16 hidden columns (SwiGLU), a 128-column head (q/k/v).
+namespace ws {
+
+constexpr int NW = 4;               // waves per workgroup
+constexpr int KCH = 1024;           // k per chunk
+constexpr int SBC = KCH / 256;      // tiles per item
+constexpr int XROW = KCH * 2 + 16;  // padded LDS row: a fragment's 16 rows hit distinct bank groups
+constexpr int MAX_STEPS = 4;        // items per wave (compile-time unrolled)
+
+struct Plan {
+    int C, G, WPC, steps, units, per_unit;
+};
+
+bool plan(const GemmWeight &w, int64_t m, int epi, int cus, Plan &p) {
+    if ((w.fmt != WF_Q4_K && w.fmt != WF_Q6_K) || m < 1 || m > 16 || w.k % KCH || w.n % 16 || cus <= 0)
+        return false;
+    if ((epi == EPI_SWIGLU || epi == EPI_QKV) && w.n % 128) return false;
+    p.C = (int)(w.k / KCH);
+    p.G = (int)(w.n / 16);
+    const int need = (p.G + NW - 1) / NW;  // workgroups per chunk that have work at step 0
+    p.WPC = std::max(1, std::min(3 * cus / p.C, need));
+    p.steps = (p.G + NW * p.WPC - 1) / (NW * p.WPC);
+    p.per_unit = epi == EPI_QKV ? 8 : epi == EPI_SWIGLU ? 2 : 1;
+    p.units = p.G / p.per_unit;
+    return p.steps <= MAX_STEPS && (size_t)p.units * 4 <= STREAM_COUNTER_BYTES;
+}
+
+size_t part_bytes(const GemmWeight &w) { return (size_t)(w.k / KCH) * (size_t)w.n * 64; }
+
+struct TileQ4 {
+    u32x4 h;
+    u32x2 q[4];
+};
+struct TileQ6 {
+    u32x4 l0, l1, h0, h1, sc;
+    uint32_t d;
+};
+
+template <int FMT>
+using Tile = typename std::conditional<FMT == WF_Q4_K, TileQ4, TileQ6>::type;
+
+__device__ __forceinline__ void load_tile(const GemmWeight &w, int64_t g, int64_t sb, int64_t SB, int l16, int kg,
+                                          TileQ4 &r) {
+    const uint8_t *b = w.q + ((g * SB + sb) * 16 + l16) * 144;  // q4k_block(16 g + l16, sb)
+    r.h = *(const u32x4 *)b;
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) r.q[cc] = *(const u32x2 *)(b + 16 + 32 * cc + 8 * kg);
+}
+
+// Lane kg = 2 r1 + h': ql bytes [32 r1 + 16 h', +16) of each half, qh bytes
+// [16 h', +16) of each half, the 16 scales and d (a 4-byte load: d and the
+// first two pad bytes of the 224-byte device block).
+__device__ __forceinline__ void load_tile(const GemmWeight &w, int64_t g, int64_t sb, int64_t SB, int l16, int kg,
+                                          TileQ6 &r) {
+    const uint8_t *b = w.q + ((g * SB + sb) * 16 + l16) * 224;  // q6k_block(16 g + l16, sb)
+    const int qo = 32 * (kg >> 1) + 16 * (kg & 1), ho = 128 + 16 * (kg & 1);
+    r.l0 = *(const u32x4 *)(b + qo);
+    r.l1 = *(const u32x4 *)(b + 64 + qo);
+    r.h0 = *(const u32x4 *)(b + ho);
+    r.h1 = *(const u32x4 *)(b + ho + 32);
+    r.sc = *(const u32x4 *)(b + 192);
+    r.d = *(const uint32_t *)(b + 208);  // d and two pad bytes
+}
+
+__device__ __forceinline__ float mix_lo(uint32_t x, float s, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(s), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float mix_hi(uint32_t x, float s, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(s), "v"(c));
+    return r;
+}
+
+// One Q6_K tile (16 rows x 256 k) into acc. Step s: half hh = s / 4, nibble
+// n = (s / 2) % 2, 8-byte half h8 = s % 2 of the lane's 16 B pieces; the values
+// are k = 128 hh + 32 (r1 + 2 n) + 16 h' + 8 h8 + i of the super-block, scale
+// index 8 hh + 4 n + kg.
+// The raw registers pass through an empty asm first, so no decoding of a tile
+// is hoisted to where its loads were issued (that would wait for them there).
+__device__ __forceinline__ void pin(TileQ6 &r) {
+    asm volatile("" : "+v"(r.l0), "+v"(r.l1), "+v"(r.h0), "+v"(r.h1), "+v"(r.sc), "+v"(r.d));
+}
+__device__ __forceinline__ void pin(TileQ4 &r) {
+    asm volatile("" : "+v"(r.h), "+v"(r.q[0]), "+v"(r.q[1]), "+v"(r.q[2]), "+v"(r.q[3]));
+}
+
+__device__ __forceinline__ void tile_q6(TileQ6 r, const uint8_t *xrow, int kg, f32x4 &acc) {
+    pin(r);
+    const float d = m16::cvt_f16_lo(r.d);
+    const uint32_t hsh = 2u * (uint32_t)(kg >> 1);  // qh bit pair of quadrant r1 (+4 for n = 1)
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        const int hh = s >> 2, n = (s >> 1) & 1, h8 = s & 1;
+        const u32x4 &L = hh ? r.l1 : r.l0;
+        const u32x4 &H = hh ? r.h1 : r.h0;
+        const float ds = d * (float)(int8_t)((r.sc[2 * hh + n] >> (8 * kg)) & 0xffu);
+        const float a = ds * 0x1p24f, b = -32.f * ds;
+        uint32_t c[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t lo = (L[2 * h8 + i] >> (4 * n)) & 0x0F0F0F0Fu;
+            const uint32_t hi = ((H[2 * h8 + i] >> (hsh + 4u * n)) & 0x03030303u) << 4;
+            c[i] = lo | hi;
+        }
+        const uint32_t p0 = c[0] & 0x00FF00FFu, p1 = __builtin_amdgcn_perm(0u, c[0], 0x0C030C01u);
+        const uint32_t p2 = c[1] & 0x00FF00FFu, p3 = __builtin_amdgcn_perm(0u, c[1], 0x0C030C01u);
+        const u32x4 bw = {pack_bf16x2(mix_lo(p0, a, b), mix_lo(p1, a, b)), pack_bf16x2(mix_hi(p0, a, b), mix_hi(p1, a, b)),
+                          pack_bf16x2(mix_lo(p2, a, b), mix_lo(p3, a, b)), pack_bf16x2(mix_hi(p2, a, b), mix_hi(p3, a, b))};
+        const bf16x8 av = *(const bf16x8 *)(xrow + 256 * hh + 128 * n + 32 * kg + 16 * h8);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bw), acc, 0, 0, 0);
+    }
+}
+
+// One Q4_K tile by code products (see the M <= 16 kernel): xq0 / xq1 hold the
+// sub-block sums X_kg, X_{4+kg} of token l16 for this super-block.
+__device__ __forceinline__ void tile_q4(TileQ4 r, const uint8_t *xrow, int kg, float xq0, float xq1,
+                                        f32x4 &accA, f32x4 &accM) {
+    pin(r);
+    const uint32_t hx = r.h[0], hy = r.h[1], hz = r.h[2], hw = r.h[3];
+    const float d = m16::cvt_f16_lo(hx), dmin = m16::cvt_f16_hi(hx);
+    const uint32_t sc_lo = hy & 0x3F3F3F3Fu, m_lo = hz & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (hw & 0x0F0F0F0Fu) | ((hy >> 2) & 0x30303030u);
+    const uint32_t m_hi = ((hw >> 4) & 0x0F0F0F0Fu) | ((hz >> 2) & 0x30303030u);
+    const uint32_t sh = 8u * (uint32_t)kg;
+    const float cc0 = fmaf(128.f, d * (float)((sc_lo >> sh) & 0xffu), dmin * (float)((m_lo >> sh) & 0xffu));
+    const float cc1 = fmaf(128.f, d * (float)((sc_hi >> sh) & 0xffu), dmin * (float)((m_hi >> sh) & 0xffu));
+    accM = __builtin_amdgcn_mfma_f32_16x16x4f32(xq0, cc0, accM, 0, 0, 0);
+    accM = __builtin_amdgcn_mfma_f32_16x16x4f32(xq1, cc1, accM, 0, 0, 0);
+    // two halves of four sub-blocks: four independent products in flight,
+    // scaled into accA as the next half's products run
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+        u32x4 bq[4];
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++)
+            m16::codes8(r.q[2 * hf + cc][0], r.q[2 * hf + cc][1], bq[2 * cc], bq[2 * cc + 1]);
+        f32x4 tv[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            const bf16x8 av = *(const bf16x8 *)(xrow + 64 * (4 * hf + jj) + 16 * kg);
+            tv[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bq[jj]),
+                                                             f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            const int j = 4 * hf + jj;
+            const float ds = d * (float)(((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3))) & 0xffu);
+#pragma unroll
+            for (int e = 0; e < 4; e++) accA[e] = fmaf(ds, tv[jj][e], accA[e]);
+        }
+    }
+}
+
+// Partial sums cross workgroups on different XCDs: stored and loaded with
+// system scope (sc0 sc1: written through to, and read from, memory).
+__device__ __forceinline__ void put_coherent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ float get_coherent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Sums over the C chunks of the four partial elements (g, row r, tokens
+// 4 kg + e) of a lane, in chunk order. Loads go out eight chunks at a time so
+// a batch costs one memory round trip.
+__device__ __forceinline__ f32x4 psum4(const float *part, int C, int G, int64_t g, int kg, int r) {
+    constexpr int B = 8;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    const float *base = part + g * 256 + (4 * kg) * 16 + r;
+    for (int c0 = 0; c0 < C; c0 += B) {
+        float v[B][4];
+#pragma unroll
+        for (int cc = 0; cc < B; cc++) {
+            const float *pc = base + (int64_t)min(c0 + cc, C - 1) * G * 256;
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[cc][e] = get_coherent(pc + e * 16);
+        }
+#pragma unroll
+        for (int cc = 0; cc < B; cc++)
+            if (c0 + cc < C) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) s[e] += v[cc][e];
+            }
+    }
+    return s;
+}
+
+template <int EPI>
+__device__ void unit_epilogue(const float *part, const Plan &p, int64_t unit, int M, int64_t N, const EpiParams &ep,
+                              int lane) {
+    const int l16 = lane & 15, kg = lane >> 4;
+    if constexpr (EPI == EPI_QKV) {
+        // head unit: lane j holds columns (2j, 2j+1) of the head, one token at a time
+        const int64_t g = unit * 8 + (lane >> 3);
+        const int r = 2 * (lane & 7);
+        const int64_t nb = unit * 128 + ep.n_offset;
+        const int sec = (int)(nb / ep.hidden);
+        const int64_t head = (nb % ep.hidden) / 128;
+        const int64_t S = ep.seq, H = ep.heads;
+        // four tokens per batch of loads (chunk sums in chunk order)
+        for (int m0 = 0; m0 < M; m0 += 4) {
+          float sx[4][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
+          for (int c0 = 0; c0 < p.C; c0 += 4) {
+            float v[4][4][2];
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const float *pc = part + ((int64_t)min(c0 + cc, p.C - 1) * p.G + g) * 256 + r;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int m = min(m0 + i, 15);
+                    v[cc][i][0] = get_coherent(pc + m * 16);
+                    v[cc][i][1] = get_coherent(pc + m * 16 + 1);
+                }
+            }
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++)
+                if (c0 + cc < p.C) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        sx[i][0] += v[cc][i][0];
+                        sx[i][1] += v[cc][i][1];
+                    }
+                }
+          }
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int m = m0 + i;
+            if (m >= M) break;
+            float x0 = sx[i][0], x1 = sx[i][1];
+            const int64_t b = m / S, s = m % S;
+            if (sec < 2) {
+                const float *nw = sec == 0 ? ep.norm_q : ep.norm_k;
+                const float ss = wave_sum(x0 * x0 + x1 * x1);
+                const float rs = 1.0f / sqrtf(ss * (1.0f / 128.0f) + 1e-6f);
+                x0 = x0 * rs * nw[2 * lane];
+                x1 = x1 * rs * nw[2 * lane + 1];
+                const float *pr = ep.pe + s * 128 + 2 * lane;
+                const float cs = pr[0], sn = pr[1];
+                const float osc = sec == 0 ? ep.q_scale : 1.0f;
+                const float y0 = (x0 * cs - x1 * sn) * osc, y1 = (x0 * sn + x1 * cs) * osc;
+                uint16_t *dst = sec == 0 ? ep.q : ep.k;
+                *(uint32_t *)(dst + ((b * H + head) * S + s) * 128 + 2 * lane) = pack_bf16x2(y0, y1);
+            } else {
+                const uint32_t pk = pack_bf16x2(x0, x1);
+                ep.vt[((b * H + head) * 128 + 2 * lane) * S + s] = (uint16_t)(pk & 0xffffu);
+                ep.vt[((b * H + head) * 128 + 2 * lane + 1) * S + s] = (uint16_t)(pk >> 16);
+                if (ep.v_bhsd) *(uint32_t *)(ep.v_bhsd + ((b * H + head) * S + s) * 128 + 2 * lane) = pk;
+            }
+          }
+        }
+    } else if constexpr (EPI == EPI_SWIGLU) {
+        // hidden columns 64 blk + 16 q + l16: gate group 8 blk + q, up group 8 blk + 4 + q
+        const int64_t blk = unit >> 2, q = unit & 3;
+        const int64_t gg = 8 * blk + q, gu = gg + 4;
+        const f32x4 gt = psum4(part, p.C, p.G, gg, kg, l16), up = psum4(part, p.C, p.G, gu, kg, l16);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int m = 4 * kg + e;
+            if (m < M)
+                ep.hmid[m * ep.ldh + 64 * blk + 16 * q + l16] =
+                    (uint16_t)(pack_bf16x2(silu(gt[e]) * up[e], 0.f) & 0xffffu);
+        }
+    } else {
+        const int64_t n = unit * 16 + l16;
+        const f32x4 sum = psum4(part, p.C, p.G, unit, kg, l16);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int m = 4 * kg + e;
+            if (m < M) {
+                const float v = sum[e];
+                if constexpr (EPI == EPI_F32) {
+                    ((float *)ep.out)[m * ep.ldo + n] = v;
+                } else if constexpr (EPI == EPI_BF16) {
+                    ((uint16_t *)ep.out)[m * ep.ldo + n] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
+                } else {  // EPI_RESID
+                    const float *grow = ep.gvec + (int64_t)(m / (int)ep.g_rows_per) * ep.g_stride;
+                    ep.x_out[m * N + n] = ep.x_in[m * N + n] + grow[n] * v;
+                }
+            }
+        }
+    }
+}
+
+template <int FMT, int EPI, int STEPS>
+__global__ __launch_bounds__(64 * NW) void ws_kernel(const uint16_t *__restrict__ A, int M, int64_t lda, GemmWeight w,
+                                                     float *__restrict__ part, uint32_t *__restrict__ counters, Plan p,
+                                                     EpiParams ep) {
+    __shared__ __attribute__((aligned(16))) uint8_t xs[16 * XROW];
+    const int lane = threadIdx.x & 63, l16 = lane & 15, kg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = blockIdx.x % p.C, slot = blockIdx.x / p.C;
+    const int64_t SB = w.k / 256, N = w.n;
+    const int64_t gstep = (int64_t)p.WPC * NW;
+    int64_t g = (int64_t)slot * NW + wave;
+
+    // x chunk -> LDS by direct loads: instruction i of wave v fills 64
+    // consecutive 16 B pieces of one row; rows past M repeat row M - 1
+#pragma unroll
+    for (int i = 0; i < 16 * (KCH / 8) / 64 / NW; i++) {
+        const int q0 = (i * NW + wave) * 64;
+        const int m = q0 / (KCH / 8), s0 = q0 % (KCH / 8);
+        const uint16_t *src = A + (int64_t)min(m, M - 1) * lda + (int64_t)c * KCH + 8 * (s0 + lane);
+        __builtin_amdgcn_global_load_lds((const void *)src, (lds_ptr_t)(xs + m * XROW + 16 * s0), 16, 0, 0);
+    }
+    if (g >= p.G) {  // no item for this wave: its x pieces still have to land
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        return;
+    }
+    Tile<FMT> ring[SBC];
+#pragma unroll
+    for (int t = 0; t < SBC; t++) {
+        load_tile(w, g, (int64_t)c * SBC + t, SB, l16, kg, ring[t]);
+        __builtin_amdgcn_sched_barrier(0);  // tiles issue in order: each wait covers one tile
+    }
+    // the x pieces were issued before the tiles: wait for them alone, then for
+    // every wave's pieces
+    constexpr int TL = FMT == WF_Q4_K ? 5 : 6;  // loads per tile
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(SBC * TL) : "memory");
+
+    const uint8_t *xrow = xs + l16 * XROW;
+    float xq0[SBC], xq1[SBC];
+    if constexpr (FMT == WF_Q4_K) {
+        // X_kg and X_{4+kg} of token l16 for the chunk's four super-blocks, in
+        // the A layout of the f32 MFMA (bf16 MFMA against row-selector ones)
+        bf16x8 ones[4];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const uint32_t v = (l16 >> 2) == s ? 0x3F803F80u : 0u;
+            ones[s] = __builtin_bit_cast(bf16x8, u32x4{v, v, v, v});
+        }
+#pragma unroll
+        for (int t = 0; t < SBC; t++) {
+            f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const bf16x8 f0 = *(const bf16x8 *)(xrow + 512 * t + 64 * j + 16 * kg);
+                const bf16x8 f1 = *(const bf16x8 *)(xrow + 512 * t + 64 * (4 + j) + 16 * kg);
+                a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], f0, a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], f1, a1, 0, 0, 0);
+            }
+            xq0[t] = a0[0];
+            xq1[t] = a1[0];
+        }
+    }
+
+    // items: the last one is peeled so the prefetch of the next item is
+    // unconditional in the loop (the load counts stay exact for the waits)
+    const int64_t g0 = g;
+    auto item = [&](auto prefetch) {
+        const int64_t gn = min(g + gstep, (int64_t)p.G - 1);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < SBC; t++) {
+            if constexpr (FMT == WF_Q4_K) tile_q4(ring[t], xrow + 512 * t, kg, xq0[t], xq1[t], acc, accM);
+            else tile_q6(ring[t], xrow + 512 * t, kg, acc);
+            // finish this tile's arithmetic here: left alone, the compiler sinks
+            // it past the loads and keeps every tile's products live
+#pragma unroll
+            for (int e = 0; e < 4; e++) asm volatile("" : "+v"(acc[e]));
+            if constexpr (decltype(prefetch)::value) load_tile(w, gn, (int64_t)c * SBC + t, SB, l16, kg, ring[t]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (FMT == WF_Q4_K) acc -= accM;
+        // partial sums of the item: acc[e] = token 4 kg + e, row 16 g + l16
+        float *dst = part + ((int64_t)c * p.G + g) * 256;
+#pragma unroll
+        for (int e = 0; e < 4; e++) put_coherent(dst + (4 * kg + e) * 16 + l16, acc[e]);
+    };
+    // straight-line over the (compile-time) step count: a loop here makes the
+    // compiler wait for every outstanding load at its head. Every step but the
+    // last prefetches (a wave with fewer items re-reads its last group's tiles
+    // once instead of branching, which would also cost register copies).
+    static_assert(STEPS >= 1 && STEPS <= MAX_STEPS, "steps");
+    item(std::integral_constant<bool, (STEPS > 1)>{});
+    if constexpr (STEPS > 1) {
+        g += gstep;
+        if (g < p.G) {
+            item(std::integral_constant<bool, (STEPS > 2)>{});
+            if constexpr (STEPS > 2) {
+                g += gstep;
+                if (g < p.G) {
+                    item(std::integral_constant<bool, (STEPS > 3)>{});
+                    if constexpr (STEPS > 3) {
+                        g += gstep;
+                        if (g < p.G) item(std::false_type{});
+                    }
+                }
+            }
+        }
+    }
+
+    // arrivals, once per wave after all of its items. The partial sums were
+    // written through to memory (system-coherent stores, no dirty L2 lines), so
+    // waiting for their completion publishes them to every XCD before the
+    // counter moves; the completing wave reads them back the same way. (A
+    // device-scope fence instead writes back and invalidates the whole L2.)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    for (int64_t gi = g0; gi < p.G; gi += gstep) {
+        const int64_t unit = EPI == EPI_QKV ? gi / 8 : EPI == EPI_SWIGLU ? 4 * (gi / 8) + (gi & 3) : gi;
+        uint32_t old = 0;
+        if (lane == 0) old = atomicAdd(&counters[unit], 1u);
+        old = __shfl(old, 0);
+        if (old == (uint32_t)(p.C * p.per_unit - 1)) {
+            unit_epilogue<EPI>(part, p, unit, M, N, ep, lane);
+            if (lane == 0) __hip_atomic_store(&counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+template <int FMT, int STEPS>
+hipError_t launch_steps(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, int epi, const EpiParams &ep,
+                        float *part, uint32_t *counters, const Plan &p, hipStream_t stream) {
+    const dim3 grid((unsigned)(p.WPC * p.C)), block(64 * NW);
+    switch (epi) {
+    case EPI_F32: ws_kernel<FMT, EPI_F32, STEPS><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
+    case EPI_BF16: ws_kernel<FMT, EPI_BF16, STEPS><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
+    case EPI_RESID: ws_kernel<FMT, EPI_RESID, STEPS><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
+    case EPI_SWIGLU: ws_kernel<FMT, EPI_SWIGLU, STEPS><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
+    case EPI_QKV: ws_kernel<FMT, EPI_QKV, STEPS><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-}  // namespace m16
+template <int FMT>
+hipError_t launch(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, int epi, const EpiParams &ep,
+                  float *part, uint32_t *counters, const Plan &p, hipStream_t stream) {
+    switch (p.steps) {
+    case 1: return launch_steps<FMT, 1>(w, a, m, lda, epi, ep, part, counters, p, stream);
+    case 2: return launch_steps<FMT, 2>(w, a, m, lda, epi, ep, part, counters, p, stream);
+    case 3: return launch_steps<FMT, 3>(w, a, m, lda, epi, ep, part, counters, p, stream);
+    case 4: return launch_steps<FMT, 4>(w, a, m, lda, epi, ep, part, counters, p, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+}  // namespace ws
 
 // Sum of the split-K partials of C[m][n], in split order.
 __device__ __forceinline__ float csum(const float *part, int splits, int64_t MN, int64_t idx) {
@@ -559,8 +858,6 @@ hipError_t launch_fmt(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t
 // chunks stay whole 256-value groups and the partial sums (written and read
 // once each) stay under half the weight bytes.
 int qgemm_stream_splits(const GemmWeight &w, int64_t m) {
-    int C, T, NG;
-    if (m16::plan(w, m, m16::device_cus(), C, T, NG)) return C;
     const int64_t nt = w.n / 64, kst = w.k / 256;
     const double wbytes = (double)w.n * (double)w.k * (w.fmt == WF_Q4_K ? 0.5625 : w.fmt == WF_Q6_K ? 0.875
                                                        : w.fmt == WF_Q8_0 ? 1.0625 : 2.0);
@@ -575,24 +872,26 @@ bool qgemm_stream_fits(const GemmWeight &w, int64_t m) {
 }
 
 size_t qgemm_stream_workspace(const GemmWeight &w, int64_t m) {
-    return (size_t)qgemm_stream_splits(w, m) * (size_t)m * (size_t)w.n * 4;
+    size_t need = (size_t)qgemm_stream_splits(w, m) * (size_t)m * (size_t)w.n * 4;
+    ws::Plan p;
+    if (ws::plan(w, m, EPI_F32, m16::device_cus(), p)) need = std::max(need, ws::part_bytes(w));
+    return STREAM_COUNTER_BYTES + need;
 }
 
 hipError_t launch_qgemm_stream(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
-                               const EpiParams &ep, float *part, hipStream_t stream) {
-    int splits = qgemm_stream_splits(w, m);
+                               const EpiParams &ep, float *work, hipStream_t stream) {
+    uint32_t *counters = (uint32_t *)work;
+    float *part = (float *)((char *)work + STREAM_COUNTER_BYTES);
+    ws::Plan wp;
+    if (ws::plan(w, m, epi, m16::device_cus(), wp)) {
+        return w.fmt == WF_Q4_K ? ws::launch<WF_Q4_K>(w, a, (int)m, lda, epi, ep, part, counters, wp, stream)
+                                : ws::launch<WF_Q6_K>(w, a, (int)m, lda, epi, ep, part, counters, wp, stream);
+    }
+    const int splits = qgemm_stream_splits(w, m);
     hipError_t e;
-    int C, T, NG;
     switch (w.fmt) {
     case WF_Q8_0: e = launch_fmt<WF_Q8_0>(w, a, m, lda, part, splits, stream); break;
-    case WF_Q4_K:
-        if (m16::plan(w, m, m16::device_cus(), C, T, NG)) {
-            splits = C;
-            e = m16::launch(w, a, m, lda, part, C, T, NG, stream);
-        } else {
-            e = launch_fmt<WF_Q4_K>(w, a, m, lda, part, splits, stream);
-        }
-        break;
+    case WF_Q4_K: e = launch_fmt<WF_Q4_K>(w, a, m, lda, part, splits, stream); break;
     case WF_Q6_K: e = launch_fmt<WF_Q6_K>(w, a, m, lda, part, splits, stream); break;
     case WF_BF16: e = launch_fmt<WF_BF16>(w, a, m, lda, part, splits, stream); break;
     default: return hipErrorInvalidValue;

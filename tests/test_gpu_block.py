@@ -150,13 +150,15 @@ def test_block_config1_shape(torch_cuda, qctx):
     check(got, ref_e, x, exact=True)
 
 
-@pytest.mark.parametrize("b,s,p", [(1, 8, 16), (2, 6, 0)])
-def test_block_hidden4096_short_m(torch_cuda, qctx, b, s, p):
-    """Hidden 4096 (32 heads) at M <= 16 tokens: the fused QKV (12288 x 4096)
-    and output (4096 x 4096) projections take the Q4_K code-product kernel,
-    with the QKV and residual epilogues; a short MLP (512) keeps the oracle
-    quick and runs on the split-K dequantizing kernel."""
-    cfg = dict(hidden=4096, heads=32, head_dim=128, mlp=512)
+@pytest.mark.parametrize("b,s,p,mlp", [(1, 8, 16, 512), (2, 6, 0, 1024), (2, 8, 8, 1024), (1, 16, 0, 2048)])
+def test_block_hidden4096_short_m(torch_cuda, qctx, b, s, p, mlp):
+    """Hidden 4096 (32 heads) at M <= 16 tokens: the fused QKV (12288 x 4096),
+    output (4096 x 4096) and gate_up (2 mlp x 4096) projections and, for
+    mlp % 1024 == 0, the Q6_K down projection take the one-launch kernel with
+    its q/k/v (RmsNorm + RoPE + layouts, batch boundaries inside the token
+    tile), residual and SwiGLU epilogues; mlp 512 sends the down projection to
+    the split-K dequantizing kernel. Short MLPs keep the oracle quick."""
+    cfg = dict(hidden=4096, heads=32, head_dim=128, mlp=mlp)
     w, x, mod, pe, kpre, vpre = make_case(21 + b + s, cfg, b, s, p, synth.Q4_K, synth.Q6_K)
     got, (k, v) = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)
     ref, kr, vr = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)

@@ -91,12 +91,14 @@ def test_qmatmul_matches_bf16_weight_products(torch_cuda, qctx, t, m, n, k):
         assert cos_sim(got, yc) >= 0.9999 and max_abs_rel(got, yc) <= 2e-2
 
 
-@pytest.mark.parametrize("m,n,k", [(16, 4096, 4096),    # one 16-row tile per workgroup
-                                   (1, 8192, 4096),     # a single token, two tiles per workgroup
-                                   (7, 12288, 4096),    # three tiles: a wave spans two n-tiles
-                                   (5, 4096, 8192)])    # two 4096-k chunks
+@pytest.mark.parametrize("m,n,k", [(16, 4096, 4096),
+                                   (1, 8192, 4096),     # a single token
+                                   (7, 12288, 4096),
+                                   (5, 4096, 8192),     # eight 1024-k chunks
+                                   (3, 1152, 1024),     # one k chunk
+                                   (2, 12416, 4096)])   # a second item for a few waves only
 def test_qmatmul_q4k_short_m_exact_weights(torch_cuda, qctx, m, n, k):
-    """Q4_K at M <= 16 and K % 4096 == 0 multiplies the raw codes and applies the
+    """Q4_K at M <= 16 and K % 1024 == 0 multiplies the raw codes and applies the
     scales afterwards: the product of the bf16 activations and the exact
     (not bf16-rounded) Q4_K weights, up to f32 summation order."""
     got, a, w = _gemm_case(torch_cuda, qctx, synth.Q4_K, m, n, k, seed=m + n + k)
@@ -108,6 +110,40 @@ def test_qmatmul_q4k_short_m_exact_weights(torch_cuda, qctx, m, n, k):
     assert cos_sim(got, ye) >= 0.9999 and max_abs_rel(got, ye) <= 2e-2
     yc = O.qmatmul(synth.Q4_K, w, n, k, a, O.CANDLE)
     assert cos_sim(got, yc) >= 0.9999 and max_abs_rel(got, yc) <= 2e-2
+
+
+def test_qmatmul_short_m_one_launch_repeats(torch_cuda, qctx):
+    """The M <= 16 Q4_K / Q6_K path adds its split-K partial sums in the same
+    launch, counting arrivals per output unit in counters that every call
+    leaves at zero: calls in a row over different shapes, token counts and
+    weights give bit-identical results to a first call, and match the
+    products of the bf16 activations and the (bf16-rounded for Q6_K, exact for
+    Q4_K) weights."""
+    torch = torch_cuda
+    cases = [(synth.Q6_K, 16, 4096, 3072), (synth.Q4_K, 16, 2048, 4096), (synth.Q6_K, 5, 1024, 12288),
+             (synth.Q4_K, 1, 3072, 2048), (synth.Q6_K, 16, 4096, 3072)]
+    first = {}
+    for i, (t, m, n, k) in enumerate(cases * 2):
+        rng = np.random.default_rng(100 + i % len(cases))
+        _, w, _, _ = synth.weight(rng, t, n, k)
+        W = qctx.upload(t, n, k, w.tobytes())
+        a_dev, a = bf16_dev(torch, rng.standard_normal((m, k)).astype(np.float32))
+        y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        qctx.qmatmul(W, a_dev.data_ptr(), m, k, y.data_ptr(), synth.BF16, stream(torch))
+        got = host(y.float())
+        W.free()
+        key = i % len(cases)
+        if key in first:
+            assert np.array_equal(got, first[key]), cases[key]
+            continue
+        first[key] = got
+        Wd = O.dequantize(t, w, n * k).reshape(n, k)
+        if t == synth.Q6_K:
+            Wd = O.bf16_round(Wd)
+        want = a.astype(np.float64) @ Wd.astype(np.float64).T
+        scale = np.abs(a).astype(np.float64) @ np.abs(Wd).astype(np.float64).T
+        # bf16 output: half an ulp of the result on top of the f32 sums
+        assert np.all(np.abs(got - want) <= 2e-5 * scale + 4e-3 * np.abs(want) + 1e-6), cases[key]
 
 
 @pytest.mark.parametrize("m", [64, 700])

@@ -2,9 +2,8 @@
 // C = A (bf16, M x K) x W^T (GGUF blocks, N x K). At these sizes the time is
 // the weight bytes over HBM bandwidth, so the kernels are shaped for streaming.
 //
-// Q4_K and Q6_K at M <= 16 with K % 1024 == 0 take the one-launch kernel in
-// namespace ws (its description is there). Everything else takes the split-K
-// kernel:
+// Q4_K and Q6_K with K % 1024 == 0 take the one-launch kernel in namespace ws
+// (its description is there). Everything else takes the split-K kernel:
 //  - 64 weight rows x one K chunk per workgroup (4 waves x 16 rows), the K
 //    range split over workgroups so that the grid holds several workgroups per
 //    CU; partial sums go to an f32 workspace [split][M][N] and a second kernel
@@ -304,58 +303,70 @@ int device_cus() {
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
 // ---------------------------------------------------------------------------
-// M <= 16, Q4_K / Q6_K, K % 1024 == 0: one launch per product.
+// M <= 64, Q4_K / Q6_K, K % 1024 == 0: one launch per product.
 //
 // Work item = (16-row weight group g, 1024-wide k chunk c) = four (group,
-// super-block) tiles, contiguous in the device layout. Workgroup b keeps chunk
-// c = b % C of the activations in LDS (x[16][1024] bf16, loaded once by direct
-// loads) and its four waves grid-stride over the groups: at step t wave v
-// takes group (t * WPC + b / C) * 4 + v. Workgroups with neighbouring ids read
+// super-block) tiles, contiguous in the device layout, against MT = 1, 2 or 4
+// tiles of 16 tokens. Workgroup b keeps chunk c = b % C of the activations in
+// LDS (x[16 MT][1024] bf16, loaded once by direct loads) and its waves (four,
+// or eight for MT = 4) grid-stride over the groups: at step t wave v takes
+// group (t * WPC + b / C) * NW + v. Workgroups with neighbouring ids read
 // neighbouring groups, so the bytes in flight at any time are one compact
 // window of the weight matrix (the pattern of a plain streaming read). Raw
 // tiles go straight to registers, four in flight per wave, one item ahead.
 //
-// Q4_K uses the exact code products of the M <= 16 kernel above (the
-// sub-block sums X_j of the chunk are computed once per wave). Q6_K
-// dequantizes each lane's 8 values of a step with v_fma_mix (the 6-bit codes
-// as f16 subnormals, scales carrying 2^24; RNE to bf16); a lane's 8 values of
-// a step are 8 consecutive k of one 16-value sub-block and the matching
-// activations are one 16 B LDS read, so the lane reads its ql / qh bytes as
-// 16 B pieces.
+// Q4_K uses the exact code products described above (the sub-block sums X_j
+// of the chunk are computed once per wave and token tile). Q6_K dequantizes
+// each lane's 8 values of a step with v_fma_mix (the 6-bit codes as f16
+// subnormals, scales carrying 2^24; RNE to bf16) once for all token tiles; a
+// lane's 8 values of a step are 8 consecutive k of one 16-value sub-block and
+// the matching activations are one 16 B LDS read, so the lane reads its ql /
+// qh bytes as 16 B pieces.
 //
-// The partial sums of an item, [16 tokens][16 rows] f32, go to
-// part[c][g]; the wave that completes the last item of an epilogue unit
-// (counter per unit, device-scope fences around it) adds the C partials of the
-// unit in chunk order -- deterministic -- applies the epilogue and resets the
-// counter for the next launch. Units: a group (F32, BF16, residual), the
-// gate and up groups of 16 hidden columns (SwiGLU), a 128-column head (q/k/v).
+// The partial sums of an item, [16 MT tokens][16 rows] f32, go to
+// part[c][g] with system-scope stores; the wave that completes the last item
+// of an epilogue unit (a counter per unit) reads the C partials of the unit
+// back the same way, adds them in chunk order -- deterministic -- applies the
+// epilogue and resets the counter for the next launch. Units: a group (F32,
+// BF16, residual), the gate and up groups of 16 hidden columns (SwiGLU), a
+// 128-column head (q/k/v).
 namespace ws {
 
-constexpr int NW = 4;               // waves per workgroup
 constexpr int KCH = 1024;           // k per chunk
 constexpr int SBC = KCH / 256;      // tiles per item
 constexpr int XROW = KCH * 2 + 16;  // padded LDS row: a fragment's 16 rows hit distinct bank groups
 constexpr int MAX_STEPS = 4;        // items per wave (compile-time unrolled)
 
+// Token tiles of 16 per item (MT), and per MT the waves per workgroup and the
+// workgroups resident per CU (LDS: 16 MT rows of XROW bytes per workgroup).
+constexpr int nwaves(int mt) { return mt == 4 ? 8 : 4; }
+constexpr int wg_per_cu(int mt) { return mt == 1 ? 3 : mt == 2 ? 2 : 1; }
+
 struct Plan {
-    int C, G, WPC, steps, units, per_unit;
+    int C, G, WPC, steps, units, per_unit, MT;
 };
 
 bool plan(const GemmWeight &w, int64_t m, int epi, int cus, Plan &p) {
-    if ((w.fmt != WF_Q4_K && w.fmt != WF_Q6_K) || m < 1 || m > 16 || w.k % KCH || w.n % 16 || cus <= 0)
+    if ((w.fmt != WF_Q4_K && w.fmt != WF_Q6_K) || m < 1 || m > 64 || w.k % KCH || w.n % 16 || cus <= 0)
         return false;
     if ((epi == EPI_SWIGLU || epi == EPI_QKV) && w.n % 128) return false;
+    p.MT = m <= 16 ? 1 : m <= 32 ? 2 : 4;
+    const int nw = nwaves(p.MT);
     p.C = (int)(w.k / KCH);
     p.G = (int)(w.n / 16);
-    const int need = (p.G + NW - 1) / NW;  // workgroups per chunk that have work at step 0
-    p.WPC = std::max(1, std::min(3 * cus / p.C, need));
-    p.steps = (p.G + NW * p.WPC - 1) / (NW * p.WPC);
+    const int need = (p.G + nw - 1) / nw;  // workgroups per chunk that have work at step 0
+    p.WPC = std::max(1, std::min(wg_per_cu(p.MT) * cus / p.C, need));
+    p.steps = (p.G + nw * p.WPC - 1) / (nw * p.WPC);
     p.per_unit = epi == EPI_QKV ? 8 : epi == EPI_SWIGLU ? 2 : 1;
     p.units = p.G / p.per_unit;
     return p.steps <= MAX_STEPS && (size_t)p.units * 4 <= STREAM_COUNTER_BYTES;
 }
 
-size_t part_bytes(const GemmWeight &w) { return (size_t)(w.k / KCH) * (size_t)w.n * 64; }
+// partial sums: [C][G][16 MT tokens][16 rows] f32
+size_t part_bytes(const GemmWeight &w, int64_t m) {
+    const int mt = m <= 16 ? 1 : m <= 32 ? 2 : 4;
+    return (size_t)(w.k / KCH) * (size_t)w.n * 64 * mt;
+}
 
 struct TileQ4 {
     u32x4 h;
@@ -403,10 +414,6 @@ __device__ __forceinline__ float mix_hi(uint32_t x, float s, float c) {
     return r;
 }
 
-// One Q6_K tile (16 rows x 256 k) into acc. Step s: half hh = s / 4, nibble
-// n = (s / 2) % 2, 8-byte half h8 = s % 2 of the lane's 16 B pieces; the values
-// are k = 128 hh + 32 (r1 + 2 n) + 16 h' + 8 h8 + i of the super-block, scale
-// index 8 hh + 4 n + kg.
 // The raw registers pass through an empty asm first, so no decoding of a tile
 // is hoisted to where its loads were issued (that would wait for them there).
 __device__ __forceinline__ void pin(TileQ6 &r) {
@@ -416,7 +423,13 @@ __device__ __forceinline__ void pin(TileQ4 &r) {
     asm volatile("" : "+v"(r.h), "+v"(r.q[0]), "+v"(r.q[1]), "+v"(r.q[2]), "+v"(r.q[3]));
 }
 
-__device__ __forceinline__ void tile_q6(TileQ6 r, const uint8_t *xrow, int kg, f32x4 &acc) {
+// One Q6_K tile (16 rows x 256 k) into acc[0..MT) (token tiles 16 tt + l16
+// at xrow + 16 tt XROW). Step s: half hh = s / 4, nibble n = (s / 2) % 2,
+// 8-byte half h8 = s % 2 of the lane's 16 B pieces; the values are
+// k = 128 hh + 32 (r1 + 2 n) + 16 h' + 8 h8 + i of the super-block, scale
+// index 8 hh + 4 n + kg. Each step's B fragment serves every token tile.
+template <int MT>
+__device__ __forceinline__ void tile_q6(TileQ6 r, const uint8_t *xrow, int kg, f32x4 *acc) {
     pin(r);
     const float d = m16::cvt_f16_lo(r.d);
     const uint32_t hsh = 2u * (uint32_t)(kg >> 1);  // qh bit pair of quadrant r1 (+4 for n = 1)
@@ -438,15 +451,20 @@ __device__ __forceinline__ void tile_q6(TileQ6 r, const uint8_t *xrow, int kg, f
         const uint32_t p2 = c[1] & 0x00FF00FFu, p3 = __builtin_amdgcn_perm(0u, c[1], 0x0C030C01u);
         const u32x4 bw = {pack_bf16x2(mix_lo(p0, a, b), mix_lo(p1, a, b)), pack_bf16x2(mix_hi(p0, a, b), mix_hi(p1, a, b)),
                           pack_bf16x2(mix_lo(p2, a, b), mix_lo(p3, a, b)), pack_bf16x2(mix_hi(p2, a, b), mix_hi(p3, a, b))};
-        const bf16x8 av = *(const bf16x8 *)(xrow + 256 * hh + 128 * n + 32 * kg + 16 * h8);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bw), acc, 0, 0, 0);
+#pragma unroll
+        for (int tt = 0; tt < MT; tt++) {
+            const bf16x8 av = *(const bf16x8 *)(xrow + tt * 16 * XROW + 256 * hh + 128 * n + 32 * kg + 16 * h8);
+            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bw), acc[tt], 0, 0, 0);
+        }
     }
 }
 
-// One Q4_K tile by code products (see the M <= 16 kernel): xq0 / xq1 hold the
-// sub-block sums X_kg, X_{4+kg} of token l16 for this super-block.
-__device__ __forceinline__ void tile_q4(TileQ4 r, const uint8_t *xrow, int kg, float xq0, float xq1,
-                                        f32x4 &accA, f32x4 &accM) {
+// One Q4_K tile by code products (see the m16 notes above) into accA / accM
+// of each token tile; xq0[tt] / xq1[tt] hold the sub-block sums X_kg,
+// X_{4+kg} of token 16 tt + l16 for this super-block.
+template <int MT>
+__device__ __forceinline__ void tile_q4(TileQ4 r, const uint8_t *xrow, int kg, const float *xq0, const float *xq1,
+                                        f32x4 *accA, f32x4 *accM) {
     pin(r);
     const uint32_t hx = r.h[0], hy = r.h[1], hz = r.h[2], hw = r.h[3];
     const float d = m16::cvt_f16_lo(hx), dmin = m16::cvt_f16_hi(hx);
@@ -456,29 +474,35 @@ __device__ __forceinline__ void tile_q4(TileQ4 r, const uint8_t *xrow, int kg, f
     const uint32_t sh = 8u * (uint32_t)kg;
     const float cc0 = fmaf(128.f, d * (float)((sc_lo >> sh) & 0xffu), dmin * (float)((m_lo >> sh) & 0xffu));
     const float cc1 = fmaf(128.f, d * (float)((sc_hi >> sh) & 0xffu), dmin * (float)((m_hi >> sh) & 0xffu));
-    accM = __builtin_amdgcn_mfma_f32_16x16x4f32(xq0, cc0, accM, 0, 0, 0);
-    accM = __builtin_amdgcn_mfma_f32_16x16x4f32(xq1, cc1, accM, 0, 0, 0);
+#pragma unroll
+    for (int tt = 0; tt < MT; tt++) {
+        accM[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xq0[tt], cc0, accM[tt], 0, 0, 0);
+        accM[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xq1[tt], cc1, accM[tt], 0, 0, 0);
+    }
     // two halves of four sub-blocks: four independent products in flight,
-    // scaled into accA as the next half's products run
+    // scaled into accA as the next products run
 #pragma unroll
     for (int hf = 0; hf < 2; hf++) {
         u32x4 bq[4];
 #pragma unroll
         for (int cc = 0; cc < 2; cc++)
             m16::codes8(r.q[2 * hf + cc][0], r.q[2 * hf + cc][1], bq[2 * cc], bq[2 * cc + 1]);
-        f32x4 tv[4];
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-            const bf16x8 av = *(const bf16x8 *)(xrow + 64 * (4 * hf + jj) + 16 * kg);
-            tv[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bq[jj]),
-                                                             f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        }
+        for (int tt = 0; tt < MT; tt++) {
+            f32x4 tv[4];
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-            const int j = 4 * hf + jj;
-            const float ds = d * (float)(((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3))) & 0xffu);
+            for (int jj = 0; jj < 4; jj++) {
+                const bf16x8 av = *(const bf16x8 *)(xrow + tt * 16 * XROW + 64 * (4 * hf + jj) + 16 * kg);
+                tv[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bq[jj]),
+                                                                 f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            }
 #pragma unroll
-            for (int e = 0; e < 4; e++) accA[e] = fmaf(ds, tv[jj][e], accA[e]);
+            for (int jj = 0; jj < 4; jj++) {
+                const int j = 4 * hf + jj;
+                const float ds = d * (float)(((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3))) & 0xffu);
+#pragma unroll
+                for (int e = 0; e < 4; e++) accA[tt][e] = fmaf(ds, tv[jj][e], accA[tt][e]);
+            }
         }
     }
 }
@@ -492,18 +516,18 @@ __device__ __forceinline__ float get_coherent(const float *p) {
     return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// Sums over the C chunks of the four partial elements (g, row r, tokens
-// 4 kg + e) of a lane, in chunk order. Loads go out eight chunks at a time so
-// a batch costs one memory round trip.
-__device__ __forceinline__ f32x4 psum4(const float *part, int C, int G, int64_t g, int kg, int r) {
+// Sums over the C chunks of the four partial elements (row r, tokens
+// 16 tt + 4 kg + e) of a lane in group g, in chunk order. Loads go out eight
+// chunks at a time so a batch costs one memory round trip. IS = floats per item.
+__device__ __forceinline__ f32x4 psum4(const float *part, int C, int G, int IS, int64_t g, int tt, int kg, int r) {
     constexpr int B = 8;
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    const float *base = part + g * 256 + (4 * kg) * 16 + r;
+    const float *base = part + g * IS + (16 * tt + 4 * kg) * 16 + r;
     for (int c0 = 0; c0 < C; c0 += B) {
         float v[B][4];
 #pragma unroll
         for (int cc = 0; cc < B; cc++) {
-            const float *pc = base + (int64_t)min(c0 + cc, C - 1) * G * 256;
+            const float *pc = base + (int64_t)min(c0 + cc, C - 1) * G * IS;
 #pragma unroll
             for (int e = 0; e < 4; e++) v[cc][e] = get_coherent(pc + e * 16);
         }
@@ -517,107 +541,121 @@ __device__ __forceinline__ f32x4 psum4(const float *part, int C, int G, int64_t 
     return s;
 }
 
-template <int EPI>
+template <int EPI, int MT>
 __device__ void unit_epilogue(const float *part, const Plan &p, int64_t unit, int M, int64_t N, const EpiParams &ep,
                               int lane) {
+    constexpr int TOK = 16 * MT, IS = 16 * TOK;
     const int l16 = lane & 15, kg = lane >> 4;
     if constexpr (EPI == EPI_QKV) {
-        // head unit: lane j holds columns (2j, 2j+1) of the head, one token at a time
+        // head unit: lane j holds columns (2j, 2j+1) of the head; eight tokens
+        // per batch of loads (chunk sums in chunk order)
         const int64_t g = unit * 8 + (lane >> 3);
         const int r = 2 * (lane & 7);
         const int64_t nb = unit * 128 + ep.n_offset;
         const int sec = (int)(nb / ep.hidden);
         const int64_t head = (nb % ep.hidden) / 128;
         const int64_t S = ep.seq, H = ep.heads;
-        // four tokens per batch of loads (chunk sums in chunk order)
-        for (int m0 = 0; m0 < M; m0 += 4) {
-          float sx[4][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
-          for (int c0 = 0; c0 < p.C; c0 += 4) {
-            float v[4][4][2];
+        constexpr int TB = 8, CB = 4;
+        for (int m0 = 0; m0 < M; m0 += TB) {
+            float sx[TB][2];
 #pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-                const float *pc = part + ((int64_t)min(c0 + cc, p.C - 1) * p.G + g) * 256 + r;
+            for (int i = 0; i < TB; i++) sx[i][0] = sx[i][1] = 0.f;
+            for (int c0 = 0; c0 < p.C; c0 += CB) {
+                float v[CB][TB][2];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int m = min(m0 + i, 15);
-                    v[cc][i][0] = get_coherent(pc + m * 16);
-                    v[cc][i][1] = get_coherent(pc + m * 16 + 1);
-                }
-            }
+                for (int cc = 0; cc < CB; cc++) {
+                    const float *pc = part + ((int64_t)min(c0 + cc, p.C - 1) * p.G + g) * IS + r;
 #pragma unroll
-            for (int cc = 0; cc < 4; cc++)
-                if (c0 + cc < p.C) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        sx[i][0] += v[cc][i][0];
-                        sx[i][1] += v[cc][i][1];
+                    for (int i = 0; i < TB; i++) {
+                        const int m = min(m0 + i, TOK - 1);
+                        v[cc][i][0] = get_coherent(pc + m * 16);
+                        v[cc][i][1] = get_coherent(pc + m * 16 + 1);
                     }
                 }
-          }
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const int m = m0 + i;
-            if (m >= M) break;
-            float x0 = sx[i][0], x1 = sx[i][1];
-            const int64_t b = m / S, s = m % S;
-            if (sec < 2) {
-                const float *nw = sec == 0 ? ep.norm_q : ep.norm_k;
-                const float ss = wave_sum(x0 * x0 + x1 * x1);
-                const float rs = 1.0f / sqrtf(ss * (1.0f / 128.0f) + 1e-6f);
-                x0 = x0 * rs * nw[2 * lane];
-                x1 = x1 * rs * nw[2 * lane + 1];
-                const float *pr = ep.pe + s * 128 + 2 * lane;
-                const float cs = pr[0], sn = pr[1];
-                const float osc = sec == 0 ? ep.q_scale : 1.0f;
-                const float y0 = (x0 * cs - x1 * sn) * osc, y1 = (x0 * sn + x1 * cs) * osc;
-                uint16_t *dst = sec == 0 ? ep.q : ep.k;
-                *(uint32_t *)(dst + ((b * H + head) * S + s) * 128 + 2 * lane) = pack_bf16x2(y0, y1);
-            } else {
-                const uint32_t pk = pack_bf16x2(x0, x1);
-                ep.vt[((b * H + head) * 128 + 2 * lane) * S + s] = (uint16_t)(pk & 0xffffu);
-                ep.vt[((b * H + head) * 128 + 2 * lane + 1) * S + s] = (uint16_t)(pk >> 16);
-                if (ep.v_bhsd) *(uint32_t *)(ep.v_bhsd + ((b * H + head) * S + s) * 128 + 2 * lane) = pk;
+                for (int cc = 0; cc < CB; cc++)
+                    if (c0 + cc < p.C) {
+#pragma unroll
+                        for (int i = 0; i < TB; i++) {
+                            sx[i][0] += v[cc][i][0];
+                            sx[i][1] += v[cc][i][1];
+                        }
+                    }
             }
-          }
+#pragma unroll
+            for (int i = 0; i < TB; i++) {
+                const int m = m0 + i;
+                if (m >= M) break;
+                float x0 = sx[i][0], x1 = sx[i][1];
+                const int64_t b = m / S, s = m % S;
+                if (sec < 2) {
+                    const float *nw = sec == 0 ? ep.norm_q : ep.norm_k;
+                    const float ss = wave_sum(x0 * x0 + x1 * x1);
+                    const float rs = 1.0f / sqrtf(ss * (1.0f / 128.0f) + 1e-6f);
+                    x0 = x0 * rs * nw[2 * lane];
+                    x1 = x1 * rs * nw[2 * lane + 1];
+                    const float *pr = ep.pe + s * 128 + 2 * lane;
+                    const float cs = pr[0], sn = pr[1];
+                    const float osc = sec == 0 ? ep.q_scale : 1.0f;
+                    const float y0 = (x0 * cs - x1 * sn) * osc, y1 = (x0 * sn + x1 * cs) * osc;
+                    uint16_t *dst = sec == 0 ? ep.q : ep.k;
+                    *(uint32_t *)(dst + ((b * H + head) * S + s) * 128 + 2 * lane) = pack_bf16x2(y0, y1);
+                } else {
+                    const uint32_t pk = pack_bf16x2(x0, x1);
+                    ep.vt[((b * H + head) * 128 + 2 * lane) * S + s] = (uint16_t)(pk & 0xffffu);
+                    ep.vt[((b * H + head) * 128 + 2 * lane + 1) * S + s] = (uint16_t)(pk >> 16);
+                    if (ep.v_bhsd) *(uint32_t *)(ep.v_bhsd + ((b * H + head) * S + s) * 128 + 2 * lane) = pk;
+                }
+            }
         }
     } else if constexpr (EPI == EPI_SWIGLU) {
         // hidden columns 64 blk + 16 q + l16: gate group 8 blk + q, up group 8 blk + 4 + q
         const int64_t blk = unit >> 2, q = unit & 3;
         const int64_t gg = 8 * blk + q, gu = gg + 4;
-        const f32x4 gt = psum4(part, p.C, p.G, gg, kg, l16), up = psum4(part, p.C, p.G, gu, kg, l16);
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int m = 4 * kg + e;
-            if (m < M)
-                ep.hmid[m * ep.ldh + 64 * blk + 16 * q + l16] =
-                    (uint16_t)(pack_bf16x2(silu(gt[e]) * up[e], 0.f) & 0xffffu);
+        for (int tt = 0; tt < MT; tt++) {
+            if (16 * tt >= M) break;
+            const f32x4 gt = psum4(part, p.C, p.G, IS, gg, tt, kg, l16);
+            const f32x4 up = psum4(part, p.C, p.G, IS, gu, tt, kg, l16);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = 16 * tt + 4 * kg + e;
+                if (m < M)
+                    ep.hmid[m * ep.ldh + 64 * blk + 16 * q + l16] =
+                        (uint16_t)(pack_bf16x2(silu(gt[e]) * up[e], 0.f) & 0xffffu);
+            }
         }
     } else {
         const int64_t n = unit * 16 + l16;
-        const f32x4 sum = psum4(part, p.C, p.G, unit, kg, l16);
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int m = 4 * kg + e;
-            if (m < M) {
-                const float v = sum[e];
-                if constexpr (EPI == EPI_F32) {
-                    ((float *)ep.out)[m * ep.ldo + n] = v;
-                } else if constexpr (EPI == EPI_BF16) {
-                    ((uint16_t *)ep.out)[m * ep.ldo + n] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
-                } else {  // EPI_RESID
-                    const float *grow = ep.gvec + (int64_t)(m / (int)ep.g_rows_per) * ep.g_stride;
-                    ep.x_out[m * N + n] = ep.x_in[m * N + n] + grow[n] * v;
+        for (int tt = 0; tt < MT; tt++) {
+            if (16 * tt >= M) break;
+            const f32x4 sum = psum4(part, p.C, p.G, IS, unit, tt, kg, l16);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = 16 * tt + 4 * kg + e;
+                if (m < M) {
+                    const float v = sum[e];
+                    if constexpr (EPI == EPI_F32) {
+                        ((float *)ep.out)[m * ep.ldo + n] = v;
+                    } else if constexpr (EPI == EPI_BF16) {
+                        ((uint16_t *)ep.out)[m * ep.ldo + n] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
+                    } else {  // EPI_RESID
+                        const float *grow = ep.gvec + (int64_t)(m / (int)ep.g_rows_per) * ep.g_stride;
+                        ep.x_out[m * N + n] = ep.x_in[m * N + n] + grow[n] * v;
+                    }
                 }
             }
         }
     }
 }
 
-template <int FMT, int EPI, int STEPS>
-__global__ __launch_bounds__(64 * NW) void ws_kernel(const uint16_t *__restrict__ A, int M, int64_t lda, GemmWeight w,
-                                                     float *__restrict__ part, uint32_t *__restrict__ counters, Plan p,
-                                                     EpiParams ep) {
-    __shared__ __attribute__((aligned(16))) uint8_t xs[16 * XROW];
+template <int FMT, int EPI, int STEPS, int MT>
+__global__ __launch_bounds__(64 * nwaves(MT), wg_per_cu(MT) * nwaves(MT) / 4) void ws_kernel(const uint16_t *__restrict__ A, int M, int64_t lda,
+                                                             GemmWeight w, float *__restrict__ part,
+                                                             uint32_t *__restrict__ counters, Plan p, EpiParams ep) {
+    constexpr int NW = nwaves(MT), TOK = 16 * MT, IS = 16 * TOK;
+    __shared__ __attribute__((aligned(16))) uint8_t xs[TOK * XROW];
     const int lane = threadIdx.x & 63, l16 = lane & 15, kg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = blockIdx.x % p.C, slot = blockIdx.x / p.C;
@@ -628,7 +666,7 @@ __global__ __launch_bounds__(64 * NW) void ws_kernel(const uint16_t *__restrict_
     // x chunk -> LDS by direct loads: instruction i of wave v fills 64
     // consecutive 16 B pieces of one row; rows past M repeat row M - 1
 #pragma unroll
-    for (int i = 0; i < 16 * (KCH / 8) / 64 / NW; i++) {
+    for (int i = 0; i < TOK * (KCH / 8) / 64 / NW; i++) {
         const int q0 = (i * NW + wave) * 64;
         const int m = q0 / (KCH / 8), s0 = q0 % (KCH / 8);
         const uint16_t *src = A + (int64_t)min(m, M - 1) * lda + (int64_t)c * KCH + 8 * (s0 + lane);
@@ -650,10 +688,11 @@ __global__ __launch_bounds__(64 * NW) void ws_kernel(const uint16_t *__restrict_
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(SBC * TL) : "memory");
 
     const uint8_t *xrow = xs + l16 * XROW;
-    float xq0[SBC], xq1[SBC];
+    float xq0[SBC][MT], xq1[SBC][MT];
     if constexpr (FMT == WF_Q4_K) {
-        // X_kg and X_{4+kg} of token l16 for the chunk's four super-blocks, in
-        // the A layout of the f32 MFMA (bf16 MFMA against row-selector ones)
+        // X_kg and X_{4+kg} of token 16 tt + l16 for the chunk's four
+        // super-blocks, in the A layout of the f32 MFMA (bf16 MFMA against
+        // row-selector ones)
         bf16x8 ones[4];
 #pragma unroll
         for (int s = 0; s < 4; s++) {
@@ -661,18 +700,21 @@ __global__ __launch_bounds__(64 * NW) void ws_kernel(const uint16_t *__restrict_
             ones[s] = __builtin_bit_cast(bf16x8, u32x4{v, v, v, v});
         }
 #pragma unroll
-        for (int t = 0; t < SBC; t++) {
-            f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < SBC; t++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const bf16x8 f0 = *(const bf16x8 *)(xrow + 512 * t + 64 * j + 16 * kg);
-                const bf16x8 f1 = *(const bf16x8 *)(xrow + 512 * t + 64 * (4 + j) + 16 * kg);
-                a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], f0, a0, 0, 0, 0);
-                a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], f1, a1, 0, 0, 0);
+            for (int tt = 0; tt < MT; tt++) {
+                const uint8_t *xr = xrow + tt * 16 * XROW + 512 * t;
+                f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const bf16x8 f0 = *(const bf16x8 *)(xr + 64 * j + 16 * kg);
+                    const bf16x8 f1 = *(const bf16x8 *)(xr + 64 * (4 + j) + 16 * kg);
+                    a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], f0, a0, 0, 0, 0);
+                    a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], f1, a1, 0, 0, 0);
+                }
+                xq0[t][tt] = a0[0];
+                xq1[t][tt] = a1[0];
             }
-            xq0[t] = a0[0];
-            xq1[t] = a1[0];
-        }
     }
 
     // items: the last one is peeled so the prefetch of the next item is
@@ -680,23 +722,30 @@ __global__ __launch_bounds__(64 * NW) void ws_kernel(const uint16_t *__restrict_
     const int64_t g0 = g;
     auto item = [&](auto prefetch) {
         const int64_t gn = min(g + gstep, (int64_t)p.G - 1);
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
+        f32x4 acc[MT], accM[MT];
+#pragma unroll
+        for (int tt = 0; tt < MT; tt++) acc[tt] = accM[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < SBC; t++) {
-            if constexpr (FMT == WF_Q4_K) tile_q4(ring[t], xrow + 512 * t, kg, xq0[t], xq1[t], acc, accM);
-            else tile_q6(ring[t], xrow + 512 * t, kg, acc);
+            if constexpr (FMT == WF_Q4_K) tile_q4<MT>(ring[t], xrow + 512 * t, kg, xq0[t], xq1[t], acc, accM);
+            else tile_q6<MT>(ring[t], xrow + 512 * t, kg, acc);
             // finish this tile's arithmetic here: left alone, the compiler sinks
             // it past the loads and keeps every tile's products live
 #pragma unroll
-            for (int e = 0; e < 4; e++) asm volatile("" : "+v"(acc[e]));
+            for (int tt = 0; tt < MT; tt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) asm volatile("" : "+v"(acc[tt][e]));
             if constexpr (decltype(prefetch)::value) load_tile(w, gn, (int64_t)c * SBC + t, SB, l16, kg, ring[t]);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (FMT == WF_Q4_K) acc -= accM;
-        // partial sums of the item: acc[e] = token 4 kg + e, row 16 g + l16
-        float *dst = part + ((int64_t)c * p.G + g) * 256;
+        // partial sums of the item: acc[tt][e] = token 16 tt + 4 kg + e, row 16 g + l16
+        float *dst = part + ((int64_t)c * p.G + g) * IS;
 #pragma unroll
-        for (int e = 0; e < 4; e++) put_coherent(dst + (4 * kg + e) * 16 + l16, acc[e]);
+        for (int tt = 0; tt < MT; tt++) {
+            if constexpr (FMT == WF_Q4_K) acc[tt] -= accM[tt];
+#pragma unroll
+            for (int e = 0; e < 4; e++) put_coherent(dst + (16 * tt + 4 * kg + e) * 16 + l16, acc[tt][e]);
+        }
     };
     // straight-line over the (compile-time) step count: a loop here makes the
     // compiler wait for every outstanding load at its head. Every step but the
@@ -733,35 +782,46 @@ __global__ __launch_bounds__(64 * NW) void ws_kernel(const uint16_t *__restrict_
         if (lane == 0) old = atomicAdd(&counters[unit], 1u);
         old = __shfl(old, 0);
         if (old == (uint32_t)(p.C * p.per_unit - 1)) {
-            unit_epilogue<EPI>(part, p, unit, M, N, ep, lane);
+            unit_epilogue<EPI, MT>(part, p, unit, M, N, ep, lane);
             if (lane == 0) __hip_atomic_store(&counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
 
-template <int FMT, int STEPS>
+template <int FMT, int STEPS, int MT>
 hipError_t launch_steps(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, int epi, const EpiParams &ep,
                         float *part, uint32_t *counters, const Plan &p, hipStream_t stream) {
-    const dim3 grid((unsigned)(p.WPC * p.C)), block(64 * NW);
+    const dim3 grid((unsigned)(p.WPC * p.C)), block(64 * nwaves(MT));
     switch (epi) {
-    case EPI_F32: ws_kernel<FMT, EPI_F32, STEPS><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
-    case EPI_BF16: ws_kernel<FMT, EPI_BF16, STEPS><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
-    case EPI_RESID: ws_kernel<FMT, EPI_RESID, STEPS><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
-    case EPI_SWIGLU: ws_kernel<FMT, EPI_SWIGLU, STEPS><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
-    case EPI_QKV: ws_kernel<FMT, EPI_QKV, STEPS><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
+    case EPI_F32: ws_kernel<FMT, EPI_F32, STEPS, MT><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
+    case EPI_BF16: ws_kernel<FMT, EPI_BF16, STEPS, MT><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
+    case EPI_RESID: ws_kernel<FMT, EPI_RESID, STEPS, MT><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
+    case EPI_SWIGLU: ws_kernel<FMT, EPI_SWIGLU, STEPS, MT><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
+    case EPI_QKV: ws_kernel<FMT, EPI_QKV, STEPS, MT><<<grid, block, 0, stream>>>(a, m, lda, w, part, counters, p, ep); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
+template <int FMT, int MT>
+hipError_t launch_mt(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, int epi, const EpiParams &ep,
+                     float *part, uint32_t *counters, const Plan &p, hipStream_t stream) {
+    switch (p.steps) {
+    case 1: return launch_steps<FMT, 1, MT>(w, a, m, lda, epi, ep, part, counters, p, stream);
+    case 2: return launch_steps<FMT, 2, MT>(w, a, m, lda, epi, ep, part, counters, p, stream);
+    case 3: return launch_steps<FMT, 3, MT>(w, a, m, lda, epi, ep, part, counters, p, stream);
+    case 4: return launch_steps<FMT, 4, MT>(w, a, m, lda, epi, ep, part, counters, p, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 template <int FMT>
 hipError_t launch(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, int epi, const EpiParams &ep,
                   float *part, uint32_t *counters, const Plan &p, hipStream_t stream) {
-    switch (p.steps) {
-    case 1: return launch_steps<FMT, 1>(w, a, m, lda, epi, ep, part, counters, p, stream);
-    case 2: return launch_steps<FMT, 2>(w, a, m, lda, epi, ep, part, counters, p, stream);
-    case 3: return launch_steps<FMT, 3>(w, a, m, lda, epi, ep, part, counters, p, stream);
-    case 4: return launch_steps<FMT, 4>(w, a, m, lda, epi, ep, part, counters, p, stream);
+    switch (p.MT) {
+    case 1: return launch_mt<FMT, 1>(w, a, m, lda, epi, ep, part, counters, p, stream);
+    case 2: return launch_mt<FMT, 2>(w, a, m, lda, epi, ep, part, counters, p, stream);
+    case 4: return launch_mt<FMT, 4>(w, a, m, lda, epi, ep, part, counters, p, stream);
     default: return hipErrorInvalidValue;
     }
 }
@@ -874,7 +934,7 @@ bool qgemm_stream_fits(const GemmWeight &w, int64_t m) {
 size_t qgemm_stream_workspace(const GemmWeight &w, int64_t m) {
     size_t need = (size_t)qgemm_stream_splits(w, m) * (size_t)m * (size_t)w.n * 4;
     ws::Plan p;
-    if (ws::plan(w, m, EPI_F32, m16::device_cus(), p)) need = std::max(need, ws::part_bytes(w));
+    if (ws::plan(w, m, EPI_F32, m16::device_cus(), p)) need = std::max(need, ws::part_bytes(w, m));
     return STREAM_COUNTER_BYTES + need;
 }
 

@@ -150,9 +150,10 @@ def test_block_config1_shape(torch_cuda, qctx):
     check(got, ref_e, x, exact=True)
 
 
-@pytest.mark.parametrize("b,s,p,mlp", [(1, 8, 16, 512), (2, 6, 0, 1024), (2, 8, 8, 1024), (1, 16, 0, 2048)])
+@pytest.mark.parametrize("b,s,p,mlp", [(1, 8, 16, 512), (2, 6, 0, 1024), (2, 8, 8, 1024), (1, 16, 0, 2048),
+                                       (2, 20, 8, 1024), (1, 64, 16, 1024)])
 def test_block_hidden4096_short_m(torch_cuda, qctx, b, s, p, mlp):
-    """Hidden 4096 (32 heads) at M <= 16 tokens: the fused QKV (12288 x 4096),
+    """Hidden 4096 (32 heads) at M <= 64 tokens: the fused QKV (12288 x 4096),
     output (4096 x 4096) and gate_up (2 mlp x 4096) projections and, for
     mlp % 1024 == 0, the Q6_K down projection take the one-launch kernel with
     its q/k/v (RmsNorm + RoPE + layouts, batch boundaries inside the token

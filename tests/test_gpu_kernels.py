@@ -77,11 +77,16 @@ def _gemm_case(torch, qctx, t, m, n, k, seed, out_type=synth.F32, std=0.02):
                                    (130, 384, 1024), (300, 128, 4096),
                                    (600, 512, 1024), (1024, 256, 768)])   # the last two: 256x256 kernel
 def test_qmatmul_matches_bf16_weight_products(torch_cuda, qctx, t, m, n, k):
+    """Products of the bf16 activations and the weights each path multiplies:
+    bf16-rounded dequantized weights on the MFMA dequant paths, the exact Q4_K
+    weights on the code-product path (Q4_K, M <= 64, K % 1024 == 0)."""
     got, a, w = _gemm_case(torch_cuda, qctx, t, m, n, k, seed=m * 7 + n + k + t)
     Wd = O.dequantize(t, w, n * k).reshape(n, k)
     Wb = O.bf16_round(Wd).astype(np.float64)
     want = a.astype(np.float64) @ Wb.T
     scale = np.abs(a).astype(np.float64) @ np.abs(Wb).T
+    if t == synth.Q4_K and m <= 64 and k % 1024 == 0:
+        want = a.astype(np.float64) @ Wd.astype(np.float64).T
     assert np.all(np.abs(got - want) <= 2e-4 * scale + 1e-6)
     # against the oracle: exact weights (exact mode) and candle's int8 activations
     ye = O.qmatmul(t, w, n, k, a, O.EXACT)
@@ -96,9 +101,12 @@ def test_qmatmul_matches_bf16_weight_products(torch_cuda, qctx, t, m, n, k):
                                    (7, 12288, 4096),
                                    (5, 4096, 8192),     # eight 1024-k chunks
                                    (3, 1152, 1024),     # one k chunk
-                                   (2, 12416, 4096)])   # a second item for a few waves only
+                                   (2, 12416, 4096),    # a second item for a few waves only
+                                   (33, 4096, 4096),    # three 16-token tiles of 64 (one padded)
+                                   (24, 2048, 2048),    # two 16-token tiles
+                                   (64, 6144, 4096)])   # four full token tiles
 def test_qmatmul_q4k_short_m_exact_weights(torch_cuda, qctx, m, n, k):
-    """Q4_K at M <= 16 and K % 1024 == 0 multiplies the raw codes and applies the
+    """Q4_K at M <= 64 and K % 1024 == 0 multiplies the raw codes and applies the
     scales afterwards: the product of the bf16 activations and the exact
     (not bf16-rounded) Q4_K weights, up to f32 summation order."""
     got, a, w = _gemm_case(torch_cuda, qctx, synth.Q4_K, m, n, k, seed=m + n + k)
@@ -113,7 +121,7 @@ def test_qmatmul_q4k_short_m_exact_weights(torch_cuda, qctx, m, n, k):
 
 
 def test_qmatmul_short_m_one_launch_repeats(torch_cuda, qctx):
-    """The M <= 16 Q4_K / Q6_K path adds its split-K partial sums in the same
+    """The M <= 64 Q4_K / Q6_K path adds its split-K partial sums in the same
     launch, counting arrivals per output unit in counters that every call
     leaves at zero: calls in a row over different shapes, token counts and
     weights give bit-identical results to a first call, and match the
@@ -121,7 +129,8 @@ def test_qmatmul_short_m_one_launch_repeats(torch_cuda, qctx):
     Q4_K) weights."""
     torch = torch_cuda
     cases = [(synth.Q6_K, 16, 4096, 3072), (synth.Q4_K, 16, 2048, 4096), (synth.Q6_K, 5, 1024, 12288),
-             (synth.Q4_K, 1, 3072, 2048), (synth.Q6_K, 16, 4096, 3072)]
+             (synth.Q4_K, 1, 3072, 2048), (synth.Q6_K, 64, 4096, 3072), (synth.Q4_K, 40, 2048, 4096),
+             (synth.Q6_K, 17, 1024, 2048), (synth.Q6_K, 16, 4096, 3072)]
     first = {}
     for i, (t, m, n, k) in enumerate(cases * 2):
         rng = np.random.default_rng(100 + i % len(cases))

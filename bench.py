@@ -50,6 +50,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-weight-streaming", action="store_true",
                     help="skip the short-token weight-streaming measurements")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the Q8_0 dequant-GEMM sets and the multi-reference attention measurements")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB, the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc pass")
@@ -199,6 +201,12 @@ def main():
     # ---- weight streaming at short token counts (the HBM-bound regime) ----
     streaming = None if args.no_weight_streaming else weight_streaming(ctx, torch, np, qimm, synth, stream, host_w0)
 
+    # ---- the other measured configurations: Q8_0 dequant-GEMM sets, multi-reference attention ----
+    q8 = mref = None
+    if not args.no_other_configs:
+        q8 = q8_gemm_sets(ctx, torch, np, qimm, synth, stream)
+        mref = multi_ref_attention(ctx, torch, qimm, stream)
+
     # ---- CPU baseline: the oracle in candle mode on a bounded sample ----
     cpu = None
     if not args.no_cpu_baseline:
@@ -233,6 +241,8 @@ def main():
         "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},
         "roofline": roofline,
         "weight_streaming": streaming,
+        "dequant_gemm_q8_0": q8,
+        "multi_ref_attention": mref,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
@@ -273,6 +283,88 @@ def weight_streaming(ctx, torch, np, qimm, synth, stream, host_w, token_counts=(
         for W in copies:
             W.free()
     return out
+
+
+def q8_gemm_sets(ctx, torch, np, qimm, synth, stream, token_counts=(4352, 256), iters=10):
+    """Dequant-GEMM with Q8_0 weights on the fused QKV [12288 x 4096], output
+    [4096 x 4096], MLP up [16384 x 4096] and down [4096 x 16384] sets, bf16
+    activations ~ N(0, 1) of 4352 tokens (the image + prefix rows of a joint
+    pass) and of 256 tokens, bf16 output. Every call reads its weights from
+    HBM (rotating copies past the last-level cache). Device time per call from
+    HIP events on the launch stream."""
+    sets = {"qkv": (3 * HID, HID), "out": (HID, HID), "up": (16384, HID), "down": (HID, 16384)}
+    out = {}
+    sh = stream.cuda_stream
+    for name, (n, k) in sets.items():
+        rng = np.random.default_rng(77)
+        data = synth.random_blocks(rng, synth.Q8_0, n, k).tobytes()
+        wbytes = len(data)
+        copies = [ctx.upload(synth.Q8_0, n, k, data) for _ in range(int(300e6 // wbytes) + 1)]
+        for m in token_counts:
+            x = torch.randn((m, k), device="cuda").to(torch.bfloat16)
+            y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+            for W in copies:
+                ctx.qmatmul(W, x.data_ptr(), m, k, y.data_ptr(), synth.BF16, sh)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for i in range(iters):
+                ctx.qmatmul(copies[i % len(copies)], x.data_ptr(), m, k, y.data_ptr(), synth.BF16, sh)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / iters
+            tflops = 2.0 * m * n * k / ms / 1e9
+            gbps = wbytes / ms / 1e6
+            out[f"{name}_m{m}"] = {"ms": round(ms, 4), "tflops": round(tflops, 1),
+                                   "frac_bf16_peak": round(tflops / PEAK_BF16_TFLOPS, 4),
+                                   "weight_gbps": round(gbps, 1), "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4)}
+            log(f"bench: Q8_0 {name} {n}x{k} at {m} tokens: {ms:.3f} ms, {tflops:.0f} TFLOP/s, {gbps:.0f} GB/s")
+        for W in copies:
+            W.free()
+    return out
+
+
+def multi_ref_attention(ctx, torch, qimm, stream, iters=10):
+    """Joint attention of the image-conditioned multi-reference step with true
+    CFG: batch 2 (the two prompts), 32 heads x 128, 4096 image-token queries
+    over a cached 8448-token prefix (256 text + 2 x 4096 condition-image
+    tokens, one prefix per prompt) plus the 4096 own keys: 12544 keys,
+    4 B H Sq (P + S) D = 1683.6 GFLOP per call."""
+    B, P, S = 2, 8448, S_IMG
+    g = torch.Generator(device="cuda").manual_seed(5)
+    kv = ctx.kv_create(1, B, HEADS, P)
+    k = torch.randn((B, HEADS, P, HD), generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn((B, HEADS, P, HD), generator=g, device="cuda").to(torch.bfloat16)
+    kv.store(0, k.data_ptr(), v.data_ptr(), stream.cuda_stream)
+    del k, v
+    q = torch.randn((B, HEADS, S, HD), generator=g, device="cuda").to(torch.bfloat16)
+    ko = torch.randn((B, HEADS, S, HD), generator=g, device="cuda").to(torch.bfloat16)
+    vto = torch.randn((B, HEADS, HD, S), generator=g, device="cuda").to(torch.bfloat16)
+    o = torch.empty((B, S, HEADS * HD), device="cuda", dtype=torch.bfloat16)
+    scale = HD ** -0.5
+
+    def call():
+        ctx.attention(q.data_ptr(), B, HEADS, S, kv, 0, ko.data_ptr(), vto.data_ptr(), S, scale, o.data_ptr(),
+                      stream.cuda_stream)
+
+    for _ in range(3):
+        call()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(iters):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    assert torch.isfinite(o.float()).all().item(), "non-finite attention output"
+    kv.free()
+    flop = 4.0 * B * HEADS * S * (P + S) * HD
+    tflops = flop / ms / 1e9
+    log(f"bench: multi-reference attention (B=2, 12544 keys): {ms:.3f} ms, {tflops:.0f} TFLOP/s")
+    return {"ms": round(ms, 4), "gflop": round(flop / 1e9, 1), "tflops": round(tflops, 1),
+            "frac_bf16_peak": round(tflops / PEAK_BF16_TFLOPS, 4), "batch": B, "prefix_tokens": P,
+            "own_tokens": S, "keys": P + S}
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_block_q4km_1024.json")

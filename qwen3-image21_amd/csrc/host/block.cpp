@@ -210,13 +210,13 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
     uint16_t *xn = (uint16_t *)(ws + o_xn), *qb = (uint16_t *)(ws + o_q);
     uint16_t *kb = k_out ? k_out : (uint16_t *)(ws + o_k);
     uint16_t *vt = (uint16_t *)(ws + o_vt), *att = (uint16_t *)(ws + o_att), *hm = (uint16_t *)(ws + o_h);
-    // split-K scratch of the short-M GEMM path, sized for the largest projection
+    // split-K scratch of the short- and mid-M GEMM paths, sized for the
+    // largest projection
     size_t part_need = 0;
     {
         const qimm_weight *ws_list[] = {blk->qkv, blk->q, blk->k, blk->v, blk->out, blk->gate_up, blk->down};
         for (const qimm_weight *wt : ws_list)
-            if (wt && qimm::qgemm_stream_fits(wt->gw, M))
-                part_need = std::max(part_need, qimm::qgemm_stream_workspace(wt->gw, M));
+            if (wt) part_need = std::max(part_need, qimm::qgemm_workspace(wt->gw, M));
     }
     if (part_need) {
         rc = ensure_part_workspace(ctx, part_need);

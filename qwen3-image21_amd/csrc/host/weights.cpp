@@ -210,8 +210,7 @@ int qimm_qmatmul(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_
     qimm::EpiParams ep{};
     ep.out = y;
     ep.ldo = w->rows;
-    if (qimm::qgemm_stream_fits(w->gw, m)) {
-        const size_t need = qimm::qgemm_stream_workspace(w->gw, m);
+    if (const size_t need = qimm::qgemm_workspace(w->gw, m)) {
         QIMM_HIP(ctx, hipSetDevice(ctx->device));
         const int rc = qimm_host::ensure_part_workspace(ctx, need);
         if (rc) return rc;

@@ -79,6 +79,17 @@ hipError_t launch_qgemm_stream(const GemmWeight &w, const uint16_t *a, int64_t m
                                const EpiParams &ep, float *work, hipStream_t stream);
 hipError_t launch_qgemm_large(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda,
                               int epi, const EpiParams &ep, hipStream_t stream);
+// Sum of split-K partials part[splits][m][N] (f32) in split order, with the
+// epilogue epi applied (the second kernel of the split paths).
+hipError_t launch_split_epilogue(const float *part, int splits, int64_t m, int64_t N, int epi, const EpiParams &ep,
+                                 hipStream_t stream);
+// K split of the 128x128 kernel (64 < M < 512) when its tiles alone leave CUs
+// idle; 1 = no split.
+int qgemm_mid_splits(const GemmWeight &w, int64_t m);
+// Scratch bytes launch_qgemm may use for (w, m) through EpiParams::part_ws
+// (0 = none): the short-M path's, or the split 128x128 path's partial sums,
+// each after STREAM_COUNTER_BYTES of counters. Without it the unsplit kernels run.
+size_t qgemm_workspace(const GemmWeight &w, int64_t m);
 
 // Exact GGUF dequantization of raw block bytes (device) to f32 (device).
 hipError_t launch_dequant(int ggml_type, const uint8_t *src, int64_t n, float *out,

@@ -162,7 +162,10 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(const uint16_t *__restric
     const int wm = wave >> 1, wn = wave & 1;
     const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
     const int64_t K = w.k;
-    const int KT = (int)(K / BK);
+    // split K (gridDim.z > 1): this workgroup covers k steps [kt0, kt0 + KT)
+    // and writes its f32 partial sums to slice blockIdx.z of ep.out
+    const int KT = (int)(K / BK / gridDim.z);
+    const int kt0 = (int)blockIdx.z * KT;
 
     // loader roles
     const int a_row = tid >> 3, a_kc = (tid & 7) * 8;
@@ -192,15 +195,15 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(const uint16_t *__restric
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-    load_a(0);
-    load_w<FMT>(w, n0 + w_nl, 0, w_h, rw);
+    load_a((int64_t)kt0 * BK);
+    load_w<FMT>(w, n0 + w_nl, (int64_t)kt0 * BK, w_h, rw);
     store_a(lds);
-    store_w<FMT>(lds + 128 * LP, w_nl, w_h, 0, rw);
+    store_w<FMT>(lds + 128 * LP, w_nl, w_h, (int64_t)kt0 * BK, rw);
     __syncthreads();
 
-    for (int kt = 0; kt < KT; kt++) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < KT;
+    for (int kt = kt0; kt < kt0 + KT; kt++) {
+        const int cur = (kt - kt0) & 1;
+        const bool more = kt + 1 < kt0 + KT;
         if (more) {
             load_a((int64_t)(kt + 1) * BK);
             load_w<FMT>(w, n0 + w_nl, (int64_t)(kt + 1) * BK, w_h, rw);
@@ -255,7 +258,7 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(const uint16_t *__restric
             f32x4 v0 = *(const f32x4 *)(cs + row * CP + cg);
             f32x4 v1 = *(const f32x4 *)(cs + row * CP + cg + 4);
             if constexpr (EPI == EPI_F32) {
-                float *o = (float *)ep.out + m * ep.ldo + n0 + cg;
+                float *o = (float *)ep.out + (int64_t)blockIdx.z * M * ep.ldo + m * ep.ldo + n0 + cg;
                 *(f32x4 *)o = v0;
                 *(f32x4 *)(o + 4) = v1;
             } else if constexpr (EPI == EPI_BF16) {
@@ -372,8 +375,8 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(const uint16_t *__restric
 
 template <int FMT>
 hipError_t launch_fmt(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
-                      const EpiParams &ep, hipStream_t stream) {
-    dim3 grid((unsigned)(w.n / BN), (unsigned)((m + BM - 1) / BM));
+                      const EpiParams &ep, hipStream_t stream, int splits = 1) {
+    dim3 grid((unsigned)(w.n / BN), (unsigned)((m + BM - 1) / BM), (unsigned)splits);
     dim3 block(256);
     switch (epi) {
     case EPI_F32: qgemm_kernel<FMT, EPI_F32><<<grid, block, 0, stream>>>(a, m, lda, w, ep); break;
@@ -386,7 +389,50 @@ hipError_t launch_fmt(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t
     return hipGetLastError();
 }
 
+int device_cus() {
+    static int cus = -1;
+    if (cus < 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+            cus = v;
+        else
+            cus = 0;
+    }
+    return cus;
+}
+
+hipError_t launch_any(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi, const EpiParams &ep,
+                      hipStream_t stream, int splits) {
+    switch (w.fmt) {
+    case WF_Q8_0: return launch_fmt<WF_Q8_0>(w, a, m, lda, epi, ep, stream, splits);
+    case WF_Q4_K: return launch_fmt<WF_Q4_K>(w, a, m, lda, epi, ep, stream, splits);
+    case WF_Q6_K: return launch_fmt<WF_Q6_K>(w, a, m, lda, epi, ep, stream, splits);
+    case WF_BF16: return launch_fmt<WF_BF16>(w, a, m, lda, epi, ep, stream, splits);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 }  // namespace
+
+// K split of the 128x128 kernel when its tiles alone would leave CUs idle:
+// doubled (up to 8) while the grid is under one workgroup per CU and each
+// share stays a whole number of 512-value groups. The partial sums cost
+// 8 s m N bytes of traffic (written once, read once); at these token counts
+// an idle CU costs more.
+int qgemm_mid_splits(const GemmWeight &w, int64_t m) {
+    if (m <= 0 || qgemm_large_fits(w, m) || qgemm_stream_fits(w, m)) return 1;
+    const int64_t tiles = (w.n / BN) * ((m + BM - 1) / BM), cus = device_cus();
+    int s = 1;
+    while (s < 8 && tiles * s < cus && w.k % (512 * 2 * s) == 0) s *= 2;
+    return s;
+}
+
+size_t qgemm_workspace(const GemmWeight &w, int64_t m) {
+    if (qgemm_large_fits(w, m)) return 0;
+    if (qgemm_stream_fits(w, m)) return qgemm_stream_workspace(w, m);
+    const int s = qgemm_mid_splits(w, m);
+    return s > 1 ? STREAM_COUNTER_BYTES + (size_t)s * (size_t)m * (size_t)w.n * 4 : 0;
+}
 
 hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
                         const EpiParams &ep, hipStream_t stream) {
@@ -394,13 +440,19 @@ hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64
     if (qgemm_large_fits(w, m)) return launch_qgemm_large(w, a, m, lda, epi, ep, stream);
     if (qgemm_stream_fits(w, m) && ep.part_ws && ep.part_ws_bytes >= qgemm_stream_workspace(w, m))
         return launch_qgemm_stream(w, a, m, lda, epi, ep, ep.part_ws, stream);
-    switch (w.fmt) {
-    case WF_Q8_0: return launch_fmt<WF_Q8_0>(w, a, m, lda, epi, ep, stream);
-    case WF_Q4_K: return launch_fmt<WF_Q4_K>(w, a, m, lda, epi, ep, stream);
-    case WF_Q6_K: return launch_fmt<WF_Q6_K>(w, a, m, lda, epi, ep, stream);
-    case WF_BF16: return launch_fmt<WF_BF16>(w, a, m, lda, epi, ep, stream);
-    default: return hipErrorInvalidValue;
+    const int splits = qgemm_mid_splits(w, m);
+    if (splits > 1 && ep.part_ws && ep.part_ws_bytes >= qgemm_workspace(w, m)) {
+        // partial sums [splits][m][n] after the counter area, then the fixed-order
+        // reduction that applies the epilogue
+        float *part = (float *)((char *)ep.part_ws + STREAM_COUNTER_BYTES);
+        EpiParams pe{};
+        pe.out = part;
+        pe.ldo = w.n;
+        const hipError_t e = launch_any(w, a, m, lda, EPI_F32, pe, stream, splits);
+        if (e != hipSuccess) return e;
+        return launch_split_epilogue(part, splits, m, w.n, epi, ep, stream);
     }
+    return launch_any(w, a, m, lda, epi, ep, stream, 1);
 }
 
 }  // namespace qimm

@@ -957,7 +957,11 @@ hipError_t launch_qgemm_stream(const GemmWeight &w, const uint16_t *a, int64_t m
     default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess) return e;
-    const int64_t N = w.n;
+    return launch_split_epilogue(part, splits, m, w.n, epi, ep, stream);
+}
+
+hipError_t launch_split_epilogue(const float *part, int splits, int64_t m, int64_t N, int epi, const EpiParams &ep,
+                                 hipStream_t stream) {
     const int64_t elems = epi == EPI_SWIGLU ? m * N / 2 : m * N;
     const dim3 grid((unsigned)((elems + 255) / 256)), block(256);
     switch (epi) {

@@ -171,6 +171,26 @@ def test_block_hidden4096_short_m(torch_cuda, qctx, b, s, p, mlp):
         assert cos_sim(v, vv) >= 0.9999 and max_abs_rel(v, vv) <= 2e-2
 
 
+@pytest.mark.parametrize("attn_type,down_type", [(synth.Q8_0, synth.Q8_0), (synth.Q4_K, synth.Q6_K)])
+def test_block_mid_m_split_k(torch_cuda, qctx, attn_type, down_type):
+    """Hidden 1024 (8 heads), MLP 2048, 128 tokens over a 16-token prefix: every
+    projection's 128x128 tiles leave CUs idle, so each runs split over K (2 or
+    4 shares) with its partial sums added by the q/k/v, SwiGLU and residual
+    epilogues of the reduction kernel."""
+    cfg = dict(hidden=1024, heads=8, head_dim=128, mlp=2048)
+    w, x, mod, pe, kpre, vpre = make_case(31, cfg, 1, 128, 16, attn_type, down_type)
+    got, (k, v) = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)
+    ref, kr, vr = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
+    check(got, ref, x)
+    ref_e, kre, vre = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
+    check(got, ref_e, x, exact=True)
+    for kk, vv in ((kr, vr), (kre, vre)):
+        assert cos_sim(k, kk) >= 0.9999 and max_abs_rel(k, kk) <= 2e-2
+        assert cos_sim(v, vv) >= 0.9999 and max_abs_rel(v, vv) <= 2e-2
+    again, _ = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
+    assert np.array_equal(got, again)
+
+
 def test_block_rejects_bad_config(torch_cuda, qctx):
     keep = []
     w = synth.block_weights(1, 256, 2, 768, synth.Q8_0)

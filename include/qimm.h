@@ -58,7 +58,11 @@ typedef struct qimm_kv qimm_kv;
 /* ---------------- context ---------------- */
 
 /* One device context. Stands in for candle's Device handle as selected in
- * src/main.rs:159-162 and owned per worker thread (src/server.rs:123-155). */
+ * src/main.rs:159-162 and owned per worker thread (src/server.rs:123-155).
+ * Calls through one context share its device scratch (block intermediates,
+ * split-K partial sums and their arrival counters), so they must not overlap
+ * on the device: issue them from one thread on one stream, or order the
+ * streams with events. Separate contexts are independent. */
 int qimm_ctx_create(int device, qimm_ctx **out);
 int qimm_ctx_destroy(qimm_ctx *ctx);
 /* Message of the last failed call on ctx (mirrors candle's bail! text,

@@ -427,17 +427,37 @@ int qgemm_mid_splits(const GemmWeight &w, int64_t m) {
     return s;
 }
 
-size_t qgemm_workspace(const GemmWeight &w, int64_t m) {
-    if (qgemm_large_fits(w, m)) return 0;
-    if (qgemm_stream_fits(w, m)) return qgemm_stream_workspace(w, m);
+namespace {
+
+// Rows of a large-M product handed to the shorter-M paths so that the 256x256
+// kernel runs whole waves: when the 256x256 tiles leave a last, partial wave
+// of at most a quarter of the CUs made of whole 256-row tile rows (4352 tokens
+// x N = 4096: 272 tiles for 256 CUs), those rows go to the split-K 128x128
+// kernel (or the short-M path) instead. Plain outputs only (their rows are
+// independent of the token index); 0 = none.
+int64_t large_tail_rows(const GemmWeight &w, int64_t m) {
+    if (!qgemm_large_fits(w, m)) return 0;
+    const int64_t mt = (m + 255) / 256, nt = w.n / 256, tiles = mt * nt, cus = device_cus();
+    const int64_t r = cus > 0 ? tiles % cus : 0;
+    if (tiles <= cus || r == 0 || r > cus / 4 || r % nt) return 0;
+    const int64_t tail = m - (mt - r / nt) * 256;
+    return (tail < 512 && m - tail >= 512) ? tail : 0;
+}
+
+size_t mid_workspace(const GemmWeight &w, int64_t m) {
     const int s = qgemm_mid_splits(w, m);
     return s > 1 ? STREAM_COUNTER_BYTES + (size_t)s * (size_t)m * (size_t)w.n * 4 : 0;
 }
 
-hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
-                        const EpiParams &ep, hipStream_t stream) {
-    if (m <= 0) return hipSuccess;
-    if (qgemm_large_fits(w, m)) return launch_qgemm_large(w, a, m, lda, epi, ep, stream);
+size_t small_workspace(const GemmWeight &w, int64_t m) {
+    return qgemm_stream_fits(w, m) ? qgemm_stream_workspace(w, m) : mid_workspace(w, m);
+}
+
+// M < 512: the short-M path when it fits and its scratch is there, else the
+// 128x128 kernel, split over K when its tiles leave CUs idle and scratch is
+// there.
+hipError_t launch_small(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi, const EpiParams &ep,
+                        hipStream_t stream) {
     if (qgemm_stream_fits(w, m) && ep.part_ws && ep.part_ws_bytes >= qgemm_stream_workspace(w, m))
         return launch_qgemm_stream(w, a, m, lda, epi, ep, ep.part_ws, stream);
     const int splits = qgemm_mid_splits(w, m);
@@ -453,6 +473,34 @@ hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64
         return launch_split_epilogue(part, splits, m, w.n, epi, ep, stream);
     }
     return launch_any(w, a, m, lda, epi, ep, stream, 1);
+}
+
+}  // namespace
+
+size_t qgemm_workspace(const GemmWeight &w, int64_t m) {
+    if (qgemm_large_fits(w, m)) {
+        const int64_t tail = large_tail_rows(w, m);
+        return tail ? small_workspace(w, tail) : 0;
+    }
+    return small_workspace(w, m);
+}
+
+hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
+                        const EpiParams &ep, hipStream_t stream) {
+    if (m <= 0) return hipSuccess;
+    if (qgemm_large_fits(w, m)) {
+        const int64_t tail = (epi == EPI_F32 || epi == EPI_BF16) ? large_tail_rows(w, m) : 0;
+        if (tail && ep.part_ws && ep.part_ws_bytes >= small_workspace(w, tail)) {
+            const int64_t head = m - tail;
+            const hipError_t e = launch_qgemm_large(w, a, head, lda, epi, ep, stream);
+            if (e != hipSuccess) return e;
+            EpiParams et = ep;
+            et.out = (char *)ep.out + (size_t)head * (size_t)ep.ldo * (epi == EPI_F32 ? 4 : 2);
+            return launch_small(w, a + head * lda, tail, lda, epi, et, stream);
+        }
+        return launch_qgemm_large(w, a, m, lda, epi, ep, stream);
+    }
+    return launch_small(w, a, m, lda, epi, ep, stream);
 }
 
 }  // namespace qimm

@@ -180,6 +180,36 @@ def test_qmatmul_full_qkv_shape_sampled_rows(torch_cuda, qctx):
     W.free()
 
 
+@pytest.mark.parametrize("m,n,k,t,out", [(4352, 4096, 4096, synth.Q4_K, synth.BF16),   # tail: split 128x128
+                                         (4136, 4096, 4096, synth.Q4_K, synth.F32),    # tail: 40-row streaming
+                                         (4352, 4096, 2048, synth.Q8_0, synth.BF16)])
+def test_qmatmul_large_m_tail_rows(torch_cuda, qctx, m, n, k, t, out):
+    """Large-M products whose last 256x256 tile row would run as a nearly empty
+    wave hand those rows to the shorter-M paths (plain outputs): sampled head
+    rows and every tail row match the products of the bf16 activations and
+    the weights each path multiplies (bf16-rounded, or exact on the Q4_K
+    code-product path), and the seam rows are continuous."""
+    torch = torch_cuda
+    rng = np.random.default_rng(m + k + t)
+    _, w, _, _ = synth.weight(rng, t, n, k)
+    W = qctx.upload(t, n, k, w.tobytes())
+    a_dev, a = bf16_dev(torch, rng.standard_normal((m, k)).astype(np.float32))
+    y = torch.empty((m, n), dtype=torch.float32 if out == synth.F32 else torch.bfloat16, device="cuda")
+    qctx.qmatmul(W, a_dev.data_ptr(), m, k, y.data_ptr(), out, stream(torch))
+    got = host(y.float())
+    W.free()
+    rows = np.concatenate([np.arange(0, 8), rng.choice(4096, 24, replace=False), np.arange(4090, m)])
+    Wd = O.dequantize(t, w, n * k).reshape(n, k).astype(np.float64)
+    Wb = O.bf16_round(Wd.astype(np.float32)).astype(np.float64)
+    ar = a[rows].astype(np.float64)
+    want_b, want_e = ar @ Wb.T, ar @ Wd.T
+    scale = np.abs(ar) @ np.abs(Wb).T
+    tol = 2e-4 * scale + 1e-6 + (4e-3 * np.abs(want_e) if out == synth.BF16 else 0)
+    err = np.minimum(np.abs(got[rows] - want_b), np.abs(got[rows] - want_e))
+    assert np.all(err <= tol), (rows[np.argmax((err - tol).max(axis=1))], float((err / (scale + 1e-9)).max()))
+    assert np.isfinite(got).all()
+
+
 def test_qmatmul_rejects_bad_shapes(torch_cuda, qctx):
     import qimm
     rng = np.random.default_rng(8)

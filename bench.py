@@ -285,11 +285,12 @@ def weight_streaming(ctx, torch, np, qimm, synth, stream, host_w, token_counts=(
     return out
 
 
-def q8_gemm_sets(ctx, torch, np, qimm, synth, stream, token_counts=(4352, 256), iters=10):
+def q8_gemm_sets(ctx, torch, np, qimm, synth, stream, token_counts=(4352, 256, 64, 16), iters=10):
     """Dequant-GEMM with Q8_0 weights on the fused QKV [12288 x 4096], output
     [4096 x 4096], MLP up [16384 x 4096] and down [4096 x 16384] sets, bf16
     activations ~ N(0, 1) of 4352 tokens (the image + prefix rows of a joint
-    pass) and of 256 tokens, bf16 output. Every call reads its weights from
+    pass) and of 256, 64 and 16 tokens (the weight-bandwidth regime), bf16
+    output. Every call reads its weights from
     HBM (rotating copies past the last-level cache). Device time per call from
     HIP events on the launch stream."""
     sets = {"qkv": (3 * HID, HID), "out": (HID, HID), "up": (16384, HID), "down": (HID, 16384)}

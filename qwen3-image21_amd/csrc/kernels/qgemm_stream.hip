@@ -2,8 +2,9 @@
 // C = A (bf16, M x K) x W^T (GGUF blocks, N x K). At these sizes the time is
 // the weight bytes over HBM bandwidth, so the kernels are shaped for streaming.
 //
-// Q4_K and Q6_K with K % 1024 == 0 take the one-launch kernel in namespace ws
-// (its description is there). Everything else takes the split-K kernel:
+// Q4_K, Q6_K and Q8_0 with K % 1024 == 0 take the one-launch kernel in
+// namespace ws (its description is there). Everything else takes the split-K
+// kernel:
 //  - 64 weight rows x one K chunk per workgroup (4 waves x 16 rows), the K
 //    range split over workgroups so that the grid holds several workgroups per
 //    CU; partial sums go to an f32 workspace [split][M][N] and a second kernel
@@ -303,7 +304,7 @@ int device_cus() {
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
 // ---------------------------------------------------------------------------
-// M <= 64, Q4_K / Q6_K, K % 1024 == 0: one launch per product.
+// M <= 64, Q4_K / Q6_K / Q8_0, K % 1024 == 0: one launch per product.
 //
 // Work item = (16-row weight group g, 1024-wide k chunk c) = four (group,
 // super-block) tiles, contiguous in the device layout, against MT = 1, 2 or 4
@@ -347,7 +348,8 @@ struct Plan {
 };
 
 bool plan(const GemmWeight &w, int64_t m, int epi, int cus, Plan &p) {
-    if ((w.fmt != WF_Q4_K && w.fmt != WF_Q6_K) || m < 1 || m > 64 || w.k % KCH || w.n % 16 || cus <= 0)
+    if ((w.fmt != WF_Q4_K && w.fmt != WF_Q6_K && w.fmt != WF_Q8_0) || m < 1 || m > 64 || w.k % KCH || w.n % 16 ||
+        cus <= 0)
         return false;
     if ((epi == EPI_SWIGLU || epi == EPI_QKV) && w.n % 128) return false;
     p.MT = m <= 16 ? 1 : m <= 32 ? 2 : 4;
@@ -377,8 +379,25 @@ struct TileQ6 {
     uint32_t d;
 };
 
+struct TileQ8 {
+    u32x4 c[4], s;
+};
+
 template <int FMT>
-using Tile = typename std::conditional<FMT == WF_Q4_K, TileQ4, TileQ6>::type;
+using Tile = typename std::conditional<FMT == WF_Q4_K, TileQ4,
+                                       typename std::conditional<FMT == WF_Q6_K, TileQ6, TileQ8>::type>::type;
+
+// Q8_0 (device layout: codes [N][K], f16 scales [N][K/32]): lane kg holds the
+// 16-code pieces at k = 64 q + 16 kg (q < 4) of its row and the row's 8
+// scales of the super-block-sized tile.
+__device__ __forceinline__ void load_tile(const GemmWeight &w, int64_t g, int64_t sb, int64_t SB, int l16, int kg,
+                                          TileQ8 &r) {
+    const int64_t n = 16 * g + l16, K = SB * 256;
+    const uint8_t *p = w.q + n * K + sb * 256 + 16 * kg;
+#pragma unroll
+    for (int q = 0; q < 4; q++) r.c[q] = *(const u32x4 *)(p + 64 * q);
+    r.s = *(const u32x4 *)(w.scales + n * (K / 32) + sb * 8);
+}
 
 __device__ __forceinline__ void load_tile(const GemmWeight &w, int64_t g, int64_t sb, int64_t SB, int l16, int kg,
                                           TileQ4 &r) {
@@ -421,6 +440,38 @@ __device__ __forceinline__ void pin(TileQ6 &r) {
 }
 __device__ __forceinline__ void pin(TileQ4 &r) {
     asm volatile("" : "+v"(r.h), "+v"(r.q[0]), "+v"(r.q[1]), "+v"(r.q[2]), "+v"(r.q[3]));
+}
+__device__ __forceinline__ void pin(TileQ8 &r) {
+    asm volatile("" : "+v"(r.c[0]), "+v"(r.c[1]), "+v"(r.c[2]), "+v"(r.c[3]), "+v"(r.s));
+}
+
+// One Q8_0 tile into acc[0..MT). Step s = 2 q + h: the lane's 8 codes
+// k = 64 q + 16 kg + 8 h + i, all in 32-value block 2 q + kg / 2; codes biased
+// to unsigned (q + 128) sit in f16 halves as subnormals, one v_fma_mix each
+// gives (q + 128) d - 128 d = q d exactly, then RNE to bf16.
+template <int MT>
+__device__ __forceinline__ void tile_q8(TileQ8 r, const uint8_t *xrow, int kg, f32x4 *acc) {
+    pin(r);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        // block 2 q + kg / 2: its scale is half kg / 2 of scale word q
+        const uint32_t sw = (kg >> 1) ? (r.s[q] >> 16) : (r.s[q] & 0xffffu);
+        const float d = m16::cvt_f16_lo(sw);
+        const float a = d * 0x1p24f, b = -128.f * d;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t u0 = r.c[q][2 * h] ^ 0x80808080u, u1 = r.c[q][2 * h + 1] ^ 0x80808080u;
+            const uint32_t p0 = u0 & 0x00FF00FFu, p1 = __builtin_amdgcn_perm(0u, u0, 0x0C030C01u);
+            const uint32_t p2 = u1 & 0x00FF00FFu, p3 = __builtin_amdgcn_perm(0u, u1, 0x0C030C01u);
+            const u32x4 bw = {pack_bf16x2(mix_lo(p0, a, b), mix_lo(p1, a, b)), pack_bf16x2(mix_hi(p0, a, b), mix_hi(p1, a, b)),
+                              pack_bf16x2(mix_lo(p2, a, b), mix_lo(p3, a, b)), pack_bf16x2(mix_hi(p2, a, b), mix_hi(p3, a, b))};
+#pragma unroll
+            for (int tt = 0; tt < MT; tt++) {
+                const bf16x8 av = *(const bf16x8 *)(xrow + tt * 16 * XROW + 128 * q + 32 * kg + 16 * h);
+                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bw), acc[tt], 0, 0, 0);
+            }
+        }
+    }
 }
 
 // One Q6_K tile (16 rows x 256 k) into acc[0..MT) (token tiles 16 tt + l16
@@ -684,7 +735,7 @@ __global__ __launch_bounds__(64 * nwaves(MT), wg_per_cu(MT) * nwaves(MT) / 4) vo
     }
     // the x pieces were issued before the tiles: wait for them alone, then for
     // every wave's pieces
-    constexpr int TL = FMT == WF_Q4_K ? 5 : 6;  // loads per tile
+    constexpr int TL = FMT == WF_Q6_K ? 6 : 5;  // loads per tile
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(SBC * TL) : "memory");
 
     const uint8_t *xrow = xs + l16 * XROW;
@@ -728,7 +779,8 @@ __global__ __launch_bounds__(64 * nwaves(MT), wg_per_cu(MT) * nwaves(MT) / 4) vo
 #pragma unroll
         for (int t = 0; t < SBC; t++) {
             if constexpr (FMT == WF_Q4_K) tile_q4<MT>(ring[t], xrow + 512 * t, kg, xq0[t], xq1[t], acc, accM);
-            else tile_q6<MT>(ring[t], xrow + 512 * t, kg, acc);
+            else if constexpr (FMT == WF_Q6_K) tile_q6<MT>(ring[t], xrow + 512 * t, kg, acc);
+            else tile_q8<MT>(ring[t], xrow + 512 * t, kg, acc);
             // finish this tile's arithmetic here: left alone, the compiler sinks
             // it past the loads and keeps every tile's products live
 #pragma unroll
@@ -944,8 +996,11 @@ hipError_t launch_qgemm_stream(const GemmWeight &w, const uint16_t *a, int64_t m
     float *part = (float *)((char *)work + STREAM_COUNTER_BYTES);
     ws::Plan wp;
     if (ws::plan(w, m, epi, m16::device_cus(), wp)) {
-        return w.fmt == WF_Q4_K ? ws::launch<WF_Q4_K>(w, a, (int)m, lda, epi, ep, part, counters, wp, stream)
-                                : ws::launch<WF_Q6_K>(w, a, (int)m, lda, epi, ep, part, counters, wp, stream);
+        switch (w.fmt) {
+        case WF_Q4_K: return ws::launch<WF_Q4_K>(w, a, (int)m, lda, epi, ep, part, counters, wp, stream);
+        case WF_Q6_K: return ws::launch<WF_Q6_K>(w, a, (int)m, lda, epi, ep, part, counters, wp, stream);
+        default: return ws::launch<WF_Q8_0>(w, a, (int)m, lda, epi, ep, part, counters, wp, stream);
+        }
     }
     const int splits = qgemm_stream_splits(w, m);
     hipError_t e;

@@ -121,16 +121,17 @@ def test_qmatmul_q4k_short_m_exact_weights(torch_cuda, qctx, m, n, k):
 
 
 def test_qmatmul_short_m_one_launch_repeats(torch_cuda, qctx):
-    """The M <= 64 Q4_K / Q6_K path adds its split-K partial sums in the same
-    launch, counting arrivals per output unit in counters that every call
-    leaves at zero: calls in a row over different shapes, token counts and
+    """The M <= 64 Q4_K / Q6_K / Q8_0 path adds its split-K partial sums in
+    the same launch, counting arrivals per output unit in counters that every
+    call leaves at zero: calls in a row over different shapes, token counts and
     weights give bit-identical results to a first call, and match the
-    products of the bf16 activations and the (bf16-rounded for Q6_K, exact for
-    Q4_K) weights."""
+    products of the bf16 activations and the (bf16-rounded for Q6_K and Q8_0,
+    exact for Q4_K) weights."""
     torch = torch_cuda
     cases = [(synth.Q6_K, 16, 4096, 3072), (synth.Q4_K, 16, 2048, 4096), (synth.Q6_K, 5, 1024, 12288),
              (synth.Q4_K, 1, 3072, 2048), (synth.Q6_K, 64, 4096, 3072), (synth.Q4_K, 40, 2048, 4096),
-             (synth.Q6_K, 17, 1024, 2048), (synth.Q6_K, 16, 4096, 3072)]
+             (synth.Q6_K, 17, 1024, 2048), (synth.Q8_0, 16, 4096, 4096), (synth.Q8_0, 64, 2048, 2048),
+             (synth.Q8_0, 3, 1024, 16384), (synth.Q6_K, 16, 4096, 3072)]
     first = {}
     for i, (t, m, n, k) in enumerate(cases * 2):
         rng = np.random.default_rng(100 + i % len(cases))
@@ -147,7 +148,7 @@ def test_qmatmul_short_m_one_launch_repeats(torch_cuda, qctx):
             continue
         first[key] = got
         Wd = O.dequantize(t, w, n * k).reshape(n, k)
-        if t == synth.Q6_K:
+        if t != synth.Q4_K:
             Wd = O.bf16_round(Wd)
         want = a.astype(np.float64) @ Wd.astype(np.float64).T
         scale = np.abs(a).astype(np.float64) @ np.abs(Wd).astype(np.float64).T

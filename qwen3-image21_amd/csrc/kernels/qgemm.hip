@@ -415,7 +415,8 @@ hipError_t launch_any(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t
 }  // namespace
 
 // K split of the 128x128 kernel when its tiles alone would leave CUs idle:
-// doubled (up to 8) while the grid is under one workgroup per CU and each
+// doubled (up to 8) while the doubled grid still fits the two resident
+// workgroups per CU (a second one hides the first one's load waits) and each
 // share stays a whole number of 512-value groups. The partial sums cost
 // 8 s m N bytes of traffic (written once, read once); at these token counts
 // an idle CU costs more.
@@ -423,7 +424,7 @@ int qgemm_mid_splits(const GemmWeight &w, int64_t m) {
     if (m <= 0 || qgemm_large_fits(w, m) || qgemm_stream_fits(w, m)) return 1;
     const int64_t tiles = (w.n / BN) * ((m + BM - 1) / BM), cus = device_cus();
     int s = 1;
-    while (s < 8 && tiles * s < cus && w.k % (512 * 2 * s) == 0) s *= 2;
+    while (s < 8 && tiles * 2 * s <= 2 * cus && w.k % (512 * 2 * s) == 0) s *= 2;
     return s;
 }
 

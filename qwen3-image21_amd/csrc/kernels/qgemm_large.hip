@@ -438,68 +438,69 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
         const int64_t H = ep.heads;
         const int64_t mw = m0 + wm * 128;  // first row of this wave
         if (sec < 2) {
+            // q/k: RMSNorm over the head's 128 columns, RoPE on (2i, 2i+1), q
+            // also scaled, bf16 rows to [B,H,S,128]; one 64-row half at a
+            // time with one token row per lane. The half's accumulators go to
+            // this wave's 32 KB of LDS as f32 [column][row] in 16 B pieces of
+            // 4 rows (piece p of column c at slot p ^ (c & 15): conflict free
+            // for the 16 B writes and for the 4 B reads of one row by 64
+            // lanes), then each lane reads its row back, so the row reduction
+            // and the RoPE partner stay inside the lane. The code stays
+            // compact: the same work done in the accumulator layout unrolls to
+            // ~10K instructions that stream through the instruction cache once
+            // per tile.
+            float *ft = (float *)lds + wave * 64 * 128;
             const float *nwt = sec == 0 ? ep.norm_q : ep.norm_k;
             const float osc = sec == 0 ? ep.q_scale : 1.0f;
-            float wq[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) wq[j] = nwt[j * 32 + l32];
-            const bool odd = lane & 1;
+            uint16_t *dst = sec == 0 ? ep.q : ep.k;
             const uint32_t Su = (uint32_t)S, Mlast = (uint32_t)(M - 1);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                // per 32 rows: the RoPE (cos, sin) pairs of all 16 x 4 elements
-                // first, then the 16 sums of squares reduced over their 32
-                // lanes together, so loads and cross-lane steps overlap
-                float2 cs[16][4];
+            for (int h = 0; h < 2; h++) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const uint32_t t = (uint32_t)(i * 32 + 8 * (r >> 2) + 4 * g + (r & 3));
-                    const uint32_t s = min((uint32_t)mw + t, Mlast) % Su;
-                    const float *pr = ep.pe + (int64_t)s * 128;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) cs[r][j] = *(const float2 *)(pr + ((j * 32 + l32) & ~1));
-                }
-                float ss[16];
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    ss[r] = 0.f;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) ss[r] += acc[i][j][r] * acc[i][j][r];
-                }
-#pragma unroll
-                for (int o = 16; o > 0; o >>= 1)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) ss[r] += __shfl_xor(ss[r], o);
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int t = i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    const float rs = 1.0f / sqrtf(ss[r] * (1.0f / 128.0f) + 1e-6f);
+                for (int ii = 0; ii < 2; ii++)
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         const int c = j * 32 + l32;
-                        const float x = acc[i][j][r] * rs * wq[j];
-                        // RoPE partner column c ^ 1 = lane ^ 1 (DPP quad_perm [1,0,3,2])
-                        const float xp = __builtin_bit_cast(
-                            float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
-                        const float cs_ = cs[r][j].x, sn = cs[r][j].y;
-                        // even column: x0 c - x1 s; odd column: x0 s + x1 c (x0 is the partner)
-                        const float y = (odd ? xp * sn + x * cs_ : x * cs_ - xp * sn) * osc;
-                        tile[t * 128 + (c ^ ((t & 7) << 3))] = (uint16_t)(pack_bf16x2(y, 0.f) & 0xffffu);
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const int p = ii * 8 + 2 * q + g;  // rows 4p .. 4p+3 of the half
+                            const int a = 2 * h + ii;
+                            *(f32x4 *)(ft + c * 64 + ((p ^ (c & 15)) << 2)) =
+                                f32x4{acc[a][j][4 * q], acc[a][j][4 * q + 1], acc[a][j][4 * q + 2],
+                                      acc[a][j][4 * q + 3]};
+                        }
                     }
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes landed
+                __builtin_amdgcn_wave_barrier();
+                float v[128], ss4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int c = 0; c < 128; c++) v[c] = ft[c * 64 + (((lane >> 2) ^ (c & 15)) << 2) + (lane & 3)];
+#pragma unroll
+                for (int c = 0; c < 128; c++) ss4[c & 3] += v[c] * v[c];
+                __builtin_amdgcn_s_waitcnt(0xc07f);
+                __builtin_amdgcn_wave_barrier();  // the half is read before the next one is written
+                const int64_t m = mw + h * 64 + lane;
+                const uint32_t mc = min((uint32_t)m, Mlast);
+                const uint32_t s = mc % Su, b = mc / Su;
+                const float rs = 1.0f / sqrtf(((ss4[0] + ss4[1]) + (ss4[2] + ss4[3])) * (1.0f / 128.0f) + 1e-6f);
+                const float *pr = ep.pe + (int64_t)s * 128;  // (cos, sin) of pair i at 2i, 2i + 1
+                uint16_t *orow = dst + (((int64_t)b * H + head) * S + s) * 128;
+#pragma unroll
+                for (int c0 = 0; c0 < 128; c0 += 8) {
+                    const f32x4 cs0 = *(const f32x4 *)(pr + c0), cs1 = *(const f32x4 *)(pr + c0 + 4);
+                    const f32x4 w0 = *(const f32x4 *)(nwt + c0), w1 = *(const f32x4 *)(nwt + c0 + 4);
+                    const float cs[8] = {cs0.x, cs0.y, cs0.z, cs0.w, cs1.x, cs1.y, cs1.z, cs1.w};
+                    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                    u32x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float x0 = v[c0 + 2 * e] * rs * wv[2 * e];
+                        const float x1 = v[c0 + 2 * e + 1] * rs * wv[2 * e + 1];
+                        const float co = cs[2 * e], sn = cs[2 * e + 1];
+                        o[e] = pack_bf16x2((x0 * co - x1 * sn) * osc, (x0 * sn + x1 * co) * osc);
+                    }
+                    if (m < M) *(u32x4 *)(orow + c0) = o;
                 }
-            }
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes landed
-            __builtin_amdgcn_wave_barrier();
-            uint16_t *dst = sec == 0 ? ep.q : ep.k;
-            // 16 lanes per row (16 x 16 B = 256 B), 4 rows per pass
-#pragma unroll 4
-            for (int pass = 0; pass < 32; pass++) {
-                const int t = pass * 4 + (lane >> 4), ch = lane & 15;
-                const int64_t m = mw + t;
-                if (m >= M) continue;
-                const u32x4 v = *(const u32x4 *)(tile + t * 128 + ((ch * 8) ^ ((t & 7) << 3)));
-                const int64_t b = m / S, s = m % S;
-                *(u32x4 *)(dst + ((b * H + head) * S + s) * 128 + ch * 8) = v;
             }
         } else {
             // V^T: tile[d][t], 8-token groups XOR-swizzled by d. Registers

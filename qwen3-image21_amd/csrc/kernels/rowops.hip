@@ -95,13 +95,16 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x
     const int tid = threadIdx.x;
     const float *xr = x + row * hidden;
     const int nv = (int)(hidden / 4);
-    f32x4 v[LN_MAXV];
+    // the modulation row is loaded with x, so its latency overlaps the row's
+    const float *sc = scale + (row / rows_per) * stride;
+    f32x4 v[LN_MAXV], sv[LN_MAXV];
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < LN_MAXV; i++) {
         const int c = tid + 256 * i;
         if (c < nv) {
             v[i] = *(const f32x4 *)(xr + 4 * c);
+            sv[i] = *(const f32x4 *)(sc + 4 * c);
             s += v[i][0] + v[i][1] + v[i][2] + v[i][3];
         }
     }
@@ -126,13 +129,12 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x
     __syncthreads();
     const float var = (red[4] + red[5] + red[6] + red[7]) / (float)hidden;
     const float rstd = 1.0f / sqrtf(var + 1e-6f);
-    const float *sc = scale + (row / rows_per) * stride;
     uint16_t *orow = out + row * hidden;
 #pragma unroll
     for (int i = 0; i < LN_MAXV; i++) {
         const int c = tid + 256 * i;
         if (c < nv) {
-            const f32x4 s4 = *(const f32x4 *)(sc + 4 * c);
+            const f32x4 s4 = sv[i];
             u32x2 pk{pack_bf16x2((v[i][0] - mean) * rstd * s4[0], (v[i][1] - mean) * rstd * s4[1]),
                      pack_bf16x2((v[i][2] - mean) * rstd * s4[2], (v[i][3] - mean) * rstd * s4[3])};
             *(u32x2 *)(orow + 4 * c) = pk;

@@ -301,7 +301,8 @@ int device_cus() {
 
 }  // namespace m16
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+// silu with the hardware reciprocal (about 1 ulp) instead of an IEEE divide
+__device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 // ---------------------------------------------------------------------------
 // M <= 64, Q4_K / Q6_K / Q8_0, K % 1024 == 0: one launch per product.

@@ -238,6 +238,15 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
                        int64_t seq, const float *mod, const float *pe, const qimm_kv *kv,
                        int64_t layer, uint16_t *k_out, uint16_t *v_out, void *stream);
 
+/* Sizes the context's device scratch for forwards of this block with up to
+ * batch x seq tokens and mod_rows modulation rows (1 or seq). A forward that
+ * needs more than the scratch holds grows it, which synchronizes the device
+ * and reallocates; after a reserve, forwards within these sizes (on this
+ * block, or on any block of the context with the same shapes) neither
+ * allocate nor synchronize. The reference allocates per call through candle
+ * and has no counterpart; this is for serving loops that must not stall. */
+int qimm_block_reserve(qimm_block *blk, int64_t batch, int64_t seq, int64_t mod_rows);
+
 /* An attention mask, the product of build_block_causal_mask
  * (src/attention_mask.rs:18-66) kept as its two inputs (device pointers):
  *   image_ids  int32 [S]: JointLayout::image_ids of the call's tokens, -1 for

@@ -432,6 +432,127 @@ done:
     return rc;
 }
 
+/* The same block forward for a subset of token rows (flat indices r = b*S + t
+ * into [0, B*S)): K and V come from every row, since every query attends over
+ * all of them, but the query side (q, attention, out-proj, both residuals and
+ * the MLP) runs for the listed rows only. x_out is [nrows, hidden]; k_out /
+ * v_out (optional) are the full [B,H,S,D]. Each output row is computed with
+ * the operations the full forward applies to that row, so it is bit-identical
+ * to that row of oq_block_forward. */
+int oq_block_forward_rows(const oq_block_cfg *cfg, const oq_block_weights *w,
+                          const float *x, int64_t b, int64_t s,
+                          const float *mod, int64_t mod_rows, const float *pe,
+                          const uint8_t *mask, int64_t mask_batch_stride,
+                          const uint16_t *prefix_k, const uint16_t *prefix_v, int64_t p,
+                          const int64_t *rows, int64_t nrows,
+                          float *x_out, float *k_out, float *v_out, int mode) {
+    const int64_t hid = cfg->hidden, H = cfg->heads, D = cfg->head_dim, F = cfg->mlp;
+    const int64_t M = b * s, skv = p + s, mstride = 4 * hid;
+    if (H * D != hid || mod_rows < 1 || (mod_rows != 1 && mod_rows != s) || nrows < 0) return -1;
+    for (int64_t i = 0; i < nrows; i++)
+        if (rows[i] < 0 || rows[i] >= M) return -1;
+    const float eps = 1e-6f;
+    int rc = 0;
+    const int64_t R = nrows > 0 ? nrows : 1;
+    float *normed = (float *)malloc(sizeof(float) * (size_t)(M * hid));
+    float *kb = (float *)malloc(sizeof(float) * (size_t)(M * hid));
+    float *vb = (float *)malloc(sizeof(float) * (size_t)(M * hid));
+    float *kh = (float *)malloc(sizeof(float) * (size_t)(M * hid));
+    float *vh = (float *)malloc(sizeof(float) * (size_t)(M * hid));
+    float *xs = (float *)malloc(sizeof(float) * (size_t)(R * hid));   /* selected rows: normed, then residual */
+    float *qs = (float *)malloc(sizeof(float) * (size_t)(R * hid));
+    float *qg = (float *)malloc(sizeof(float) * (size_t)(R * hid));   /* q of one batch entry [H, n, D] */
+    float *og = (float *)malloc(sizeof(float) * (size_t)(R * hid));
+    float *att = (float *)malloc(sizeof(float) * (size_t)(R * hid));
+    float *pr = (float *)malloc(sizeof(float) * (size_t)(R * D));     /* pe rows of the selected tokens */
+    float *gu = (float *)malloc(sizeof(float) * (size_t)(R * 2 * F));
+    float *hm = (float *)malloc(sizeof(float) * (size_t)(R * F));
+    int64_t *sel = (int64_t *)malloc(sizeof(int64_t) * (size_t)R);
+    uint8_t *mg = mask ? (uint8_t *)malloc((size_t)(R * (skv > 0 ? skv : 1))) : NULL;
+    float *pk = NULL, *pv = NULL;
+    if (!normed || !kb || !vb || !kh || !vh || !xs || !qs || !qg || !og || !att || !pr || !gu || !hm || !sel ||
+        (mask && !mg)) { rc = -2; goto done; }
+    if (p > 0) {
+        if (!prefix_k || !prefix_v) { rc = -1; goto done; }
+        pk = (float *)malloc(sizeof(float) * (size_t)(b * H * p * D));
+        pv = (float *)malloc(sizeof(float) * (size_t)(b * H * p * D));
+        if (!pk || !pv) { rc = -2; goto done; }
+        oq_bf16_to_f32_n(prefix_k, b * H * p * D, pk);
+        oq_bf16_to_f32_n(prefix_v, b * H * p * D, pv);
+    }
+    /* norm1 over every row (K and V need them all) */
+    for (int64_t bb = 0; bb < b; bb++)
+        oq_layernorm_mod(x + bb * s * hid, s, hid, mod + bb * mod_rows * mstride, mstride,
+                         mod_rows == 1 ? s : 1, eps, normed + bb * s * hid);
+    if ((rc = qlin(&w->to_k, normed, M, kb, mode))) goto done;
+    if ((rc = qlin(&w->to_v, normed, M, vb, mode))) goto done;
+    oq_rmsnorm(kb, M * H, D, w->norm_k, eps);
+    bshd_to_bhsd(kb, b, s, H, D, kh);
+    bshd_to_bhsd(vb, b, s, H, D, vh);
+    oq_apply_rope(kh, b * H, s, D, pe);
+    if (k_out) memcpy(k_out, kh, sizeof(float) * (size_t)(M * hid));
+    if (v_out) memcpy(v_out, vh, sizeof(float) * (size_t)(M * hid));
+    /* q for the selected rows */
+    for (int64_t i = 0; i < nrows; i++) memcpy(xs + i * hid, normed + rows[i] * hid, sizeof(float) * (size_t)hid);
+    if ((rc = qlin(&w->to_q, xs, nrows, qs, mode))) goto done;
+    oq_rmsnorm(qs, nrows * H, D, w->norm_q, eps);
+    /* attention per batch entry over [prefix ; own] of that entry */
+    for (int64_t bb = 0; bb < b; bb++) {
+        int64_t n = 0;
+        for (int64_t i = 0; i < nrows; i++)
+            if (rows[i] / s == bb) sel[n++] = i;
+        if (!n) continue;
+        for (int64_t j = 0; j < n; j++) {
+            const int64_t t = rows[sel[j]] % s;
+            memcpy(pr + j * D, pe + t * D, sizeof(float) * (size_t)D);
+            for (int64_t hh = 0; hh < H; hh++)
+                memcpy(qg + (hh * n + j) * D, qs + sel[j] * hid + hh * D, sizeof(float) * (size_t)D);
+            if (mask)
+                memcpy(mg + j * skv, mask + bb * mask_batch_stride + t * skv, (size_t)skv);
+        }
+        oq_apply_rope(qg, H, n, D, pr);
+        if ((rc = oq_attention(qg, pk ? pk + bb * H * p * D : NULL, pv ? pv + bb * H * p * D : NULL, p,
+                               kh + bb * H * s * D, vh + bb * H * s * D, s, 1, H, n, D,
+                               1.0 / sqrt((double)D), mg, 0, og, mode)))
+            goto done;
+        for (int64_t j = 0; j < n; j++)
+            for (int64_t hh = 0; hh < H; hh++)
+                memcpy(att + sel[j] * hid + hh * D, og + (hh * n + j) * D, sizeof(float) * (size_t)D);
+    }
+    if ((rc = qlin(&w->to_out, att, nrows, qs, mode))) goto done;
+    /* x1 = x + tanh(gate1) * attn, then norm2 per selected row */
+    for (int64_t i = 0; i < nrows; i++) {
+        const int64_t bb = rows[i] / s, t = rows[i] % s;
+        const float *mr = mod + (bb * mod_rows + (mod_rows == 1 ? 0 : t)) * mstride;
+        for (int64_t c = 0; c < hid; c++)
+            x_out[i * hid + c] = x[rows[i] * hid + c] + tanhf(mr[hid + c]) * qs[i * hid + c];
+        oq_layernorm_mod(x_out + i * hid, 1, hid, mr + 2 * hid, mstride, 1, eps, xs + i * hid);
+    }
+    if (w->fused_gate_up) {
+        if ((rc = qlin(&w->gate_up, xs, nrows, gu, mode))) goto done;
+        for (int64_t r = 0; r < nrows; r++)
+            for (int64_t c = 0; c < F; c++)
+                hm[r * F + c] = silu_f(gu[r * 2 * F + c]) * gu[r * 2 * F + F + c];
+    } else {
+        if ((rc = qlin(&w->gate_layer, xs, nrows, gu, mode))) goto done;
+        if ((rc = qlin(&w->proj, xs, nrows, gu + nrows * F, mode))) goto done;
+        for (int64_t r = 0; r < nrows; r++)
+            for (int64_t c = 0; c < F; c++)
+                hm[r * F + c] = silu_f(gu[r * F + c]) * gu[nrows * F + r * F + c];
+    }
+    if ((rc = qlin(&w->down, hm, nrows, qs, mode))) goto done;
+    for (int64_t i = 0; i < nrows; i++) {
+        const int64_t bb = rows[i] / s, t = rows[i] % s;
+        const float *g = mod + (bb * mod_rows + (mod_rows == 1 ? 0 : t)) * mstride + 3 * hid;
+        for (int64_t c = 0; c < hid; c++)
+            x_out[i * hid + c] = x_out[i * hid + c] + tanhf(g[c]) * qs[i * hid + c];
+    }
+done:
+    free(normed); free(kb); free(vb); free(kh); free(vh); free(xs); free(qs); free(qg); free(og);
+    free(att); free(pr); free(gu); free(hm); free(sel); free(mg); free(pk); free(pv);
+    return rc;
+}
+
 /* timestep_embedding (src/scheduler.rs:101-126): f_i = exp(-ln(1e4) * i/half)
  * in f32, emb = 1000 t f_i, output [cos ; sin]. */
 void oq_timestep_embedding(const float *t, int64_t b, int64_t dim, float *out) {

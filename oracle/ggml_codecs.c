@@ -524,6 +524,78 @@ static float vdot_q6_k(const unpacked_w *u, int64_t r, const int8_t *xq, const f
     return sumf;
 }
 
+/* Exact-mode product y[m][n] = sum_k x[m][k] w[n][k] in f64. The product of
+ * two f32 values is exact in f64, so only the additions round: each output
+ * keeps four partial sums, lane l adding the terms k = l (mod 4) in increasing
+ * k, and returns (s0 + s1) + (s2 + s3). That order depends on the output's own
+ * row and column only, never on M, N or the tiling below, so a subset of rows
+ * gives bit-identical outputs. Tiles of 32 x 32 outputs keep both operand
+ * panels in the core's L2; 2 x 4 outputs share each operand load. */
+typedef double v4d __attribute__((vector_size(32)));
+typedef float v4f __attribute__((vector_size(16)));
+
+static inline v4d ld4d(const float *p) {
+    v4f f;
+    memcpy(&f, p, sizeof(f));
+    return __builtin_convertvector(f, v4d);
+}
+
+static inline float fin4(v4d a) { return (float)((a[0] + a[1]) + (a[2] + a[3])); }
+
+static inline void tail4(v4d *acc, const float *xr, const float *wr, int64_t k4, int64_t K) {
+    for (int64_t k = k4; k < K; k++) (*acc)[k - k4] += (double)xr[k] * (double)wr[k];
+}
+
+static void gemm_exact_f64(const float *x, int64_t M, const float *w, int64_t N, int64_t K, float *y) {
+    const int64_t T = 32, k4 = K & ~(int64_t)3;
+    const int64_t tm = (M + T - 1) / T, tn = (N + T - 1) / T;
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+    for (int64_t bi = 0; bi < tm; bi++)
+        for (int64_t bj = 0; bj < tn; bj++) {
+            const int64_t m0 = bi * T, m1 = m0 + T < M ? m0 + T : M;
+            const int64_t n0 = bj * T, n1 = n0 + T < N ? n0 + T : N;
+            for (int64_t m = m0; m < m1; m += 2) {
+                const int two = m + 1 < m1;
+                const float *x0 = x + m * K, *x1 = x + (two ? m + 1 : m) * K;
+                int64_t n = n0;
+                for (; n + 4 <= n1; n += 4) {
+                    const float *w0 = w + n * K, *w1 = w0 + K, *w2 = w1 + K, *w3 = w2 + K;
+                    v4d a00 = {0}, a01 = {0}, a02 = {0}, a03 = {0};
+                    v4d a10 = {0}, a11 = {0}, a12 = {0}, a13 = {0};
+                    for (int64_t k = 0; k < k4; k += 4) {
+                        const v4d p0 = ld4d(x0 + k), p1 = ld4d(x1 + k);
+                        const v4d q0 = ld4d(w0 + k), q1 = ld4d(w1 + k), q2 = ld4d(w2 + k), q3 = ld4d(w3 + k);
+                        a00 += p0 * q0; a01 += p0 * q1; a02 += p0 * q2; a03 += p0 * q3;
+                        a10 += p1 * q0; a11 += p1 * q1; a12 += p1 * q2; a13 += p1 * q3;
+                    }
+                    tail4(&a00, x0, w0, k4, K); tail4(&a01, x0, w1, k4, K);
+                    tail4(&a02, x0, w2, k4, K); tail4(&a03, x0, w3, k4, K);
+                    tail4(&a10, x1, w0, k4, K); tail4(&a11, x1, w1, k4, K);
+                    tail4(&a12, x1, w2, k4, K); tail4(&a13, x1, w3, k4, K);
+                    float *y0 = y + m * N + n;
+                    y0[0] = fin4(a00); y0[1] = fin4(a01); y0[2] = fin4(a02); y0[3] = fin4(a03);
+                    if (two) {
+                        float *y1 = y0 + N;
+                        y1[0] = fin4(a10); y1[1] = fin4(a11); y1[2] = fin4(a12); y1[3] = fin4(a13);
+                    }
+                }
+                for (; n < n1; n++) {
+                    const float *w0 = w + n * K;
+                    v4d a0 = {0}, a1 = {0};
+                    for (int64_t k = 0; k < k4; k += 4) {
+                        const v4d q0 = ld4d(w0 + k);
+                        a0 += ld4d(x0 + k) * q0;
+                        a1 += ld4d(x1 + k) * q0;
+                    }
+                    tail4(&a0, x0, w0, k4, K);
+                    tail4(&a1, x1, w0, k4, K);
+                    y[m * N + n] = fin4(a0);
+                    if (two) y[(m + 1) * N + n] = fin4(a1);
+                }
+            }
+        }
+}
+
 int oq_qmatmul(int wtype, const void *w, int64_t N, int64_t K,
                const float *x, int64_t M, float *y, int mode) {
     int bs = oq_block_size(wtype);
@@ -535,19 +607,18 @@ int oq_qmatmul(int wtype, const void *w, int64_t N, int64_t K,
         float *wf = (float *)malloc(sizeof(float) * (size_t)(N * K));
         if (!wf) return -2;
         oq_dequantize(wtype, w, N * K, wf);
+        if (mode == OQ_MODE_EXACT) {
+            gemm_exact_f64(x, M, wf, N, K, y);
+            free(wf);
+            return 0;
+        }
 #pragma omp parallel for collapse(2) schedule(static)
         for (int64_t m = 0; m < M; m++)
             for (int64_t n = 0; n < N; n++) {
                 const float *xr = x + m * K, *wr = wf + n * K;
-                if (mode == OQ_MODE_EXACT) {
-                    double acc = 0.0;
-                    for (int64_t k = 0; k < K; k++) acc += (double)xr[k] * (double)wr[k];
-                    y[m * N + n] = (float)acc;
-                } else {
-                    float acc = 0.f;
-                    for (int64_t k = 0; k < K; k++) acc += xr[k] * wr[k];
-                    y[m * N + n] = acc;
-                }
+                float acc = 0.f;
+                for (int64_t k = 0; k < K; k++) acc += xr[k] * wr[k];
+                y[m * N + n] = acc;
             }
         free(wf);
         return 0;

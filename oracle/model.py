@@ -17,12 +17,22 @@ Pinning (tests/test_step_cpu.py, tests/test_gpu_step.py):
   mu = 0.5 exactly at 256 image tokens;
 - layout pieces: the reference's layout tests (src/joint_layout.rs:133-164) and
   the image ids of oracle.joint_layout;
-- silu / gelu_tanh: the odd-part identities f(x) - f(-x) = x and f(0) = 0;
-- the t = 0 embedding: the constant [1 x 128, 0 x 128] the reference states
+- silu / gelu_tanh: the odd-part identities f(x) - f(-x) = x and f(0) = 0,
+  and the tanh-form GELU(1);
+- the timestep embedding (oracle.timestep_embedding): the closed form
+  [cos(1000 t f_i) | sin(1000 t f_i)], f_i = 10000^(-i/128), at t up to 1, the
+  known points t = 0.001 (angle 1 rad) and t = pi/2000 (angle pi/2), the
+  angle ratio 10000^(-1/128) and the angles recovered by atan2; the t = 0
+  constant [1 x 128, 0 x 128] the reference states
   (src/quantized_transformer.rs:337);
-- the composition itself: a model whose global weights are zero outputs zero
-  velocity, and with zero blocks (no layers) the forward reduces to
-  proj_out(LN(img_in(x)) * (1 + norm_out(silu(t_emb)))).
+- time_embed, modulation, txt_in and final_layer with special weights whose
+  outputs have closed forms: identity linears give silu(t); modulation rows
+  [I; 2I; 0; -I] give the four chunks of silu(t_emb); the text embedder gives
+  gelu_tanh(x / rms(x) * (1 + stored)); the final layer's rows have mean 0 and
+  spread |1 + c| when norm_out maps silu(t_emb) to the constant c;
+- the composition: with no blocks, identity img_in / proj_out and a zero
+  norm_out the forward returns LayerNorm(latents), and a zero proj_out gives
+  zero velocity.
 """
 from __future__ import annotations
 

@@ -126,6 +126,16 @@ int oq_block_forward(const oq_block_cfg *cfg, const oq_block_weights *w,
                      const uint8_t *mask, int64_t mask_batch_stride,
                      const uint16_t *prefix_k, const uint16_t *prefix_v, int64_t p,
                      float *x_out, float *k_out, float *v_out, int mode);
+/* The same forward for the token rows listed in rows[nrows] (flat b*S + t):
+ * x_out [nrows, hidden], bit-identical to those rows of oq_block_forward;
+ * k_out / v_out (optional) are the full [B,H,S,D]. */
+int oq_block_forward_rows(const oq_block_cfg *cfg, const oq_block_weights *w,
+                          const float *x, int64_t b, int64_t s,
+                          const float *mod, int64_t mod_rows, const float *pe,
+                          const uint8_t *mask, int64_t mask_batch_stride,
+                          const uint16_t *prefix_k, const uint16_t *prefix_v, int64_t p,
+                          const int64_t *rows, int64_t nrows,
+                          float *x_out, float *k_out, float *v_out, int mode);
 
 /* ---- timestep path ---- */
 /* [cos(1000 t f_i), sin(1000 t f_i)], f_i = exp(-ln(1e4) i / half), dim 256. */

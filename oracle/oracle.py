@@ -52,6 +52,8 @@ def lib():
             "oq_block_causal_mask": (None, [vp, i64, vp]),
             "oq_attention": (i32, [vp, vp, vp, i64, vp, vp, i64, i64, i64, i64, i64, C.c_double, vp, i64, vp, i32]),
             "oq_block_forward": (i32, [vp, vp, vp, i64, i64, vp, i64, vp, vp, i64, vp, vp, i64, vp, vp, vp, i32]),
+            "oq_block_forward_rows": (i32, [vp, vp, vp, i64, i64, vp, i64, vp, vp, i64, vp, vp, i64, vp, i64,
+                                            vp, vp, vp, i32]),
             "oq_timestep_embedding": (None, [vp, i64, i64, vp]),
             "oq_silu_inplace": (None, [vp, i64]),
             "oq_now_seconds": (C.c_double, []),
@@ -122,7 +124,8 @@ def qmatmul(t, w, n, k, x, mode=CANDLE):
     x = _c(x, np.float32)
     m = x.size // k
     y = np.empty((m, n), dtype=np.float32)
-    rc = lib().oq_qmatmul(t, _p(_c(w, np.uint8)), n, k, _p(x), m, _p(y), mode)
+    w = _c(w, np.uint8)
+    rc = lib().oq_qmatmul(t, _p(w), n, k, _p(x), m, _p(y), mode)
     assert rc == 0, rc
     return y
 
@@ -139,7 +142,8 @@ def layernorm_mod(x, scale=None, eps=1e-6):
 
 def rmsnorm(x, w, eps=1e-6):
     x = _c(x, np.float32).copy()
-    lib().oq_rmsnorm(_p(x), x.size // x.shape[-1], x.shape[-1], _p(_c(w, np.float32)), eps)
+    w = _c(w, np.float32)
+    lib().oq_rmsnorm(_p(x), x.size // x.shape[-1], x.shape[-1], _p(w), eps)
     return x
 
 
@@ -160,7 +164,8 @@ def apply_rope(x, pe):
     """x [..., S, D] rotated by pe [S, D]."""
     x = _c(x, np.float32).copy()
     s, d = x.shape[-2], x.shape[-1]
-    lib().oq_apply_rope(_p(x), x.size // (s * d), s, d, _p(_c(pe, np.float32)))
+    pe = _c(pe, np.float32)
+    lib().oq_apply_rope(_p(x), x.size // (s * d), s, d, _p(pe))
     return x
 
 
@@ -225,17 +230,9 @@ class _Cfg(C.Structure):
     _fields_ = [("hidden", C.c_int64), ("heads", C.c_int64), ("head_dim", C.c_int64), ("mlp", C.c_int64)]
 
 
-def block_forward(cfg, weights, x, mod, pe, prefix_k=None, prefix_v=None, mask=None, mode=CANDLE):
-    """TransformerBlock::forward. cfg: dict(hidden, heads, head_dim, mlp). weights: dict name ->
-    (type, bytes, rows, cols) for to_q, to_k, to_v, to_out, gate_up | (proj, gate_layer), down;
-    plus norm_q / norm_k f32 arrays. x [B,S,h]; mod [B, 1|S, 4h]; pe [S, D];
-    prefix_k/v bf16 (uint16) [B,H,P,D]. Returns (x_out, k [B,H,S,D], v [B,H,S,D])."""
+def _block_args(cfg, weights, x, mod, prefix_k, prefix_v, mask, keep):
     x = _c(x, np.float32)
     b, s, hid = x.shape
-    H, D = cfg["heads"], cfg["head_dim"]
-    mod = _c(mod, np.float32)
-    mod_rows = mod.shape[1]
-    keep = []
 
     def qw(name):
         if name not in weights:
@@ -246,10 +243,11 @@ def block_forward(cfg, weights, x, mod, pe, prefix_k=None, prefix_v=None, mask=N
         return _QW(t, arr.ctypes.data, rows, cols)
 
     nq, nk = _c(weights["norm_q"], np.float32), _c(weights["norm_k"], np.float32)
+    keep += [nq, nk]
     fused = "gate_up" in weights
     bw = _BW(qw("to_q"), qw("to_k"), qw("to_v"), qw("to_out"), 1 if fused else 0, qw("gate_up"), qw("proj"),
              qw("gate_layer"), qw("down"), nq.ctypes.data, nk.ctypes.data)
-    c = _Cfg(cfg["hidden"], H, D, cfg["mlp"])
+    c = _Cfg(cfg["hidden"], cfg["heads"], cfg["head_dim"], cfg["mlp"])
     p = 0
     pk = pv = None
     if prefix_k is not None:
@@ -259,13 +257,47 @@ def block_forward(cfg, weights, x, mod, pe, prefix_k=None, prefix_v=None, mask=N
     if mask is not None:
         mk = _c(mask, np.uint8)
         mstride = 0 if mk.shape[0] == 1 else s * (p + s)
+    mod = _c(mod, np.float32)
+    keep += [x, mod, pk, pv, mk]
+    return x, b, s, bw, c, mod, pk, pv, p, mk, mstride
+
+
+def block_forward(cfg, weights, x, mod, pe, prefix_k=None, prefix_v=None, mask=None, mode=CANDLE):
+    """TransformerBlock::forward. cfg: dict(hidden, heads, head_dim, mlp). weights: dict name ->
+    (type, bytes, rows, cols) for to_q, to_k, to_v, to_out, gate_up | (proj, gate_layer), down;
+    plus norm_q / norm_k f32 arrays. x [B,S,h]; mod [B, 1|S, 4h]; pe [S, D];
+    prefix_k/v bf16 (uint16) [B,H,P,D]. Returns (x_out, k [B,H,S,D], v [B,H,S,D])."""
+    keep = []
+    x, b, s, bw, c, mod, pk, pv, p, mk, mstride = _block_args(cfg, weights, x, mod, prefix_k, prefix_v, mask, keep)
+    H, D = cfg["heads"], cfg["head_dim"]
     xo = np.empty_like(x)
     ko = np.empty((b, H, s, D), dtype=np.float32)
     vo = np.empty((b, H, s, D), dtype=np.float32)
-    rc = lib().oq_block_forward(C.byref(c), C.byref(bw), _p(x), b, s, _p(mod), mod_rows, _p(_c(pe, np.float32)),
-                                _p(mk), mstride, _p(pk), _p(pv), p, _p(xo), _p(ko), _p(vo), mode)
+    pe = _c(pe, np.float32)
+    rc = lib().oq_block_forward(C.byref(c), C.byref(bw), _p(x), b, s, _p(mod), mod.shape[1],
+                                _p(pe), _p(mk), mstride, _p(pk), _p(pv), p, _p(xo), _p(ko),
+                                _p(vo), mode)
     if rc != 0:
         raise ValueError(f"oq_block_forward -> {rc}")
+    return xo, ko, vo
+
+
+def block_forward_rows(cfg, weights, x, mod, pe, rows, prefix_k=None, prefix_v=None, mask=None, mode=CANDLE):
+    """block_forward for the token rows `rows` (flat indices b*S + t): returns (x_out [len(rows), h],
+    k [B,H,S,D], v [B,H,S,D]); each row equals that row of block_forward bit for bit."""
+    keep = []
+    x, b, s, bw, c, mod, pk, pv, p, mk, mstride = _block_args(cfg, weights, x, mod, prefix_k, prefix_v, mask, keep)
+    H, D = cfg["heads"], cfg["head_dim"]
+    r = _c(rows, np.int64)
+    xo = np.empty((r.size, x.shape[2]), dtype=np.float32)
+    ko = np.empty((b, H, s, D), dtype=np.float32)
+    vo = np.empty((b, H, s, D), dtype=np.float32)
+    pe = _c(pe, np.float32)
+    rc = lib().oq_block_forward_rows(C.byref(c), C.byref(bw), _p(x), b, s, _p(mod), mod.shape[1],
+                                     _p(pe), _p(mk), mstride, _p(pk), _p(pv), p, _p(r), r.size,
+                                     _p(xo), _p(ko), _p(vo), mode)
+    if rc != 0:
+        raise ValueError(f"oq_block_forward_rows -> {rc}")
     return xo, ko, vo
 
 

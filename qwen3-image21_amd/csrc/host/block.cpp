@@ -82,6 +82,9 @@ int qimm_block_create(qimm_ctx *ctx, const qimm_block_config *cfg, const qimm_bl
     const int64_t hid = cfg->hidden, H = cfg->heads, D = cfg->head_dim, F = cfg->mlp;
     if (D != 128 || H <= 0 || H * D != hid || F <= 0 || F % 64 || hid % 256)
         return set_err(ctx, QIMM_ERR_SHAPE, "block: needs head_dim 128, hidden = heads*128 (multiple of 256), mlp % 64 == 0");
+    // the LayerNorm kernel holds one row in registers: 256 threads x 8 float4
+    if (hid > qimm::LN_MAX_HIDDEN)
+        return set_err(ctx, QIMM_ERR_SHAPE, "block: hidden must be at most " + std::to_string(qimm::LN_MAX_HIDDEN));
     if (!tensor_ok(t->to_q, hid, hid) || !tensor_ok(t->to_k, hid, hid) || !tensor_ok(t->to_v, hid, hid) ||
         !tensor_ok(t->to_out, hid, hid) || !tensor_ok(t->mlp_out, hid, F))
         return set_err(ctx, QIMM_ERR_SHAPE, "block: attention / mlp_out tensors missing or mis-shaped");
@@ -164,6 +167,32 @@ int qimm_block_destroy(qimm_block *blk) {
 
 namespace {
 
+// Workspace of one forward: modp [B*mod_rows,4h] f32 | xn [M,h] | q | k | vt |
+// attn [M,h] | hmid [M,F] (bf16), and the split-K scratch of the short- and
+// mid-M GEMM paths, sized for the largest projection.
+struct WsLayout {
+    size_t modp, xn, q, k, vt, att, h, total, part;
+};
+
+WsLayout ws_layout(const qimm_block *blk, int64_t batch, int64_t seq, int64_t mod_rows) {
+    const int64_t hid = blk->cfg.hidden, F = blk->cfg.mlp, M = batch * seq;
+    WsLayout L{};
+    size_t off = 0;
+    L.modp = off; off += align_up((size_t)(batch * mod_rows * 4 * hid) * 4);
+    L.xn = off; off += align_up((size_t)(M * hid) * 2);
+    L.q = off; off += align_up((size_t)(M * hid) * 2);
+    L.k = off; off += align_up((size_t)(M * hid) * 2);
+    L.vt = off; off += align_up((size_t)(M * hid) * 2);
+    L.att = off; off += align_up((size_t)(M * hid) * 2);
+    L.h = off; off += align_up((size_t)(M * F) * 2);
+    L.total = off;
+    L.part = 0;
+    const qimm_weight *ws_list[] = {blk->qkv, blk->q, blk->k, blk->v, blk->out, blk->gate_up, blk->down};
+    for (const qimm_weight *wt : ws_list)
+        if (wt) L.part = std::max(L.part, qimm::qgemm_workspace(wt->gw, M));
+    return L;
+}
+
 // TransformerBlock::forward (src/quantized_transformer.rs:258-285) with
 // modulation rows [B, mod_rows, 4 hidden] (mod_rows 1 broadcasts over the
 // tokens, mod_rows == seq gives one row per token) and an optional attention
@@ -193,31 +222,18 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
     const int64_t M = batch * seq;
     hipStream_t s = (hipStream_t)stream;
 
-    // workspace: modp [B*mod_rows,4h] f32 | xn [M,h] | q | k | vt | attn [M,h] | hmid [M,F] (bf16)
-    size_t off = 0;
-    const size_t o_modp = off; off += align_up((size_t)(batch * mod_rows * 4 * hid) * 4);
-    const size_t o_xn = off; off += align_up((size_t)(M * hid) * 2);
-    const size_t o_q = off; off += align_up((size_t)(M * hid) * 2);
-    const size_t o_k = off; off += align_up((size_t)(M * hid) * 2);
-    const size_t o_vt = off; off += align_up((size_t)(M * hid) * 2);
-    const size_t o_att = off; off += align_up((size_t)(M * hid) * 2);
-    const size_t o_h = off; off += align_up((size_t)(M * F) * 2);
+    // the workspace grows (a device-wide sync, free and allocation) only when
+    // this call needs more than any earlier call or qimm_block_reserve
+    const WsLayout L = ws_layout(blk, batch, seq, mod_rows);
     QIMM_HIP(ctx, hipSetDevice(ctx->device));
-    int rc = ensure_workspace(ctx, off);
+    int rc = ensure_workspace(ctx, L.total);
     if (rc) return rc;
     char *ws = (char *)ctx->ws;
-    float *modp = (float *)(ws + o_modp);
-    uint16_t *xn = (uint16_t *)(ws + o_xn), *qb = (uint16_t *)(ws + o_q);
-    uint16_t *kb = k_out ? k_out : (uint16_t *)(ws + o_k);
-    uint16_t *vt = (uint16_t *)(ws + o_vt), *att = (uint16_t *)(ws + o_att), *hm = (uint16_t *)(ws + o_h);
-    // split-K scratch of the short- and mid-M GEMM paths, sized for the
-    // largest projection
-    size_t part_need = 0;
-    {
-        const qimm_weight *ws_list[] = {blk->qkv, blk->q, blk->k, blk->v, blk->out, blk->gate_up, blk->down};
-        for (const qimm_weight *wt : ws_list)
-            if (wt) part_need = std::max(part_need, qimm::qgemm_workspace(wt->gw, M));
-    }
+    float *modp = (float *)(ws + L.modp);
+    uint16_t *xn = (uint16_t *)(ws + L.xn), *qb = (uint16_t *)(ws + L.q);
+    uint16_t *kb = k_out ? k_out : (uint16_t *)(ws + L.k);
+    uint16_t *vt = (uint16_t *)(ws + L.vt), *att = (uint16_t *)(ws + L.att), *hm = (uint16_t *)(ws + L.h);
+    const size_t part_need = L.part;
     if (part_need) {
         rc = ensure_part_workspace(ctx, part_need);
         if (rc) return rc;
@@ -320,6 +336,18 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
 }  // namespace
 
 extern "C" {
+
+int qimm_block_reserve(qimm_block *blk, int64_t batch, int64_t seq, int64_t mod_rows) {
+    if (!blk) return QIMM_ERR_ARG;
+    qimm_ctx *ctx = blk->ctx;
+    if (batch <= 0 || seq <= 0 || (mod_rows != 1 && mod_rows != seq))
+        return set_err(ctx, QIMM_ERR_SHAPE, "block reserve: batch, seq > 0 and mod_rows 1 or seq");
+    const WsLayout L = ws_layout(blk, batch, seq, mod_rows);
+    QIMM_HIP(ctx, hipSetDevice(ctx->device));
+    int rc = ensure_workspace(ctx, L.total);
+    if (rc) return rc;
+    return L.part ? ensure_part_workspace(ctx, L.part) : QIMM_OK;
+}
 
 int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t batch, int64_t seq,
                        const float *mod, const float *pe, const qimm_kv *kv, int64_t layer, uint16_t *k_out,

@@ -46,8 +46,11 @@ int ensure_part_workspace(qimm_ctx *ctx, size_t bytes) {
     QIMM_HIP(ctx, hipMalloc(&ctx->ws_part, bytes));
     ctx->ws_part_bytes = bytes;
     // the arrival counters at the front of the short-M GEMM scratch start at
-    // zero; the kernels leave them zero after every call
+    // zero; the kernels leave them zero after every call. The fill runs on the
+    // null stream, so wait for it: the GEMM that reads the counters may be
+    // launched on a non-blocking stream, which the null stream does not order.
     QIMM_HIP(ctx, hipMemset(ctx->ws_part, 0, std::min(bytes, qimm::STREAM_COUNTER_BYTES)));
+    QIMM_HIP(ctx, hipDeviceSynchronize());
     return QIMM_OK;
 }
 

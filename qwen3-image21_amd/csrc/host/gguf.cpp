@@ -262,15 +262,16 @@ bool parse(qimm_gguf *g, std::string &why) {
             c.fail("tensor " + t.name + " row length " + std::to_string(t.ne[0]) + " is not a multiple of its block");
             break;
         }
-        // rows = ne1*ne2*ne3 (each <= 2^40, checked so the product cannot wrap)
-        const unsigned __int128 rows = (unsigned __int128)t.ne[1] * (uint64_t)t.ne[2] * (uint64_t)t.ne[3];
-        const unsigned __int128 nb = rows * (uint64_t)(t.ne[0] / blk) * (uint64_t)bytes;
-        if (t.rel_off > g->size || nb > (unsigned __int128)(g->size) || t.abs_off > g->size ||
-            (uint64_t)nb > g->size - t.abs_off) {
+        // nb = ne1 * ne2 * ne3 * (ne0 / blk) * bytes, each product checked for
+        // overflow: a wrapped size could pass the bounds check below
+        uint64_t nb = (uint64_t)(t.ne[0] / blk);
+        bool wrap = __builtin_mul_overflow(nb, (uint64_t)bytes, &nb);
+        for (int d = 1; d < 4 && !wrap; d++) wrap = __builtin_mul_overflow(nb, (uint64_t)t.ne[d], &nb);
+        if (wrap || t.rel_off > g->size || nb > g->size || t.abs_off > g->size || nb > g->size - t.abs_off) {
             c.fail("tensor " + t.name + " data lies outside the file");
             break;
         }
-        t.nbytes = (uint64_t)nb;
+        t.nbytes = nb;
     }
     why = c.why;
     return c.ok;
@@ -518,8 +519,12 @@ int qimm_gguf_model_tensors(const qimm_gguf *g, qimm_model_tensors *out, char *e
             put_err(err, err_len, std::string(name) + ": GGML type " + std::to_string(t->type) + " has no known layout");
             return QIMM_ERR_TYPE;
         }
+        if (t->ne[2] != 1 || t->ne[3] != 1) {
+            put_err(err, err_len, std::string(name) + " is not a matrix");
+            return QIMM_ERR_SHAPE;
+        }
         dst.ggml_type = t->type;
-        dst.rows = t->ne[1] * t->ne[2] * t->ne[3];
+        dst.rows = t->ne[1];
         dst.cols = t->ne[0];
         dst.data = g->map + t->abs_off;
         dst.nbytes = (size_t)t->nbytes;

@@ -198,8 +198,10 @@ int qimm_dequant(qimm_ctx *ctx, int ggml_type, const void *dev_bytes, int64_t n,
     return QIMM_OK;
 }
 
-int qimm_qmatmul(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_t m, int64_t lda, void *y,
-                 int out_type, void *stream) {
+namespace {
+
+int qmatmul_check(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_t m, int64_t lda, void *y,
+                  int out_type) {
     if (!ctx || !w || !x_bf16 || !y || m < 0) return QIMM_ERR_ARG;
     if (out_type != QIMM_TYPE_F32 && out_type != QIMM_TYPE_BF16)
         return set_err(ctx, QIMM_ERR_TYPE, "qmatmul: output must be F32 or BF16");
@@ -207,6 +209,14 @@ int qimm_qmatmul(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_
         return set_err(ctx, QIMM_ERR_SHAPE, "qmatmul: needs N % 128 == 0, K % 64 == 0, lda >= K, lda % 8 == 0");
     if (((uintptr_t)x_bf16 | (uintptr_t)y) & 15)
         return set_err(ctx, QIMM_ERR_ARG, "qmatmul: x and y must be 16-byte aligned");
+    return QIMM_OK;
+}
+
+}  // namespace
+
+int qimm_qmatmul(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_t m, int64_t lda, void *y,
+                 int out_type, void *stream) {
+    if (const int rc = qmatmul_check(ctx, w, x_bf16, m, lda, y, out_type)) return rc;
     qimm::EpiParams ep{};
     ep.out = y;
     ep.ldo = w->rows;

@@ -100,7 +100,10 @@ hipError_t launch_dequant(int ggml_type, const uint8_t *src, int64_t n, float *o
 hipError_t launch_mod_prep(const float *mod, int64_t rows, int64_t hidden, float *modp,
                            hipStream_t stream);
 
-// out[m][:] = bf16(LayerNorm(x[m][:]) * modp_scale[(m / rows_per) * stride + :])
+// out[m][:] = bf16(LayerNorm(x[m][:]) * modp_scale[(m / rows_per) * stride + :]);
+// one workgroup keeps a row in registers, so hidden <= LN_MAX_HIDDEN
+// (hipErrorInvalidValue beyond).
+constexpr int64_t LN_MAX_HIDDEN = 8192;
 hipError_t launch_ln_mod(const float *x, int64_t m, int64_t hidden, const float *scale,
                          int64_t stride, int64_t rows_per, uint16_t *out, hipStream_t stream);
 

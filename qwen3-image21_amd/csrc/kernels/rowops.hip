@@ -85,7 +85,7 @@ __global__ void mod_prep_kernel(const float *__restrict__ mod, int64_t n, int64_
 // ---- LayerNorm (weight 1, bias 0, eps 1e-6) * (1 + scale) -> bf16 ----
 // src/quantized_transformer.rs:231-237, 267-269, 276-278. One 256-thread
 // workgroup per row; the row stays in registers for the two-pass variance.
-constexpr int LN_MAXV = 8;  // float4 chunks per thread: hidden <= 8192
+constexpr int LN_MAXV = (int)(LN_MAX_HIDDEN / 4 / 256);  // float4 chunks per thread
 
 __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x, int64_t hidden,
                                                      const float *__restrict__ scale, int64_t stride,
@@ -233,6 +233,7 @@ hipError_t launch_mod_prep(const float *mod, int64_t rows, int64_t hidden, float
 hipError_t launch_ln_mod(const float *x, int64_t m, int64_t hidden, const float *scale, int64_t stride,
                          int64_t rows_per, uint16_t *out, hipStream_t stream) {
     if (m <= 0) return hipSuccess;
+    if (hidden > LN_MAX_HIDDEN || hidden % 4) return hipErrorInvalidValue;
     ln_mod_kernel<<<dim3((unsigned)m), dim3(256), 0, stream>>>(x, hidden, scale, stride, rows_per, out);
     return hipGetLastError();
 }

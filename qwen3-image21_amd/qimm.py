@@ -64,6 +64,7 @@ SIGNATURES = [
     ("qimm_block_create", _i32, [_vp, _vp, _vp, C.POINTER(_vp)]),
     ("qimm_block_destroy", _i32, [_vp]),
     ("qimm_block_forward", _i32, [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp]),
+    ("qimm_block_reserve", _i32, [_vp, _i64, _i64, _i64]),
     ("qimm_block_forward_masked", _i32, [_vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp,
                                          _vp]),
     ("qimm_block_profile", _i32, [_vp, _i32]),
@@ -306,6 +307,10 @@ class KvCache:
 class Block:
     def __init__(self, ctx, h, cfg):
         self.ctx, self.h, self.cfg = ctx, h, cfg
+
+    def reserve(self, batch, seq, mod_rows=1):
+        """Pre-size the context scratch so forwards up to batch x seq tokens do not allocate."""
+        self.ctx.check(self.ctx.lib.qimm_block_reserve(self.h, batch, seq, mod_rows), "qimm_block_reserve")
 
     def forward(self, x_dev, x_out_dev, batch, seq, mod_dev, pe_dev, kv=None, layer=0, k_out=None, v_out=None,
                 stream=0):

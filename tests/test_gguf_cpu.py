@@ -129,6 +129,21 @@ def test_corrupted_fields_rejected(tmp_path, what):
     assert e.value.status == 8
 
 
+@pytest.mark.parametrize("ne", [(1 << 40, 1 << 40, 1 << 40, 1 << 40),   # product is 0 modulo 2^128
+                                (1 << 35, 1 << 30, 1, 1)])                 # fits 128 bits, not 64
+def test_tensor_size_overflow_rejected(tmp_path, ne):
+    """Each dimension passes the per-dimension cap, but the byte count
+    ne1 ne2 ne3 (ne0 / 32) 34 of a Q8_0 tensor overflows: a wrapped size must
+    not slip past the bounds check."""
+    head = b"GGUF" + u32(3) + u64(1) + u64(0)
+    head += gstr("img_in.weight") + u32(4) + b"".join(u64(v) for v in ne) + u32(8) + u64(0)
+    p = tmp_path / "wrap.gguf"
+    p.write_bytes(head + b"\0" * ((-len(head)) % 32) + b"\0" * 64)
+    with pytest.raises(qimm.QimmError) as e:
+        qimm.GGUF(str(p))
+    assert e.value.status == 8
+
+
 def G_blob_with_alignment(al):
     head = b"GGUF" + u32(3) + u64(0) + u64(1) + gstr("general.alignment") + u32(4) + u32(al)
     return head

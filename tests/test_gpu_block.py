@@ -171,6 +171,28 @@ def test_block_hidden4096_short_m(torch_cuda, qctx, b, s, p, mlp):
         assert cos_sim(v, vv) >= 0.9999 and max_abs_rel(v, vv) <= 2e-2
 
 
+@pytest.mark.parametrize("b,s,p,mlp,attn_type,down_type", [
+    (1, 516, 16, 1024, synth.Q4_K, synth.Q6_K),   # a 4-row second tile row
+    (2, 264, 8, 1024, synth.Q4_K, synth.Q6_K),    # batch boundary inside the first 256-row tile
+    (1, 768, 0, 2048, synth.Q8_0, synth.Q8_0)])   # three full tile rows, no prefix
+def test_block_hidden4096_large_m(torch_cuda, qctx, b, s, p, mlp, attn_type, down_type):
+    """Hidden 4096 (32 heads) at M >= 512 tokens: the 256 x 256 GEMM's fused
+    q/k/v epilogue over 32 heads (head = column / 128 across 48 column tiles, V
+    written transposed), its residual and SwiGLU epilogues and the XCD-aware tile
+    order, with partial tiles and a batch boundary inside a tile; output, k and v
+    against both oracle modes. Short MLPs keep the oracle quick."""
+    cfg = dict(hidden=4096, heads=32, head_dim=128, mlp=mlp)
+    w, x, mod, pe, kpre, vpre = make_case(61 + b + s, cfg, b, s, p, attn_type, down_type)
+    got, (k, v) = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)
+    ref, kr, vr = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
+    check(got, ref, x)
+    ref_e, kre, vre = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
+    check(got, ref_e, x, exact=True)
+    for kk, vv in ((kr, vr), (kre, vre)):
+        assert cos_sim(k, kk) >= 0.9999 and max_abs_rel(k, kk) <= 2e-2
+        assert cos_sim(v, vv) >= 0.9999 and max_abs_rel(v, vv) <= 2e-2
+
+
 @pytest.mark.parametrize("attn_type,down_type", [(synth.Q8_0, synth.Q8_0), (synth.Q4_K, synth.Q6_K)])
 def test_block_mid_m_split_k(torch_cuda, qctx, attn_type, down_type):
     """Hidden 1024 (8 heads), MLP 2048, 128 tokens over a 16-token prefix: every
@@ -202,3 +224,19 @@ def test_block_rejects_bad_config(torch_cuda, qctx):
     T.to_q = qimm.make_tensor(synth.Q8_0, 256, 256, b"\0" * 100, keep)   # wrong byte count
     with pytest.raises(qimm.QimmError, match="QIMM_ERR_SHAPE"):
         qctx.block_create(c, T)
+
+
+def test_block_reserve_then_forward(torch_cuda, qctx):
+    """qimm_block_reserve pre-sizes the context scratch: forwards at the reserved
+    size and below give the same bits as forwards that grow the scratch themselves,
+    and bad sizes are rejected."""
+    w, x, mod, pe, kpre, vpre = make_case(12, SMALL, 1, 96, 16, synth.Q4_K, synth.Q6_K)
+    a, _ = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre)
+    keep = []
+    blk = qctx.block_create(qimm.BlockConfig(256, 2, 128, 768), block_tensors(w, keep))
+    blk.reserve(2, 600)
+    with pytest.raises(qimm.QimmError, match="QIMM_ERR_SHAPE"):
+        blk.reserve(1, 64, 3)
+    blk.free()
+    b, _ = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre)
+    assert np.array_equal(a, b)

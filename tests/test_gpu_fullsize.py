@@ -1,0 +1,169 @@
+"""GPU parity at the reference's full shapes, through the C ABI.
+
+- The 1024x1024 block step with Q4_K_M weights: hidden 4096, 32 heads x 128,
+  MLP 12288, 4096 image tokens (64 x 64 latent grid) over a cached 256-token
+  bf16 text prefix; q/k/v/out/gate_up in Q4_K, the down projection in Q6_K
+  (TransformerBlock::forward, src/quantized_transformer.rs:258-285, at the
+  sizes of src/transformer.rs:63-88). This runs the 256 x 256 GEMM with its
+  fused q/k/v (32 heads), SwiGLU (N = 24576) and residual (Q6_K, K = 12288)
+  epilogues and its XCD-aware tile order, on 16 x 16..96 tiles.
+- The image-conditioned multi-reference step with true CFG: batch 2 (the two
+  prompts), 4096 target tokens over an 8448-token cached prefix each (256 text
+  + 2 condition images of 64 x 64 latents), 12544 keys; Q8_0 weights
+  (src/quantized_transformer.rs:143-148, src/pipeline.rs:154-155,178-186).
+- The Q8_0 dequant-GEMM sets at 4352 and 256 tokens: fused QKV 12288 x 4096,
+  out 4096 x 4096, MLP up 16384 x 4096 and down 4096 x 16384
+  (src/quantized_transformer.rs:19-33).
+
+Bars. Against the oracle's exact mode (f32 activations, f64 sums of the exact
+weights): cosine >= 0.9999 on the output and on the update x_out - x, and
+max|a-b|/max|b| <= 2e-2. Against its candle mode (the reference CPU path, whose
+activations are quantized to int8 per 256 values for K-quant weights and per 32
+for Q8_0): max|a-b|/max|b| <= 2e-2, and a cosine no lower than the candle
+path's own cosine to exact arithmetic (less 2e-5) on the same rows. At hidden
+4096 with MLP 12288 the int8 quantization of the SwiGLU hidden state alone puts
+the candle output at cosine ~0.99988 from exact arithmetic, below the 0.9999
+that a direct comparison would ask; the bf16 activations here are ~20x closer
+to exact arithmetic than that, and the test asserts that the GPU lies closer to
+the exact product than the candle path does. Where the oracle would take
+minutes, the query side runs for sampled token rows only
+(oracle.block_forward_rows: every row's K and V, bit-identical rows).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import synth
+from gpu_util import bf16_dev, cos_sim, max_abs_rel, host, stream
+from test_gpu_block import make_case, run_block
+from test_gpu_kernels import _attention_case
+
+pytestmark = pytest.mark.gpu
+
+CFG4 = dict(hidden=4096, heads=32, head_dim=128, mlp=12288)
+
+
+def sampled_rows(rng, m, tile=256, extra=48):
+    """First and last rows, both rows at every 256-row tile seam, and random rows."""
+    seams = np.arange(tile, m, tile)
+    rows = np.concatenate([np.arange(0, 4), seams - 1, seams, rng.choice(m, extra, replace=False),
+                           np.arange(m - 4, m)])
+    return np.unique(rows)
+
+
+def check_block(got, cand, exact, x):
+    """got, cand, exact: the same token rows [R, hidden]; x: their inputs."""
+    c_ge, c_ce = cos_sim(got, exact), cos_sim(cand, exact)
+    u_ge, u_ce = cos_sim(got - x, exact - x), cos_sim(cand - x, exact - x)
+    c_gc = cos_sim(got, cand)
+    print(f"cos(gpu, exact) {c_ge:.7f} update {u_ge:.7f}; cos(candle, exact) {c_ce:.7f} update {u_ce:.7f}; "
+          f"cos(gpu, candle) {c_gc:.7f}; mar gpu-exact {max_abs_rel(got, exact):.2e} "
+          f"gpu-candle {max_abs_rel(got, cand):.2e}", flush=True)
+    assert c_ge >= 0.9999 and u_ge >= 0.9999 and max_abs_rel(got, exact) <= 2e-2
+    assert c_ge >= c_ce and u_ge >= u_ce        # closer to exact arithmetic than the candle path
+    assert c_gc >= min(0.9999, c_ce - 2e-5) and max_abs_rel(got, cand) <= 2e-2
+
+
+def kv_close(got, want):
+    assert cos_sim(got, want) >= 0.9999 and max_abs_rel(got, want) <= 2e-2, (cos_sim(got, want),
+                                                                            max_abs_rel(got, want))
+
+
+def test_block_1024_q4km_full_size(torch_cuda, qctx):
+    b, s, p = 1, 4096, 256
+    print("case: block 1024^2 Q4_K_M, hidden 4096, 32 heads, MLP 12288, 4096 tokens over 256", flush=True)
+    w, x, mod, pe, kpre, vpre = make_case(4, CFG4, b, s, p, synth.Q4_K, synth.Q6_K)
+    got, (k, v) = run_block(torch_cuda, qctx, CFG4, w, x, mod, pe, kpre, vpre, want_kv=True)
+    assert np.isfinite(got).all()
+    # every output row against the candle-mode oracle
+    ref, kr, vr = O.block_forward(CFG4, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
+    assert max_abs_rel(got, ref) <= 2e-2
+    kv_close(k, kr)
+    kv_close(v, vr)
+    # sampled rows against exact mode (and candle on the same rows), every K / V
+    rows = sampled_rows(np.random.default_rng(40), s)
+    ref_e, kre, vre = O.block_forward_rows(CFG4, w, x, mod, pe, rows, kpre, vpre, mode=O.EXACT)
+    check_block(got.reshape(s, -1)[rows], ref.reshape(s, -1)[rows], ref_e, x.reshape(s, -1)[rows])
+    kv_close(k, kre)
+    kv_close(v, vre)
+
+
+def multi_ref_pe(text_len, cond, grid):
+    """RoPE rows of the target over a joint layout of text, condition images and
+    the target (EmbedNd::forward, src/rope.rs:104-211): positions run on past the
+    condition images, so the target's frame index is text_len + the images' extents."""
+    shapes = [(1, g, g) for g in cond] + [(1, grid, grid)]
+    mask = [0] * text_len + [1] * (sum(g * g for g in cond) + grid * grid)
+    return O.rope_table(shapes, mask)[-grid * grid:]
+
+
+def test_multi_ref_attention_full_size(torch_cuda, qctx):
+    """Batch 2, 32 heads, 4096 queries over an 8448-token cached prefix plus 4096
+    own keys (12544 keys): sampled query rows of both batch entries against the
+    oracle's exact (f64) attention on the same bf16 Q/K/V."""
+    b, h, sq, p = 2, 32, 4096, 8448
+    print("case: multi-reference attention B2 H32 4096 queries, 8448 + 4096 keys", flush=True)
+    got, q, ko, vo, kp, vp = _attention_case(torch_cuda, qctx, b, h, sq, p, sq, seed=5)
+    assert np.isfinite(got).all()
+    rows = np.array([0, 1, 31, 32, 255, 256, 1777, 2048, 3333, 4094, 4095])
+    want = O.attention(q[:, :, rows], ko, vo, kp, vp, mode=O.EXACT)
+    g = got[:, :, rows]
+    assert cos_sim(g, want) >= 0.9999 and max_abs_rel(g, want) <= 2e-2, (cos_sim(g, want), max_abs_rel(g, want))
+    for bb in range(b):
+        assert cos_sim(g[bb], want[bb]) >= 0.9999
+
+
+def test_multi_ref_block_q8_0_full_size(torch_cuda, qctx):
+    """One Q8_0 block of the multi-reference step, both CFG prompts batched: 2 x 4096
+    target tokens, each prompt over its own 8448-token bf16 prefix cache. Every K / V
+    against the candle-mode oracle; the output on sampled rows of both prompts
+    against exact and candle mode."""
+    b, s, p = 2, 4096, 8448
+    print("case: multi-reference block Q8_0, B2 x 4096 tokens over 8448-token prefixes", flush=True)
+    rng = np.random.default_rng(55)
+    w = synth.block_weights(55, CFG4["hidden"], CFG4["heads"], CFG4["mlp"], synth.Q8_0, synth.Q8_0)
+    x = rng.standard_normal((b, s, CFG4["hidden"]), dtype=np.float32)
+    mod = (rng.standard_normal((b, 1, 4 * CFG4["hidden"]), dtype=np.float32) * 0.5).astype(np.float32)
+    pe = multi_ref_pe(256, [64, 64], 64)
+    kpre = O.f32_to_bf16(rng.standard_normal((b, CFG4["heads"], p, 128), dtype=np.float32))
+    vpre = O.f32_to_bf16(rng.standard_normal((b, CFG4["heads"], p, 128), dtype=np.float32))
+    got, (k, v) = run_block(torch_cuda, qctx, CFG4, w, x, mod, pe, kpre, vpre, want_kv=True)
+    assert np.isfinite(got).all()
+    r0 = sampled_rows(np.random.default_rng(56), s, extra=24)
+    rows = np.concatenate([r0, s + r0])
+    got_r = got.reshape(b * s, -1)[rows]
+    xr = x.reshape(b * s, -1)[rows]
+    ref, kr, vr = O.block_forward_rows(CFG4, w, x, mod, pe, rows, kpre, vpre, mode=O.CANDLE)
+    kv_close(k, kr)
+    kv_close(v, vr)
+    ref_e, _, _ = O.block_forward_rows(CFG4, w, x, mod, pe, rows, kpre, vpre, mode=O.EXACT)
+    check_block(got_r, ref, ref_e, xr)
+
+
+Q8_SETS = {"qkv": (12288, 4096), "out": (4096, 4096), "up": (16384, 4096), "down": (4096, 16384)}
+
+
+@pytest.mark.parametrize("m", [4352, 256])
+@pytest.mark.parametrize("name", list(Q8_SETS))
+def test_q8_0_gemm_sets_sampled_rows(torch_cuda, qctx, name, m):
+    """A [m x K] bf16 ~ N(0,1) times a Q8_0 weight set from N(0, 0.02) (the GGML
+    rule d = amax/127), bf16 output: sampled rows (every tile seam, head and
+    tail) against the oracle's exact and candle modes."""
+    torch = torch_cuda
+    n, k = Q8_SETS[name]
+    print(f"case: Q8_0 {name} {n}x{k} at {m} tokens", flush=True)
+    rng = np.random.default_rng(n + k + m)
+    _, w, _, _ = synth.weight(rng, synth.Q8_0, n, k)
+    W = qctx.upload(synth.Q8_0, n, k, w.tobytes())
+    a_dev, a = bf16_dev(torch, rng.standard_normal((m, k), dtype=np.float32))
+    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    qctx.qmatmul(W, a_dev.data_ptr(), m, k, y.data_ptr(), synth.BF16, stream(torch))
+    got = host(y.float())
+    W.free()
+    assert np.isfinite(got).all()
+    rows = sampled_rows(rng, m, tile=128 if m < 512 else 256, extra=16)
+    for mode in (O.EXACT, O.CANDLE):
+        want = O.qmatmul(synth.Q8_0, w, n, k, a[rows], mode)
+        g = got[rows]
+        assert cos_sim(g, want) >= 0.9999 and max_abs_rel(g, want) <= 2e-2, (mode, cos_sim(g, want),
+                                                                            max_abs_rel(g, want))

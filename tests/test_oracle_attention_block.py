@@ -194,3 +194,49 @@ def test_block_cached_equals_uncached(mode):
     ref = out_full[:, p:]
     assert cos_sim(out_cached - x_img, ref - x_img) > 0.99999
     assert np.max(np.abs(out_cached - ref)) / np.max(np.abs(ref)) < 1e-3
+
+
+@pytest.mark.parametrize("mode", [O.CANDLE, O.EXACT])
+@pytest.mark.parametrize("per_token_mod,masked,fused", [(False, False, True), (True, True, False),
+                                                        (False, True, True)])
+def test_block_rows_equal_full_block_rows(mode, per_token_mod, masked, fused):
+    """oq_block_forward_rows (query side for a subset of token rows) against the
+    full forward: bit-identical rows and K/V, over two batch entries, a prefix,
+    per-token modulation rows, a block-causal mask and the separate proj/gate
+    MLP; the rows come unsorted and straddle the batch boundary."""
+    b, s, p = 2, 20, 6
+    w, _, _, rng = tiny_inputs(44, s, fused=fused)
+    x = rng.standard_normal((b, s, CFG["hidden"])).astype(np.float32)
+    mod = (rng.standard_normal((b, s if per_token_mod else 1, 4 * CFG["hidden"])) * 0.5).astype(np.float32)
+    pe = O.rope_table([(1, 4, 5)], [0] * p + [1] * s)[p:]
+    kpre = O.f32_to_bf16(rng.standard_normal((b, 2, p, 128)))
+    vpre = O.f32_to_bf16(rng.standard_normal((b, 2, p, 128)))
+    mask = None
+    if masked:
+        mask = (rng.random((b, s, p + s)) < 0.7).astype(np.uint8)
+        mask[:, :, p] = 1   # every query keeps at least one key
+    full, kf, vf = O.block_forward(CFG, w, x, mod, pe, kpre, vpre, mask=mask, mode=mode)
+    rows = np.array([27, 3, 0, 19, 20, 39, 11])
+    got, kr, vr = O.block_forward_rows(CFG, w, x, mod, pe, rows, kpre, vpre, mask=mask, mode=mode)
+    assert np.array_equal(got, full.reshape(b * s, -1)[rows])
+    assert np.array_equal(kr, kf) and np.array_equal(vr, vf)
+
+
+def test_exact_gemm_is_row_and_tile_independent():
+    """Exact mode's f64 sums depend on the output's own row and column only:
+    any row subset, odd M and N and a K that is not a multiple of 4 (f32
+    weights) give bit-identical outputs, equal to numpy's f64 product up to the
+    final rounding to f32."""
+    rng = np.random.default_rng(45)
+    for t, n, k in ((O.F32, 37, 75), (O.Q8_0, 70, 96), (O.Q4_K, 33 * 4, 512)):
+        m = 67
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        if t == O.F32:
+            w = rng.standard_normal((n, k)).astype(np.float32).view(np.uint8).ravel()
+        else:
+            _, w, _, _ = synth.weight(rng, t, n, k)
+        y = O.qmatmul(t, w, n, k, x, O.EXACT)
+        rows = np.array([66, 0, 33, 5])
+        assert np.array_equal(O.qmatmul(t, w, n, k, x[rows], O.EXACT), y[rows])
+        want = x.astype(np.float64) @ O.dequantize(t, w, n * k).reshape(n, k).astype(np.float64).T
+        assert np.max(np.abs(y - want)) <= 1e-6 * np.abs(want).max()

@@ -8,6 +8,7 @@ import pytest
 import model as OM
 import oracle as O
 import qimm
+import synth
 
 
 # ---- sigmas: ports of src/scheduler.rs:148-185, plus independent checks ----
@@ -104,3 +105,125 @@ def test_zero_timestep_embedding_constant():
     # zero_modulation feeds the constant [cos 0 ..., sin 0 ...] (src/quantized_transformer.rs:336-340)
     z = O.timestep_embedding(np.array([0.0], np.float32))
     assert np.array_equal(z, OM.zero_sinusoid(1))
+
+
+# ---- timestep embedding: closed forms of src/scheduler.rs:101-126 ----
+
+def _angles(t):
+    return 1000.0 * np.float64(t) * 10000.0 ** (-np.arange(128) / 128.0)
+
+
+@pytest.mark.parametrize("t", [0.001, 0.3, 0.97, 1.0])
+def test_timestep_embedding_closed_form(t):
+    """[cos(1000 t f_i) | sin(1000 t f_i)], f_i = 10000^(-i/128): cos first, the
+    1000 time factor, exponent i/128 (not i/127). The tolerance covers the f32
+    argument at t = 1 (angles up to 1000 rad, a few ulp each)."""
+    got = O.timestep_embedding(np.array([t], np.float32))[0].astype(np.float64)
+    a = _angles(np.float32(t))
+    assert np.abs(got[:128] - np.cos(a)).max() <= 3e-4
+    assert np.abs(got[128:] - np.sin(a)).max() <= 3e-4
+
+
+def test_timestep_embedding_known_points():
+    e = O.timestep_embedding(np.array([0.001, np.pi / 2000, 1e-6], np.float32)).astype(np.float64)
+    # t = 0.001: the first angle is exactly 1 rad
+    assert abs(e[0, 0] - np.cos(1.0)) < 1e-6 and abs(e[0, 128] - np.sin(1.0)) < 1e-6
+    # t = pi/2000: the first angle is pi/2
+    assert abs(e[1, 0]) < 1e-6 and abs(e[1, 128] - 1.0) < 1e-6
+    # tiny t: cos half ~ 1, sin half ~ the angles themselves, which fall by 10000^(-1/128) per index
+    assert np.all(np.abs(e[2, :128] - 1.0) < 1e-6)
+    ratio = e[2, 129:256] / e[2, 128:255]
+    assert np.allclose(ratio, 10000.0 ** (-1 / 128), rtol=1e-4)
+
+
+def test_timestep_embedding_angles_recovered():
+    # t = 0.003: every angle lies in (0, 3], so atan2 recovers it without wrapping
+    e = O.timestep_embedding(np.array([0.003], np.float32))[0].astype(np.float64)
+    ang = np.arctan2(e[128:], e[:128])
+    assert np.allclose(ang, _angles(np.float32(0.003)), rtol=2e-6, atol=1e-7)
+
+
+# ---- oracle/model.py compositions: special weights with closed-form outputs ----
+
+def _f32w(mat):
+    mat = np.ascontiguousarray(mat, dtype=np.float32)
+    return (synth.F32, mat.view(np.uint8).ravel(), mat.shape[0], mat.shape[1])
+
+
+def test_time_embed_identity_weights_is_silu():
+    # linear_2(silu(linear_1(t))) with identity linears = silu(t) (src/quantized_transformer.rs:50-54)
+    rng = np.random.default_rng(60)
+    t = rng.standard_normal((3, 256)).astype(np.float32)
+    g = {"t_linear_1": _f32w(np.eye(256)), "t_linear_2": _f32w(np.eye(256))}
+    got = OM.time_embed(g, t)
+    want = t.astype(np.float64) / (1.0 + np.exp(-t.astype(np.float64)))
+    assert np.abs(got - want).max() < 1e-6
+
+
+def test_modulation_chunks_and_silu():
+    # Modulation::forward = silu(t_emb) . W^T (:226-228), [B, 1, 4h]; W rows [I; 2I; 0; -I]
+    rng = np.random.default_rng(61)
+    h = 64
+    temb = rng.standard_normal((2, h)).astype(np.float32)
+    eye = np.eye(h)
+    g = {"modulation": _f32w(np.concatenate([eye, 2 * eye, 0 * eye, -eye]))}
+    got = OM.modulation(g, temb)
+    s = temb.astype(np.float64) / (1.0 + np.exp(-temb.astype(np.float64)))
+    assert got.shape == (2, 1, 4 * h)
+    want = np.concatenate([s, 2 * s, 0 * s, -s], axis=-1)[:, None, :]
+    assert np.abs(got - want).max() < 1e-6
+
+
+@pytest.mark.parametrize("stored", [0.0, 0.25])
+def test_text_embedder_closed_form(stored):
+    """QTextEmbedder (:76-81) with identity in/out layers: gelu_tanh(x / rms(x) * (1 + stored)),
+    the stored norm weight being scale - 1 (ZeroCenterRMSNorm). An erf GELU or a missing
+    +1 fails this."""
+    rng = np.random.default_rng(62)
+    d = 64
+    x = (3.0 * rng.standard_normal((2, 5, d))).astype(np.float32)
+    g = {"txt_norm": _f32w(np.full((1, d), stored)), "txt_in": _f32w(np.eye(d)), "txt_out": _f32w(np.eye(d))}
+    got = OM.txt_in(g, x)
+    xd = x.astype(np.float64)
+    z = xd / np.sqrt((xd ** 2).mean(-1, keepdims=True) + 1e-6) * (1.0 + stored)
+    want = 0.5 * z * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (z + 0.044715 * z ** 3)))
+    assert np.abs(got - want).max() < 2e-6
+
+
+@pytest.mark.parametrize("c", [0.0, 1.5, -0.5])
+def test_final_layer_scale_after_layernorm(c):
+    """FinalLayer (:300-309) + proj_out: LN(h) * (1 + linear(silu(t_emb))). With
+    proj_out = I and a norm_out weight that maps silu(t_emb) to the constant c,
+    every output row has mean 0 and standard deviation |1 + c|; scaling before the
+    norm, or skipping the silu, gives another spread."""
+    rng = np.random.default_rng(63)
+    hid = 64
+    h = (2.0 * rng.standard_normal((2, 7, hid)) + 0.5).astype(np.float32)
+    t0 = 1.25
+    temb = np.zeros((2, hid), np.float32)
+    temb[:, 0] = t0
+    w = np.zeros((hid, hid))
+    w[:, 0] = c / (t0 / (1.0 + np.exp(-t0)))
+    g = {"norm_out": _f32w(w), "proj_out": _f32w(np.eye(hid))}
+    out = OM.final_layer(g, h, temb).astype(np.float64)
+    assert np.abs(out.mean(-1)).max() < 1e-5
+    assert np.abs(out.std(-1) - abs(1.0 + c)).max() < 1e-4
+
+
+def test_model_forward_without_blocks():
+    """With no blocks, identity img_in / proj_out and a zero norm_out the cached
+    forward (:471-551) returns LayerNorm(latents); with proj_out zero it returns
+    zero velocity."""
+    rng = np.random.default_rng(64)
+    ch, hid = 64, 64
+    lat = rng.standard_normal((1, 9, ch)).astype(np.float32)
+    t_sin = O.timestep_embedding(np.array([0.4], np.float32))
+    g = {"img_in": _f32w(np.eye(hid)), "t_linear_1": _f32w(rng.standard_normal((hid, 256)) * 0.1),
+         "t_linear_2": _f32w(np.eye(hid)), "modulation": _f32w(np.zeros((4 * hid, hid))),
+         "norm_out": _f32w(np.zeros((hid, hid))), "proj_out": _f32w(np.eye(hid))}
+    out = OM.model_forward(dict(hidden=hid), g, [], lat, t_sin, None).astype(np.float64)
+    ld = lat.astype(np.float64)
+    want = (ld - ld.mean(-1, keepdims=True)) / np.sqrt(ld.var(-1, keepdims=True) + 1e-6)
+    assert np.abs(out - want).max() < 1e-5
+    g["proj_out"] = _f32w(np.zeros((ch, hid)))
+    assert not OM.model_forward(dict(hidden=hid), g, [], lat, t_sin, None).any()

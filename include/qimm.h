@@ -106,6 +106,21 @@ int qimm_dequant(qimm_ctx *ctx, int ggml_type, const void *dev_bytes, int64_t n,
 int qimm_qmatmul(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_t m,
                  int64_t lda, void *y, int out_type, void *stream);
 
+/* qimm_qmatmul that allocates nothing, for callers that cannot allocate
+ * device memory during a call (code under HIP graph capture, tight serving
+ * loops). It has no counterpart in the reference. Same arguments, kernels and
+ * results as qimm_qmatmul; the split-K partial sums and arrival counters live
+ * in a static device array of QIMM_NOALLOC_SCRATCH_BYTES (48 MiB) per device,
+ * set up when the device's first context is created and held until the
+ * process ends, instead of the context's growable scratch. Every shape the
+ * library plans needs at most ~34 MB; a product that would need more returns
+ * QIMM_ERR_SHAPE. All calls on one device share that array (it keeps the last
+ * call's contents; the counters return to zero after every call), so calls
+ * that overlap on one device, from any context or stream, race: order them. */
+#define QIMM_NOALLOC_SCRATCH_BYTES (48u << 20)
+int qimm_qmatmul_noalloc(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_t m,
+                         int64_t lda, void *y, int out_type, void *stream);
+
 /* ---------------- host-side layout and RoPE ---------------- */
 
 /* JointLayout::new (src/joint_layout.rs:52-103). text_image_mask may be NULL

@@ -83,6 +83,8 @@ int qimm_ctx_create(int device, qimm_ctx **out) {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return QIMM_ERR_ARG;
     if (hipSetDevice(device) != hipSuccess) return QIMM_ERR_HIP;
+    // once per device: the static scratch of qimm_qmatmul_noalloc
+    if (qimm::noalloc_scratch_setup(device) != hipSuccess) return QIMM_ERR_HIP;
     qimm_ctx *c = new (std::nothrow) qimm_ctx();
     if (!c) return QIMM_ERR_OOM;
     c->device = device;

@@ -200,6 +200,8 @@ int qimm_dequant(qimm_ctx *ctx, int ggml_type, const void *dev_bytes, int64_t n,
 
 namespace {
 
+static_assert(qimm::NOALLOC_SCRATCH_BYTES == QIMM_NOALLOC_SCRATCH_BYTES, "static scratch size of qimm.h");
+
 int qmatmul_check(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_t m, int64_t lda, void *y,
                   int out_type) {
     if (!ctx || !w || !x_bf16 || !y || m < 0) return QIMM_ERR_ARG;
@@ -226,6 +228,29 @@ int qimm_qmatmul(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_
         if (rc) return rc;
         ep.part_ws = (float *)ctx->ws_part;
         ep.part_ws_bytes = ctx->ws_part_bytes;
+    }
+    QIMM_HIP(ctx, qimm::launch_qgemm(w->gw, (const uint16_t *)x_bf16, m, lda,
+                                     out_type == QIMM_TYPE_F32 ? qimm::EPI_F32 : qimm::EPI_BF16, ep,
+                                     (hipStream_t)stream));
+    return QIMM_OK;
+}
+
+int qimm_qmatmul_noalloc(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_t m, int64_t lda, void *y,
+                         int out_type, void *stream) {
+    if (const int rc = qmatmul_check(ctx, w, x_bf16, m, lda, y, out_type)) return rc;
+    qimm::EpiParams ep{};
+    ep.out = y;
+    ep.ldo = w->rows;
+    if (const size_t need = qimm::qgemm_workspace(w->gw, m)) {
+        if (need > qimm::NOALLOC_SCRATCH_BYTES)
+            return set_err(ctx, QIMM_ERR_SHAPE,
+                           "qmatmul_noalloc: this product needs " + std::to_string(need) +
+                               " bytes of scratch, more than the static " +
+                               std::to_string(qimm::NOALLOC_SCRATCH_BYTES) + "; use qimm_qmatmul");
+        void *p = qimm::noalloc_scratch(ctx->device);
+        if (!p) return set_err(ctx, QIMM_ERR_STATE, "qmatmul_noalloc: static scratch not set up on this device");
+        ep.part_ws = (float *)p;
+        ep.part_ws_bytes = qimm::NOALLOC_SCRATCH_BYTES;
     }
     QIMM_HIP(ctx, qimm::launch_qgemm(w->gw, (const uint16_t *)x_bf16, m, lda,
                                      out_type == QIMM_TYPE_F32 ? qimm::EPI_F32 : qimm::EPI_BF16, ep,

@@ -91,6 +91,17 @@ int qgemm_mid_splits(const GemmWeight &w, int64_t m);
 // each after STREAM_COUNTER_BYTES of counters. Without it the unsplit kernels run.
 size_t qgemm_workspace(const GemmWeight &w, int64_t m);
 
+// Static scratch of the allocation-free product (noalloc.hip): one file-scope
+// device array per device. The split planners keep qgemm_workspace below
+// ~34 MB for every shape (short-M partials <= 32 MiB, split 128x128 partials
+// <= 16 MiB, plus the counters), so 48 MiB covers them all.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)48 << 20;  // QIMM_NOALLOC_SCRATCH_BYTES of qimm.h
+// Looks up the array's device address on `device` (which must be current)
+// once, zeroes its counter area and waits; later calls return at once.
+hipError_t noalloc_scratch_setup(int device);
+// The device address looked up by noalloc_scratch_setup, or null before it.
+void *noalloc_scratch(int device);
+
 // Exact GGUF dequantization of raw block bytes (device) to f32 (device).
 hipError_t launch_dequant(int ggml_type, const uint8_t *src, int64_t n, float *out,
                           hipStream_t stream);

@@ -46,6 +46,7 @@ SIGNATURES = [
     ("qimm_weight_device_bytes", _i64, [_vp]),
     ("qimm_dequant", _i32, [_vp, _i32, _vp, _i64, _vp, _vp]),
     ("qimm_qmatmul", _i32, [_vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp]),
+    ("qimm_qmatmul_noalloc", _i32, [_vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp]),
     ("qimm_joint_layout", _i32, [_i64, _vp, _vp, _i64, _i64, _i64, _vp, _i64,
                                  C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i64)]),
     ("qimm_rope_table", _i32, [_vp, _i64, _vp, _i64, _vp, C.c_double, _vp]),
@@ -204,6 +205,11 @@ class Context:
 
     def qmatmul(self, w: "Weight", x_dev: int, m: int, lda: int, y_dev: int, out_type: int, stream: int = 0):
         self.check(self.lib.qimm_qmatmul(self.h, w.h, x_dev, m, lda, y_dev, out_type, stream), "qimm_qmatmul")
+
+    def qmatmul_noalloc(self, w: "Weight", x_dev: int, m: int, lda: int, y_dev: int, out_type: int, stream: int = 0):
+        """qmatmul with the library's static per-device scratch: no device allocation in the call."""
+        self.check(self.lib.qimm_qmatmul_noalloc(self.h, w.h, x_dev, m, lda, y_dev, out_type, stream),
+                   "qimm_qmatmul_noalloc")
 
     # -- cache --
     def kv_create(self, layers: int, batch: int, heads: int, prefix_len: int, head_dim: int = 128) -> "KvCache":

@@ -51,7 +51,8 @@ def main():
     ap.add_argument("--no-weight-streaming", action="store_true",
                     help="skip the short-token weight-streaming measurements")
     ap.add_argument("--no-other-configs", action="store_true",
-                    help="skip the Q8_0 dequant-GEMM sets and the multi-reference attention measurements")
+                    help="skip the Q8_0 dequant-GEMM sets, the multi-reference attention, the MLP-16384 block, "
+                         "the 8448-token prefix fill, the config-1 block and the torch SDPA bar")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB, the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc pass")
@@ -161,40 +162,13 @@ def main():
         nprof += 1
     for blk in blocks:
         blk.profile(False)
-    if nprof == 0:
-        for blk in blocks:
-            blk.free()
-        kv.free()
-        log("bench: no profiled steps, stage report skipped")
-        return
-    stages = {k: v / nprof for k, v in stage_sum.items()}
-    log("bench: stages " + ", ".join(f"{k} {v:.3f}" for k, v in stages.items()) + " ms")
-
     att_flop = 4.0 * HEADS * S_IMG * (S_IMG + P_TXT) * HD
-    gemm = {"qkv": (3 * HID, HID), "out_proj": (HID, HID), "gate_up": (2 * MLP, HID), "down": (HID, MLP)}
-    kernels = {"attention": {"ms": stages["attention"], "gflop": att_flop / 1e9}}
-    for name, (n, k) in gemm.items():
-        kernels[name] = {"ms": stages[name], "gflop": 2.0 * S_IMG * n * k / 1e9}
-    qk4 = synth.row_bytes(synth.Q4_K, HID)
-    kernels["qkv"]["weight_bytes"] = 3 * HID * qk4
-    kernels["out_proj"]["weight_bytes"] = HID * qk4
-    kernels["gate_up"]["weight_bytes"] = 2 * MLP * qk4
-    kernels["down"]["weight_bytes"] = HID * synth.row_bytes(synth.Q6_K, MLP)
-    for kname, kd in kernels.items():
-        kd["tflops"] = kd["gflop"] / kd["ms"]
-        kd["frac_bf16_peak"] = kd["tflops"] / PEAK_BF16_TFLOPS
-        if "weight_bytes" in kd:
-            kd["weight_gbps"] = kd["weight_bytes"] / kd["ms"] / 1e6
-        log(f"bench: {kname}: {kd['ms']:.3f} ms, {kd['tflops']:.1f} TFLOP/s")
-
-    dom_name = max(kernels, key=lambda n: kernels[n]["ms"])
-    dom = kernels[dom_name]
-    traffic = measured_traffic(dom_name)
-    roofline = {"kernel": dom_name, "bound": "mfma", "achieved": round(dom["tflops"], 2),
-                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(dom["tflops"] / PEAK_BF16_TFLOPS, 4),
-                "traffic": traffic["bytes"] if traffic else None, "flop_per_launch": dom["gflop"] * 1e9}
-    if traffic:
-        roofline["traffic_source"] = traffic["source"]
+    kernels = roofline = stages = None
+    if nprof == 0:
+        log("bench: no profiled steps, stage report skipped")
+    else:
+        stages = {k: v / nprof for k, v in stage_sum.items()}
+        kernels, roofline = stage_report(stages, att_flop, synth)
 
     block_flop = att_flop + 2.0 * S_IMG * HID * (3 * HID + HID + 2 * MLP) + 2.0 * S_IMG * MLP * HID
 
@@ -202,10 +176,14 @@ def main():
     streaming = None if args.no_weight_streaming else weight_streaming(ctx, torch, np, qimm, synth, stream, host_w0)
 
     # ---- the other measured configurations: Q8_0 dequant-GEMM sets, multi-reference attention ----
-    q8 = mref = None
+    q8 = mref = mlp16k = pfill = cfg1 = sdpa = None
     if not args.no_other_configs:
         q8 = q8_gemm_sets(ctx, torch, np, qimm, synth, stream)
         mref = multi_ref_attention(ctx, torch, qimm, stream)
+        mlp16k = block_mlp16384(ctx, torch, np, qimm, synth, stream, kv, x, x_out, mod, pe)
+        pfill = prefix_fill_8448(ctx, torch, np, qimm, synth, stream)
+        cfg1 = config1_block(ctx, torch, np, qimm, synth, stream, cpu=not args.no_cpu_baseline)
+        sdpa = torch_sdpa_bar(torch, stream)
 
     # ---- CPU baseline: the oracle in candle mode on a bounded sample ----
     cpu = None
@@ -233,19 +211,53 @@ def main():
                    "hidden": HID, "heads": HEADS, "head_dim": HD, "mlp": MLP, "batch": 1,
                    "image_tokens": S_IMG, "prefix_tokens": P_TXT, "distinct_blocks": args.blocks,
                    "weights_mb_per_block": round(wbytes / 1e6, 1)},
-        "attention_tflops": round(kernels["attention"]["tflops"], 2),
-        "attention_frac_bf16_peak": round(kernels["attention"]["frac_bf16_peak"], 4),
+        "attention_tflops": round(kernels["attention"]["tflops"], 2) if kernels else None,
+        "attention_frac_bf16_peak": round(kernels["attention"]["frac_bf16_peak"], 4) if kernels else None,
         "block_tflops": round(block_flop / ms_step / 1e9, 2),
         "block_frac_bf16_peak": round(block_flop / ms_step / 1e9 / PEAK_BF16_TFLOPS, 4),
-        "stages_ms": {k: round(v, 4) for k, v in stages.items()},
-        "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},
+        "stages_ms": {k: round(v, 4) for k, v in stages.items()} if stages else None,
+        "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()} if kernels else None,
         "roofline": roofline,
         "weight_streaming": streaming,
         "dequant_gemm_q8_0": q8,
         "multi_ref_attention": mref,
+        "block_mlp16384": mlp16k,
+        "prefix_fill_8448": pfill,
+        "config1_block": cfg1,
+        "attention_torch_sdpa": sdpa,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+
+
+def stage_report(stages, att_flop, synth):
+    """Per-kernel ms, TFLOP/s and roofline fraction from the stage times of the
+    block step; the dominant kernel's roofline with its measured HBM traffic."""
+    log("bench: stages " + ", ".join(f"{k} {v:.3f}" for k, v in stages.items()) + " ms")
+    gemm = {"qkv": (3 * HID, HID), "out_proj": (HID, HID), "gate_up": (2 * MLP, HID), "down": (HID, MLP)}
+    kernels = {"attention": {"ms": stages["attention"], "gflop": att_flop / 1e9}}
+    for name, (n, k) in gemm.items():
+        kernels[name] = {"ms": stages[name], "gflop": 2.0 * S_IMG * n * k / 1e9}
+    qk4 = synth.row_bytes(synth.Q4_K, HID)
+    kernels["qkv"]["weight_bytes"] = 3 * HID * qk4
+    kernels["out_proj"]["weight_bytes"] = HID * qk4
+    kernels["gate_up"]["weight_bytes"] = 2 * MLP * qk4
+    kernels["down"]["weight_bytes"] = HID * synth.row_bytes(synth.Q6_K, MLP)
+    for kname, kd in kernels.items():
+        kd["tflops"] = kd["gflop"] / kd["ms"]
+        kd["frac_bf16_peak"] = kd["tflops"] / PEAK_BF16_TFLOPS
+        if "weight_bytes" in kd:
+            kd["weight_gbps"] = kd["weight_bytes"] / kd["ms"] / 1e6
+        log(f"bench: {kname}: {kd['ms']:.3f} ms, {kd['tflops']:.1f} TFLOP/s")
+    dom_name = max(kernels, key=lambda n: kernels[n]["ms"])
+    dom = kernels[dom_name]
+    traffic = measured_traffic(dom_name)
+    roofline = {"kernel": dom_name, "bound": "mfma", "achieved": round(dom["tflops"], 2),
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(dom["tflops"] / PEAK_BF16_TFLOPS, 4),
+                "traffic": traffic["bytes"] if traffic else None, "flop_per_launch": dom["gflop"] * 1e9}
+    if traffic:
+        roofline["traffic_source"] = traffic["source"]
+    return kernels, roofline
 
 
 def weight_streaming(ctx, torch, np, qimm, synth, stream, host_w, token_counts=(16, 64), iters=50):
@@ -368,6 +380,212 @@ def multi_ref_attention(ctx, torch, qimm, stream, iters=10):
             "own_tokens": S, "keys": P + S}
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def upload_block(ctx, qimm, synth, cfg, w, types):
+    """Block from host GGUF bytes: w[name] = bytes, types[name] = (ggml type, rows, cols)."""
+    keep = []
+    T = qimm.BlockTensors()
+    for name, field in (("to_q", "to_q"), ("to_k", "to_k"), ("to_v", "to_v"), ("to_out", "to_out"),
+                        ("gate_up", "gate_up"), ("down", "mlp_out")):
+        t, r, c = types[name]
+        setattr(T, field, qimm.make_tensor(t, r, c, w[name].tobytes(), keep))
+    for name in ("norm_q", "norm_k"):
+        setattr(T, name, qimm.make_tensor(synth.F32, HD, 1, w[name].tobytes(), keep))
+    return ctx.block_create(qimm.BlockConfig(cfg["hidden"], cfg["heads"], HD, cfg["mlp"]), T)
+
+
+def random_block(np, synth, seed, hidden, mlp, attn_type, down_type):
+    rng = np.random.default_rng(seed)
+    types = {"to_q": (attn_type, hidden, hidden), "to_k": (attn_type, hidden, hidden),
+             "to_v": (attn_type, hidden, hidden), "to_out": (attn_type, hidden, hidden),
+             "gate_up": (attn_type, 2 * mlp, hidden), "down": (down_type, hidden, mlp)}
+    w = {n: synth.random_blocks(rng, t, r, c) for n, (t, r, c) in types.items()}
+    w["norm_q"] = (1 + 0.02 * rng.standard_normal(HD)).astype(np.float32)
+    w["norm_k"] = (1 + 0.02 * rng.standard_normal(HD)).astype(np.float32)
+    return w, types
+
+
+def timed(torch, stream, fn, iters, warmup=2):
+    for _ in range(warmup):
+        fn()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(iters):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def block_mlp16384(ctx, torch, np, qimm, synth, stream, kv, x, x_out, mod, pe, nblocks=2, iters=16):
+    """The block step at 1024x1024 with an MLP of 16384 (the MLP width the headline
+    configuration states; the reference's own blocks use 3 x hidden = 12288): the same
+    4096 tokens over the 256-token prefix, Q4_K with a Q6_K down projection, two distinct
+    blocks cycled (more bytes than the last-level cache). 2491.1 GFLOP per step."""
+    mlp = 16384
+    blocks = []
+    for i in range(nblocks):
+        w, types = random_block(np, synth, 3000 + i, HID, mlp, synth.Q4_K, synth.Q6_K)
+        blocks.append(upload_block(ctx, qimm, synth, dict(hidden=HID, heads=HEADS, mlp=mlp), w, types))
+        del w
+    sh = stream.cuda_stream
+    it = [0]
+
+    def step():
+        i = it[0]
+        it[0] += 1
+        blocks[i % nblocks].forward(x.data_ptr(), x_out.data_ptr(), 1, S_IMG, mod.data_ptr(), pe.data_ptr(), kv,
+                                    i % LAYERS, None, None, sh)
+
+    ms = timed(torch, stream, step, iters, warmup=4)
+    assert torch.isfinite(x_out).all().item(), "non-finite block output"
+    for b in blocks:
+        b.free()
+    flop = 4.0 * HEADS * S_IMG * (S_IMG + P_TXT) * HD + 2.0 * S_IMG * HID * (4 * HID + 3 * mlp)
+    log(f"bench: block step with MLP 16384: {ms:.3f} ms, {flop / ms / 1e9:.0f} TFLOP/s")
+    return {"ms": round(ms, 4), "gflop": round(flop / 1e9, 1), "tflops": round(flop / ms / 1e9, 1),
+            "frac_bf16_peak": round(flop / ms / 1e9 / PEAK_BF16_TFLOPS, 4), "mlp": mlp}
+
+
+def prefix_fill_8448(ctx, torch, np, qimm, synth, stream, iters=4):
+    """The prefix pass of the multi-reference step (prefix_kv): one Q8_0 block over the
+    8448 prefix tokens of one prompt (256 text + 2 condition images of 64 x 64 latents),
+    block-causal mask from the image ids, the t = 0 modulation row, the layer's K/V
+    written out as the cache entry. Attention work counts the allowed (query, key)
+    pairs only: 4 x 32 heads x 128 x pairs."""
+    P, T = 8448, 256
+    w, types = random_block(np, synth, 4000, HID, MLP, synth.Q8_0, synth.Q8_0)
+    blk = upload_block(ctx, qimm, synth, dict(hidden=HID, heads=HEADS, mlp=MLP), w, types)
+    del w
+    ids = np.array([-1] * T + [0] * 4096 + [1] * 4096, dtype=np.int32)
+    pe_h = qimm.rope_table([(1, 64, 64), (1, 64, 64)], [0] * T + [1] * 8192)
+    g = torch.Generator(device="cuda").manual_seed(9)
+    xp = torch.randn((1, P, HID), generator=g, device="cuda")
+    xo = torch.empty_like(xp)
+    mod0 = 0.5 * torch.randn((1, 1, 4 * HID), generator=g, device="cuda")
+    ids_d = torch.from_numpy(ids).cuda()
+    pe_d = torch.from_numpy(np.ascontiguousarray(pe_h)).cuda()
+    k_o = torch.empty((1, HEADS, P, HD), dtype=torch.bfloat16, device="cuda")
+    v_o = torch.empty_like(k_o)
+    sh = stream.cuda_stream
+
+    def call():
+        blk.forward_masked(xp.data_ptr(), xo.data_ptr(), 1, P, mod0.data_ptr(), 1, pe_d.data_ptr(),
+                           image_ids=ids_d.data_ptr(), k_out=k_o.data_ptr(), v_out=v_o.data_ptr(), stream=sh)
+
+    ms = timed(torch, stream, call, iters)
+    blk.profile(True)
+    call()
+    st = blk.stage_times()
+    blk.profile(False)
+    assert torch.isfinite(xo).all().item(), "non-finite prefix output"
+    blk.free()
+    text_pairs = T * (T + 1) // 2
+    pairs = text_pairs + 4096 * (T + 4096) + 4096 * P
+    att_flop = 4.0 * HEADS * HD * pairs
+    gemm_flop = 2.0 * P * HID * (4 * HID + 3 * MLP)
+    log(f"bench: prefix fill P=8448 (Q8_0 block, block-causal mask): {ms:.3f} ms per block per prompt, "
+        f"attention {st['attention']:.3f} ms ({att_flop / st['attention'] / 1e9:.0f} TFLOP/s on allowed pairs)")
+    return {"ms": round(ms, 4), "attention_ms": round(st["attention"], 4),
+            "attention_gflop_allowed_pairs": round(att_flop / 1e9, 1),
+            "attention_tflops": round(att_flop / st["attention"] / 1e9, 1),
+            "gemm_gflop": round(gemm_flop / 1e9, 1), "stages_ms": {k: round(v, 4) for k, v in st.items()},
+            "prefix_tokens": P, "weights": "Q8_0"}
+
+
+def config1_block(ctx, torch, np, qimm, synth, stream, cpu=True, iters=50):
+    """The reference CPU-path configuration, timed in full on the GPU and on the host
+    cores: hidden 3072, 24 heads x 128, MLP 9216, 256 image tokens (16 x 16 grid) over a
+    64-token bf16 prefix, N(0, 0.02) weights quantized to Q8_0, 63.8 GFLOP per block.
+    The CPU leg is the oracle in candle mode (int8 activations) on the same inputs."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    cfg = dict(hidden=3072, heads=24, head_dim=HD, mlp=9216)
+    b, s, p = 1, 256, 64
+    w = synth.block_weights(11, cfg["hidden"], cfg["heads"], cfg["mlp"], synth.Q8_0)
+    types = {"to_q": (synth.Q8_0, 3072, 3072), "to_k": (synth.Q8_0, 3072, 3072), "to_v": (synth.Q8_0, 3072, 3072),
+             "to_out": (synth.Q8_0, 3072, 3072), "gate_up": (synth.Q8_0, 2 * 9216, 3072),
+             "down": (synth.Q8_0, 3072, 9216)}
+    wb = {n: (w[n][1] if isinstance(w[n], tuple) else w[n]) for n in w}
+    blk = upload_block(ctx, qimm, synth, cfg, wb, types)
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((b, s, cfg["hidden"])).astype(np.float32)
+    mod = (rng.standard_normal((b, 1, 4 * cfg["hidden"])) * 0.5).astype(np.float32)
+    pe_h = qimm.rope_table([(1, 16, 16)], [0] * p + [1] * s)[p:]
+    kpre = rng.standard_normal((b, cfg["heads"], p, HD)).astype(np.float32)
+    vpre = rng.standard_normal((b, cfg["heads"], p, HD)).astype(np.float32)
+    kb = torch.from_numpy(kpre).to(torch.bfloat16)
+    vb = torch.from_numpy(vpre).to(torch.bfloat16)
+    kv = ctx.kv_create(1, b, cfg["heads"], p)
+    kd, vd = kb.cuda(), vb.cuda()
+    sh = stream.cuda_stream
+    kv.store(0, kd.data_ptr(), vd.data_ptr(), sh)
+    xd = torch.from_numpy(x).cuda()
+    xo = torch.empty_like(xd)
+    md = torch.from_numpy(mod).cuda()
+    ped = torch.from_numpy(np.ascontiguousarray(pe_h)).cuda()
+
+    def call():
+        blk.forward(xd.data_ptr(), xo.data_ptr(), b, s, md.data_ptr(), ped.data_ptr(), kv, 0, None, None, sh)
+
+    ms = timed(torch, stream, call, iters, warmup=5)
+    got = xo.cpu().numpy()
+    blk.free()
+    kv.free()
+    flop = 2.0 * s * cfg["hidden"] * (4 * cfg["hidden"] + 3 * cfg["mlp"]) + 4.0 * cfg["heads"] * s * (s + p) * HD
+    out = {"gpu_ms": round(ms, 4), "gflop": round(flop / 1e9, 2), "gpu_tflops": round(flop / ms / 1e9, 1),
+           "weights": "Q8_0", "hidden": 3072, "heads": 24, "mlp": 9216, "tokens": s, "prefix_tokens": p}
+    log(f"bench: config-1 block (hidden 3072, 256 tokens over 64): GPU {ms:.4f} ms")
+    if cpu:
+        kp16 = O.f32_to_bf16(kpre)
+        vp16 = O.f32_to_bf16(vpre)
+        O.lib()
+        t0 = O.now()
+        ref, _, _ = O.block_forward(cfg, w, x, mod, pe_h, kp16, vp16, mode=O.CANDLE)
+        cpu_ms = (O.now() - t0) * 1e3
+        cos = float((got.ravel().astype(np.float64) @ ref.ravel()) /
+                    np.sqrt((got.ravel().astype(np.float64) ** 2).sum() * (ref.ravel().astype(np.float64) ** 2).sum()))
+        out.update({"cpu_ms": round(cpu_ms, 1), "cpu_cores": O.num_threads(), "cpu_model": cpu_model(),
+                    "cpu_kind": "port (oracle, candle mode: int8 activations, integer vec-dots)",
+                    "gpu_vs_cpu_cosine": round(cos, 7)})
+        log(f"bench: config-1 block on the CPU oracle: {cpu_ms:.1f} ms on {O.num_threads()} threads, "
+            f"GPU/CPU output cosine {cos:.7f}")
+    return out
+
+
+def torch_sdpa_bar(torch, stream, iters=20):
+    """torch's fused attention (flash or memory-efficient backend; the math backend is
+    excluded) at the cached step's attention shape: B1, 32 heads, 4096 queries over
+    4352 keys, bf16, as a practical bar for the joint-attention kernel on this GPU."""
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        import torch.nn.functional as F
+        g = torch.Generator(device="cuda").manual_seed(3)
+        q = torch.randn((1, HEADS, S_IMG, HD), generator=g, device="cuda").to(torch.bfloat16)
+        k = torch.randn((1, HEADS, S_IMG + P_TXT, HD), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((1, HEADS, S_IMG + P_TXT, HD), generator=g, device="cuda").to(torch.bfloat16)
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            ms = timed(torch, stream, lambda: F.scaled_dot_product_attention(q, k, v), iters)
+        flop = 4.0 * HEADS * S_IMG * (S_IMG + P_TXT) * HD
+        log(f"bench: torch SDPA at the attention shape: {ms:.3f} ms, {flop / ms / 1e9:.0f} TFLOP/s")
+        return {"ms": round(ms, 4), "tflops": round(flop / ms / 1e9, 1),
+                "frac_bf16_peak": round(flop / ms / 1e9 / PEAK_BF16_TFLOPS, 4)}
+    except Exception as e:  # no fused backend: report why, measure nothing
+        log(f"bench: torch SDPA bar unavailable: {e}")
+        return {"error": str(e)[:200]}
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_block_q4km_1024.json")
 
 
@@ -416,7 +634,8 @@ def cpu_baseline(rows, host_w):
     log(f"cpu baseline: attention {t_att:.2f}s")
     scale = S_IMG / rows
     ms = (t_gemm + t_att) * scale * 1e3
-    return {"value": round(ms, 1), "unit": "ms/block-step", "cores": O.num_threads(), "kind": "port",
+    return {"value": round(ms, 1), "unit": "ms/block-step", "cores": O.num_threads(), "cpu_model": cpu_model(),
+            "kind": "port",
             "sample": f"{rows} of 4096 token rows through q/k/v/out/gate_up/down quantized matmuls plus "
                       f"attention of {rows} queries over 4352 keys, timed and scaled x{scale:g}; "
                       f"LayerNorm/modulation omitted",

@@ -171,7 +171,7 @@ namespace {
 // attn [M,h] | hmid [M,F] (bf16), and the split-K scratch of the short- and
 // mid-M GEMM paths, sized for the largest projection.
 struct WsLayout {
-    size_t modp, xn, q, k, vt, att, h, total, part;
+    size_t modp, xn, q, k, vt, att, h, lim, total, part;
 };
 
 WsLayout ws_layout(const qimm_block *blk, int64_t batch, int64_t seq, int64_t mod_rows) {
@@ -185,6 +185,7 @@ WsLayout ws_layout(const qimm_block *blk, int64_t batch, int64_t seq, int64_t mo
     L.vt = off; off += align_up((size_t)(M * hid) * 2);
     L.att = off; off += align_up((size_t)(M * hid) * 2);
     L.h = off; off += align_up((size_t)(M * F) * 2);
+    L.lim = off; off += align_up((size_t)seq * 4);  // per-query key limits of the block-causal mask
     L.total = off;
     L.part = 0;
     const qimm_weight *ws_list[] = {blk->qkv, blk->q, blk->k, blk->v, blk->out, blk->gate_up, blk->down};
@@ -287,6 +288,7 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
     }
     if (img || kvalid)
         QIMM_HIP(ctx, qimm::launch_attention_masked(qb, pk, pvt, P, kb, vt, seq, batch, H, seq, 1.0f, img, kvalid,
+                                                    (int32_t *)(ws + L.lim),
                                                     att, s));
     else
         QIMM_HIP(ctx, qimm::launch_attention_log2(qb, pk, pvt, P, kb, vt, seq, batch, H, seq, att, s));
@@ -445,14 +447,21 @@ int qimm_attention_masked(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64
     if (mask->image_ids && (P != 0 || so != sq))
         return set_err(ctx, QIMM_ERR_SHAPE, "attention: the block-causal mask needs no prefix and so == sq");
     const hipStream_t s = (hipStream_t)stream;
+    int32_t *lim = nullptr;
+    if (mask->image_ids) {
+        QIMM_HIP(ctx, hipSetDevice(ctx->device));
+        const int rc = ensure_workspace(ctx, (size_t)sq * 4);
+        if (rc) return rc;
+        lim = (int32_t *)ctx->ws;
+    }
     const uint16_t *pk = nullptr, *pvt = nullptr;
     if (kv) {
         const int rc = kv_layer(kv, layer, s, &pk, &pvt);
         if (rc) return rc;
     }
     QIMM_HIP(ctx, qimm::launch_attention_masked(q, pk, pvt, P, k_own, vt_own, so, batch, heads, sq,
-                                                scale * 1.4426950408889634f, mask->image_ids, mask->key_valid, out,
-                                                s));
+                                                scale * 1.4426950408889634f, mask->image_ids, mask->key_valid, lim,
+                                                out, s));
     return kv ? kv_release(kv, layer, s) : QIMM_OK;
 }
 

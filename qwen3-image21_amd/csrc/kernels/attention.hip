@@ -23,6 +23,12 @@
 //    scale*log2 e) and the rescale of O is a rare wave-uniform branch; row
 //    sums use v_dot2_f32_bf16 over the packed bf16 probabilities, the same
 //    values the PV product uses.
+//    With MASKED it also applies the key mask of build_block_causal_mask
+//    (image ids) and key validity, per 64-key window and wave: a window whose
+//    keys all lie before the wave's first query, or all share the queries'
+//    image block, runs unmasked; one with no visible key is skipped; the
+//    others test each score. A workgroup stops at the last key any of its
+//    queries may see (key_limit_kernel).
 //  - attn_any_kernel (any lengths): 4 waves x 32 queries, K/V^T staged through
 //    registers with per-element bounds, the reference shape for ragged tails.
 #include "device_common.h"
@@ -73,6 +79,39 @@ __device__ __forceinline__ float dot2_ones(uint32_t pair, float acc) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), one, acc, false);
 }
 
+// Under the block-causal mask query q sees key k when q >= k or both lie in
+// the same image block, so the last key it may see is
+// lim[q] - 1 = max(q, last index of its image id). One workgroup: the last
+// index of every id in LDS (ids outside [0, S) see every key), then lim.
+constexpr int LIMIT_MAX_S = 16384;
+
+__global__ __launch_bounds__(1024) void key_limit_kernel(const int32_t *__restrict__ img, int S,
+                                                         int32_t *__restrict__ lim) {
+    __shared__ int32_t last[LIMIT_MAX_S];
+    for (int i = threadIdx.x; i < S; i += 1024) last[i] = -1;
+    __syncthreads();
+    for (int k = threadIdx.x; k < S; k += 1024) {
+        const int id = img[k];
+        if (id >= 0 && id < S) atomicMax(&last[id], k);
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < S; q += 1024) {
+        const int id = img[q];
+        lim[q] = (id >= S ? S - 1 : id >= 0 ? max(q, last[id]) : q) + 1;
+    }
+}
+
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+    return v;
+}
+
 namespace fast {
 
 constexpr int NW = 8;            // waves per workgroup
@@ -89,10 +128,11 @@ constexpr float RESCALE_TH = 8.0f;    // log2 units
 // K tile: key row r holds 16 B chunk c at slot c ^ (r % 16); V^T tile: d row
 // holds 8-key chunk c at slot c ^ ((d / 2) % 8). A 16-lane phase of b128 reads
 // (16 rows, one chunk) then covers all 64 banks once.
-template <bool PRE>
+template <bool PRE, bool MASKED>
 __global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *__restrict__ q, Seg s0, Seg s1,
                                                                int64_t H, int64_t Sq, int64_t nq, int64_t B,
-                                                               float sl2, uint16_t *__restrict__ out) {
+                                                               float sl2, uint16_t *__restrict__ out, KeyMask km,
+                                                               const int32_t *__restrict__ lim) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
 
@@ -102,7 +142,9 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *_
     const int64_t total = nq * H * B;
     int64_t L = blockIdx.x;
     if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
-    const int64_t qt = L % nq, hh = (L / nq) % H, bb = L / (nq * H);
+    // under a key limit later query tiles see more keys: they start first, so
+    // that the short tiles fill the tail
+    const int64_t qt = (MASKED && lim) ? nq - 1 - L % nq : L % nq, hh = (L / nq) % H, bb = L / (nq * H);
     const int64_t bh = bb * H + hh;
     const int64_t q0 = qt * QB + wave * 32;
 
@@ -121,7 +163,33 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *_
 
     const int len0 = (int)s0.len, len1 = (int)s1.len;
     const int nb0 = (len0 + KB - 1) / KB, nb1 = (len1 + KB - 1) / KB;
-    const int nblk = nb0 + nb1;
+    int nblk = nb0 + nb1;
+
+    // Mask state of the wave: its queries [q_lo, q_hi], the lane's query qi
+    // and image id, the id range of the wave's queries; with a key limit the
+    // workgroup's loop ends at the last key any of its queries may see (the
+    // block-causal form has no prefix, so keys are the queries' sequence).
+    int q_lo = 0, q_hi = 0, qid_min = -1, qid_max = -1;
+    if constexpr (MASKED) {
+        const int qi = (int)min(q0 + l32, Sq - 1);
+        q_lo = (int)min(q0, Sq - 1);
+        q_hi = (int)min(q0 + 31, Sq - 1);
+        if (km.img) {
+            const int idq = km.img[qi];
+            qid_min = __builtin_amdgcn_readfirstlane(wave_min_i(idq));
+            qid_max = __builtin_amdgcn_readfirstlane(wave_max_i(idq));
+        }
+        if (lim) {
+            __shared__ int wlim[NW];
+            const int wl = __builtin_amdgcn_readfirstlane(wave_max_i(lim[qi]));
+            if (lane == 0) wlim[wave] = wl;
+            __syncthreads();
+            int kmax = wlim[0];
+#pragma unroll
+            for (int i = 1; i < NW; i++) kmax = max(kmax, wlim[i]);
+            nblk = min(nblk, (kmax + KB - 1) / KB);
+        }
+    }
     const char *kb0 = (const char *)(s0.k + bh * (int64_t)len0 * HD);
     const char *kb1 = (const char *)(s1.k + bh * (int64_t)len1 * HD);
     const char *vb0 = (const char *)(s0.vt + bh * (int64_t)HD * len0);
@@ -145,11 +213,12 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *_
     // rows and masks keys from `hi` on. Every load stays inside the segment.
     struct Blk {
         const char *kb, *vb;
-        int len, kv0, lo, hi;
+        int len, kv0, lo, hi, kbase;  // kbase: index of the segment's first key in [s0 ; s1]
     };
-    auto blk_of = [&](int j) {
+    auto blk_of = [&](int j) __attribute__((always_inline)) {
         Blk b;
         const bool first = j < nb0;
+        b.kbase = first ? 0 : len0;
         b.len = first ? len0 : len1;
         b.kb = first ? kb0 : kb1;
         b.vb = first ? vb0 : vb1;
@@ -165,7 +234,7 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *_
         }
         return b;
     };
-    auto dma = [&](const Blk &b, int stage) {
+    auto dma = [&](const Blk &b, int stage) __attribute__((always_inline)) {
         uint8_t *base = lds + stage * STAGE;
         if (b.len >= KB) {
             const char *kg = b.kb + (int64_t)b.kv0 * 256;
@@ -221,8 +290,13 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *_
 #pragma unroll
     for (int r = 0; r < 16; r++) negm[r] = 0.f;
     bool first_half = true;
+    bool fresh = true;  // MASKED: this lane's query has seen no visible key yet
 
-    auto half_step = [&](const uint8_t *stg, int h, int lo, int hi) {
+    // kmask: visible keys of the window (bit kv), kid: lane kv holds the image
+    // id of window key kv, kb0: index of the window's first key, partial: test
+    // each score (MASKED only)
+    auto half_step = [&](const uint8_t *stg, int h, int lo, int hi, uint64_t kmask, int kid, int kb0,
+                         bool partial) __attribute__((always_inline)) {
         f32x16 st = negm;
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
@@ -236,6 +310,33 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *_
                 if (kv < lo || kv >= hi) st[r] = -INFINITY;
             }
         }
+        if constexpr (MASKED) {
+            if (partial) {
+                // branch-free per-score test (bitwise, no short circuit): the
+                // key's validity bit and, with image ids, causal or same block.
+                // The lane's query and its image id are fetched here: only
+                // windows tested score by score need them.
+                const uint32_t kmw = h ? (uint32_t)(kmask >> 32) : (uint32_t)kmask;
+                if (km.img) {
+                    const int qi = (int)min(q0 + l32, Sq - 1);
+                    const int idq = km.img[qi];
+                    const int qrel = qi - kb0 - h * 32;  // keys of this half at or before the query
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int kvh = 16 * (r >> 3) + 8 * g + (r & 7);
+                        const int idk = __shfl(kid, h * 32 + kvh);
+                        const int ok = (int)((kmw >> kvh) & 1u) & ((int)(qrel >= kvh) | ((int)(idq >= 0) & (int)(idk == idq)));
+                        st[r] = ok ? st[r] : -INFINITY;
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int kvh = 16 * (r >> 3) + 8 * g + (r & 7);
+                        st[r] = ((kmw >> kvh) & 1u) ? st[r] : -INFINITY;
+                    }
+                }
+            }
+        }
         float m0 = st[0], m1 = st[1];
 #pragma unroll
         for (int r = 2; r < 16; r += 2) {
@@ -244,11 +345,28 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *_
         }
         float mx = xmax32(fmaxf(m0, m1));
         if (!PRE) mx *= sl2;  // log2 units
-        if (first_half || __builtin_amdgcn_ballot_w64(mx > RESCALE_TH)) {
+        bool rescale;
+        if constexpr (MASKED) {
+            // a lane's first visible key sets its reference point; a row with
+            // none yet keeps 0 (its probabilities are exp2(-inf) = 0)
+            const bool has = mx > -INFINITY;
+            rescale = __builtin_amdgcn_ballot_w64(fresh ? has : mx > RESCALE_TH) != 0;
+        } else {
+            rescale = first_half || __builtin_amdgcn_ballot_w64(mx > RESCALE_TH);
+        }
+        if (rescale) {
             // move the reference point up by d (log2 units); the first half of
             // a row has at least one unmasked key, so d is finite there
-            const float d = first_half ? mx : fmaxf(mx, 0.f);
-            const float alpha = first_half ? 0.f : __builtin_amdgcn_exp2f(-d);
+            float d, alpha;
+            if constexpr (MASKED) {
+                const bool has = mx > -INFINITY;
+                d = fresh ? (has ? mx : 0.f) : fmaxf(mx, 0.f);
+                alpha = fresh ? 0.f : __builtin_amdgcn_exp2f(-d);
+                fresh = fresh && !has;
+            } else {
+                d = first_half ? mx : fmaxf(mx, 0.f);
+                alpha = first_half ? 0.f : __builtin_amdgcn_exp2f(-d);
+            }
             first_half = false;
             l_run *= alpha;
 #pragma unroll
@@ -282,18 +400,57 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *_
         }
     };
 
+    // MASKED: lane kv loads the image id of window key kv (0 without ids), or
+    // KEY_OFF for a padded key, one block ahead; waited for with the tiles.
+    constexpr int KEY_OFF = -0x7fffffff - 1;
+    int mk = 0;
+    auto mask_load = [&](const Blk &b) __attribute__((always_inline)) {
+        const int kv = min(lane, b.len - 1 - b.kv0);
+        const int64_t key = (int64_t)b.kbase + b.kv0 + kv;
+        const bool valid = km.kvalid ? km.kvalid[bb * km.kv_len + key] != 0 : true;
+        const int id = km.img ? km.img[key] : 0;
+        mk = valid ? id : KEY_OFF;
+    };
+
     // block j computes from stage cur while block j+1 streams into the other
-    auto step = [&](int j, int cur) {
-        if (j + 1 < nblk) dma(blk_of(j + 1), cur ^ 1);
+    auto step = [&](int j, int cur) __attribute__((always_inline)) {
         const Blk b = blk_of(j);
+        int kid = 0, kb0 = 0;
+        uint64_t kmask = 0;
+        bool skip = false, partial = false;
+        if constexpr (MASKED) {
+            // classify the window for this wave's queries (wave-uniform)
+            kid = mk;
+            kb0 = b.kbase + b.kv0;
+            const bool in = lane >= b.lo && lane < b.hi;
+            const uint64_t inm = __builtin_amdgcn_ballot_w64(in);
+            kmask = __builtin_amdgcn_ballot_w64(in && mk != KEY_OFF);
+            const int k_lo = kb0 + b.lo, k_hi = kb0 + b.hi - 1;
+            bool full = kmask == inm, empty = kmask == 0;
+            if (km.img) {
+                const uint64_t same = __builtin_amdgcn_ballot_w64(in && mk == qid_min);
+                const bool one_block = qid_min == qid_max && qid_min >= 0;
+                full = full && (k_hi <= q_lo || (one_block && same == inm));
+                empty = empty || (k_lo > q_hi && (qid_max < 0 || (qid_min == qid_max && same == 0)));
+            }
+            skip = empty;
+            partial = !full && !empty;
+            if (j + 1 < nblk) mask_load(blk_of(j + 1));
+        }
+        if (j + 1 < nblk) dma(blk_of(j + 1), cur ^ 1);
         const uint8_t *stg = lds + cur * STAGE;
-        half_step(stg, 0, b.lo, b.hi);
-        half_step(stg, 1, b.lo, b.hi);
+        if (!skip) {
+            half_step(stg, 0, b.lo, b.hi, kmask, kid, kb0, partial);
+            half_step(stg, 1, b.lo, b.hi, kmask, kid, kb0, partial);
+        }
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): block j+1 landed
         __syncthreads();
     };
 
-    if (nblk > 0) dma(blk_of(0), 0);
+    if (nblk > 0) {
+        if constexpr (MASKED) mask_load(blk_of(0));
+        dma(blk_of(0), 0);
+    }
     __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
     int j = 0;
@@ -568,8 +725,8 @@ hipError_t launch(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, in
     }
     if ((p & 7) == 0 && (so & 7) == 0) {
         const int64_t nq = (sq + fast::QB - 1) / fast::QB;
-        fast::attn_fast_kernel<PRE><<<dim3((unsigned)(nq * h * b)), dim3(64 * fast::NW), 0, stream>>>(
-            q, s0, s1, h, sq, nq, b, sl2, out);
+        fast::attn_fast_kernel<PRE, false><<<dim3((unsigned)(nq * h * b)), dim3(64 * fast::NW), 0, stream>>>(
+            q, s0, s1, h, sq, nq, b, sl2, out, KeyMask{nullptr, nullptr, p + so}, nullptr);
     } else {
         const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;
         anylen::attn_any_kernel<false><<<dim3((unsigned)(nq * h * b)), dim3(256), 0, stream>>>(
@@ -589,7 +746,7 @@ hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_
 hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
                                    const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
                                    int64_t sq, float sl2, const int32_t *img, const uint8_t *kvalid,
-                                   uint16_t *out, hipStream_t stream) {
+                                   int32_t *lim_scratch, uint16_t *out, hipStream_t stream) {
     if (sq <= 0 || b <= 0 || h <= 0) return hipSuccess;
     if (p < 0 || so < 0 || p + so <= 0) return hipErrorInvalidValue;
     if (img && (p != 0 || so != sq)) return hipErrorInvalidValue;  // block-causal: one shared sequence
@@ -598,9 +755,21 @@ hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const 
         s0 = s1;
         s1 = Seg{ko, vto, 0};
     }
+    const KeyMask km{img, kvalid, p + so};
+    if ((p & 7) == 0 && (so & 7) == 0 && (!img || (lim_scratch && sq <= LIMIT_MAX_S))) {
+        if (img) {
+            key_limit_kernel<<<dim3(1), dim3(1024), 0, stream>>>(img, (int)sq, lim_scratch);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
+        const int64_t nq = (sq + fast::QB - 1) / fast::QB;
+        fast::attn_fast_kernel<false, true><<<dim3((unsigned)(nq * h * b)), dim3(64 * fast::NW), 0, stream>>>(
+            q, s0, s1, h, sq, nq, b, sl2, out, km, img ? lim_scratch : nullptr);
+        return hipGetLastError();
+    }
     const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;
     anylen::attn_any_kernel<true><<<dim3((unsigned)(nq * h * b)), dim3(256), 0, stream>>>(
-        q, s0, s1, h, sq, nq, b, sl2, out, KeyMask{img, kvalid, p + so});
+        q, s0, s1, h, sq, nq, b, sl2, out, km);
     return hipGetLastError();
 }
 

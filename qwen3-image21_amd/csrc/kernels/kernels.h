@@ -127,11 +127,13 @@ hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_
 // Masked attention (build_block_causal_mask semantics): img [sq] image block
 // ids (-1 text) for a prefix-less call where queries and keys are one
 // sequence (so == sq), kvalid [b][p + so] key validity; either may be null.
-// sl2 = softmax scale * log2(e), or 1 when q already carries it.
+// sl2 = softmax scale * log2(e), or 1 when q already carries it. lim_scratch
+// (sq int32, may be null) holds each query's last visible key for the
+// block-causal form; without it that form takes the register-staged kernel.
 hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
                                    const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
                                    int64_t sq, float sl2, const int32_t *img, const uint8_t *kvalid,
-                                   uint16_t *out, hipStream_t stream);
+                                   int32_t *lim_scratch, uint16_t *out, hipStream_t stream);
 // The same with q already multiplied by scale * log2(e) (the QKV epilogue's
 // q_scale), so scores are in log2 units.
 hipError_t launch_attention_log2(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp,

@@ -128,6 +128,104 @@ def test_attention_cached_step_key_valid(torch_cuda, qctx, b, h, p, so, pads):
     assert cos_sim(got, want) >= 0.9999 and max_abs_rel(got, want) <= 2e-2
 
 
+def _masked_case(torch, qctx, ids, kvalid, h, rows=None, seed=0, qmul=1.0):
+    """Prefix-less masked attention of ids.size tokens on the GPU and in the oracle (exact mode),
+    on all rows or on the listed query rows."""
+    b, s = kvalid.shape[0] if kvalid is not None else 1, ids.size
+    rng = np.random.default_rng(seed)
+    q_dev, q = _bhsd(torch, rng, b, h, s, qmul)
+    k_dev, k = _bhsd(torch, rng, b, h, s)
+    _, v = _bhsd(torch, rng, b, h, s)
+    ids_dev = dev(torch, ids.astype(np.int32))
+    kv_dev = dev(torch, kvalid) if kvalid is not None else None
+    vt_dev = _vt(torch, v)
+    out = torch.empty((b, s, h * 128), dtype=torch.bfloat16, device="cuda")
+    qctx.attention_masked(q_dev.data_ptr(), b, h, s, None, 0, k_dev.data_ptr(), vt_dev.data_ptr(), s,
+                          128 ** -0.5, out.data_ptr(), ids_dev.data_ptr(),
+                          kv_dev.data_ptr() if kv_dev is not None else None, stream(torch))
+    got = host(out.float()).reshape(b, s, h, 128).transpose(0, 2, 1, 3)
+    rows = np.arange(s) if rows is None else np.asarray(rows)
+    mask = O.block_causal_mask(ids)[rows][None]
+    if kvalid is not None:
+        mask = mask * kvalid[:, None, :]
+    want = O.attention(np.ascontiguousarray(q[:, :, rows]), k, v, scale=128 ** -0.5, mask=mask, mode=O.EXACT)
+    return got[:, :, rows], want
+
+
+def _ids(*runs):
+    """image ids from (id, count) runs; -1 = text."""
+    return np.concatenate([np.full(n, i, dtype=np.int64) for i, n in runs])
+
+
+@pytest.mark.parametrize("runs,b,pad", [
+    (((-1, 40), (0, 256), (1, 256), (-1, 24), (2, 128)), 2, "last"),   # block edges off the 64-key grid
+    (((-1, 16), (0, 64), (-1, 24), (1, 128)), 2, "first"),               # padding on the first keys
+    (((-1, 24), (0, 40), (-1, 16), (0, 24), (1, 32)), 1, None),          # one id in two runs
+    (((0, 96), (1, 96), (2, 64)), 1, None),                              # no text
+    (((-1, 200),), 2, "first"),                                          # text only: causal
+])
+def test_attention_block_causal_fast_path(torch_cuda, qctx, runs, b, pad):
+    """Every length a multiple of 8: the masked form of the fast kernel, with windows
+    that run unmasked, skipped windows and windows tested score by score; rows whose
+    first keys are padding start their softmax later."""
+    ids = _ids(*runs)
+    kvalid = None
+    if pad:
+        kvalid = np.ones((b, ids.size), dtype=np.uint8)
+        text = np.nonzero(ids < 0)[0]
+        if pad == "last":
+            kvalid[-1, text[-9:]] = 0
+        else:
+            kvalid[-1, text[:5]] = 0
+    got, want = _masked_case(torch_cuda, qctx, ids, kvalid, h=2, seed=ids.size + b)
+    if pad == "first":
+        # queries that see only padded keys have an all -inf row: NaN, as the
+        # reference's softmax gives
+        bad = np.isnan(want)
+        assert np.array_equal(np.isnan(got), bad)
+        got, want = np.where(bad, 0, got), np.where(bad, 0, want)
+    assert cos_sim(got, want) >= 0.9999 and max_abs_rel(got, want) <= 2e-2, (cos_sim(got, want),
+                                                                             max_abs_rel(got, want))
+
+
+def test_attention_block_causal_prefix_8448(torch_cuda, qctx):
+    """The multi-reference prefix: 256 text tokens and two 64 x 64 condition images
+    (8448 tokens), sampled query rows around every block edge."""
+    ids = _ids((-1, 256), (0, 4096), (1, 4096))
+    rows = [0, 1, 63, 64, 200, 255, 256, 257, 1000, 4351, 4352, 4353, 6000, 8446, 8447]
+    got, want = _masked_case(torch_cuda, qctx, ids, None, h=4, rows=rows, seed=8448)
+    assert cos_sim(got, want) >= 0.9999 and max_abs_rel(got, want) <= 2e-2, (cos_sim(got, want),
+                                                                             max_abs_rel(got, want))
+
+
+@pytest.mark.parametrize("b,h,p,so", [(2, 2, 64, 64), (1, 3, 136, 256)])
+def test_attention_cached_step_key_valid_fast_path(torch_cuda, qctx, b, h, p, so):
+    """Cached step with key validity, both segments multiples of 8 (the fast kernel's
+    masked form): padding at the start of the prefix and inside it."""
+    torch = torch_cuda
+    rng = np.random.default_rng(p + so + 1)
+    kvalid = np.ones((b, p + so), dtype=np.uint8)
+    kvalid[0, :70] = 0           # whole first window and part of the second
+    kvalid[-1, 3:11] = 0
+    q_dev, q = _bhsd(torch, rng, b, h, so)
+    ko_dev, ko = _bhsd(torch, rng, b, h, so)
+    _, vo = _bhsd(torch, rng, b, h, so)
+    kp_dev, kp = _bhsd(torch, rng, b, h, p)
+    vp_dev, vp = _bhsd(torch, rng, b, h, p)
+    kv = qctx.kv_create(1, b, h, p)
+    kv.store(0, kp_dev.data_ptr(), vp_dev.data_ptr(), stream(torch))
+    kv_dev = dev(torch, kvalid)
+    vt_dev = _vt(torch, vo)
+    out = torch.empty((b, so, h * 128), dtype=torch.bfloat16, device="cuda")
+    qctx.attention_masked(q_dev.data_ptr(), b, h, so, kv, 0, ko_dev.data_ptr(), vt_dev.data_ptr(), so,
+                          128 ** -0.5, out.data_ptr(), None, kv_dev.data_ptr(), stream(torch))
+    got = host(out.float()).reshape(b, so, h, 128).transpose(0, 2, 1, 3)
+    kv.free()
+    mask = np.broadcast_to(kvalid[:, None, :], (b, so, p + so))
+    want = O.attention(q, ko, vo, kp, vp, mask=mask, mode=O.EXACT)
+    assert cos_sim(got, want) >= 0.9999 and max_abs_rel(got, want) <= 2e-2
+
+
 def test_attention_masked_rejects_bad_calls(torch_cuda, qctx):
     torch = torch_cuda
     b, h, s = 1, 1, 16

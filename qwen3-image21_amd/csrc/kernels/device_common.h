@@ -17,16 +17,16 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // IEEE binary16 -> f32 by bit manipulation (exact for every input, subnormals
 // included), so dequantized values never depend on the FP16 denormal mode.
+// Branch-free (selects, no divergent control flow in the GEMM loops that
+// decode block scales every k step).
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
-    uint32_t sign = (h & 0x8000u) << 16;
-    uint32_t e = (h >> 10) & 0x1fu;
-    uint32_t m = h & 0x3ffu;
-    if (e == 0) {
-        float v = (float)m * 5.9604644775390625e-08f;  // m * 2^-24, exact
-        return __uint_as_float(__float_as_uint(v) | sign);
-    }
-    if (e == 31) return __uint_as_float(sign | 0x7f800000u | (m << 13));
-    return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu;
+    const uint32_t m = h & 0x3ffu;
+    const uint32_t sub = __float_as_uint((float)m * 5.9604644775390625e-08f) | sign;  // m * 2^-24, exact
+    const uint32_t norm = sign | ((e + 112u) << 23) | (m << 13);
+    const uint32_t inf = sign | 0x7f800000u | (m << 13);
+    return __uint_as_float(e == 0 ? sub : (e == 31 ? inf : norm));
 }
 
 // Round-to-nearest-even f32 -> bf16 (lowers to v_cvt_pk_bf16_f32 on gfx950).

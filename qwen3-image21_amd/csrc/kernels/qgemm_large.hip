@@ -57,17 +57,17 @@ __device__ __forceinline__ uint32_t byte_of(const u32x4 &x, int i) {
 
 // Q4_K 6-bit scale/min of sub-block j from the 12 packed bytes at bytes 4..15
 // of the block header word (GGML layout).
+// Branch-free: j comes from the k step at run time, and a branch here would
+// split the step's scheduling region.
 __device__ __forceinline__ void q4k_sc_m(const u32x4 &h, int j, float &sc, float &mn) {
-    uint32_t s, m;
-    if (j < 4) {
-        s = byte_of(h, 4 + j) & 63u;
-        m = byte_of(h, 8 + j) & 63u;
-    } else {
-        s = (byte_of(h, 8 + j) & 0xFu) | ((byte_of(h, j) >> 6) << 4);
-        m = (byte_of(h, 8 + j) >> 4) | ((byte_of(h, 4 + j) >> 6) << 4);
-    }
-    sc = (float)s;
-    mn = (float)m;
+    // the 12 packed bytes sit at header bytes 4..15: scales[i] = byte 4 + i
+    const int jl = j & 3;
+    const uint32_t b4 = byte_of(h, 4 + jl), b8 = byte_of(h, 8 + jl), b12 = byte_of(h, 12 + jl);
+    const uint32_t s_lo = b4 & 63u, m_lo = b8 & 63u;                         // sub-blocks 0-3
+    const uint32_t s_hi = (b12 & 0xFu) | ((b4 >> 6) << 4);                   // sub-blocks 4-7
+    const uint32_t m_hi = (b12 >> 4) | ((b8 >> 6) << 4);
+    sc = (float)(j < 4 ? s_lo : s_hi);
+    mn = (float)(j < 4 ? m_lo : m_hi);
 }
 
 // 8 unsigned byte codes (two words) -> 8 bf16 of code*ds + off (exact f32 value,

@@ -568,29 +568,42 @@ __device__ __forceinline__ float get_coherent(const float *p) {
     return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// Sums over the C chunks of the four partial elements (row r, tokens
-// 16 tt + 4 kg + e) of a lane in group g, in chunk order. Loads go out eight
-// chunks at a time so a batch costs one memory round trip. IS = floats per item.
-__device__ __forceinline__ f32x4 psum4(const float *part, int C, int G, int IS, int64_t g, int tt, int kg, int r) {
-    constexpr int B = 8;
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    const float *base = part + g * IS + (16 * tt + 4 * kg) * 16 + r;
-    for (int c0 = 0; c0 < C; c0 += B) {
-        float v[B][4];
+// Sums over the C chunks of NS slices at once: slice s is the four partial
+// elements (row r, tokens 16 tts[s] + 4 kg + e) of a lane in group gs[s],
+// summed in chunk order. Every slice's loads of a batch of CB chunks go out
+// together (VB values in flight per lane), so the whole unit costs
+// ceil(C / CB) memory round trips instead of one or more per slice.
+// IS = floats per item.
+template <int NS, int VB>
+__device__ __forceinline__ void psum_slices(const float *part, int C, int G, int IS, const int64_t (&gs)[NS],
+                                            const int (&tts)[NS], int kg, int r, f32x4 (&out)[NS]) {
+    constexpr int CB = VB / (4 * NS) > 0 ? VB / (4 * NS) : 1;
+    const float *base[NS];
 #pragma unroll
-        for (int cc = 0; cc < B; cc++) {
-            const float *pc = base + (int64_t)min(c0 + cc, C - 1) * G * IS;
+    for (int s = 0; s < NS; s++) {
+        base[s] = part + gs[s] * IS + (16 * tts[s] + 4 * kg) * 16 + r;
+        out[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int c0 = 0; c0 < C; c0 += CB) {
+        float v[NS][CB][4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) v[cc][e] = get_coherent(pc + e * 16);
+        for (int cc = 0; cc < CB; cc++) {
+            if (c0 + cc >= C) break;  // wave-uniform: no loads past the last chunk
+            const int64_t off = (int64_t)(c0 + cc) * G * IS;
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[s][cc][e] = get_coherent(base[s] + off + e * 16);
         }
 #pragma unroll
-        for (int cc = 0; cc < B; cc++)
+        for (int cc = 0; cc < CB; cc++)
             if (c0 + cc < C) {
 #pragma unroll
-                for (int e = 0; e < 4; e++) s[e] += v[cc][e];
+                for (int s = 0; s < NS; s++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) out[s][e] += v[s][cc][e];
             }
     }
-    return s;
 }
 
 template <int EPI, int MT>
@@ -599,15 +612,16 @@ __device__ void unit_epilogue(const float *part, const Plan &p, int64_t unit, in
     constexpr int TOK = 16 * MT, IS = 16 * TOK;
     const int l16 = lane & 15, kg = lane >> 4;
     if constexpr (EPI == EPI_QKV) {
-        // head unit: lane j holds columns (2j, 2j+1) of the head; eight tokens
-        // per batch of loads (chunk sums in chunk order)
+        // head unit: lane j holds columns (2j, 2j+1) of the head; TB tokens x
+        // CB chunks per batch of loads (chunk sums in chunk order; 64 values
+        // per lane where registers are scarce, 128 otherwise)
         const int64_t g = unit * 8 + (lane >> 3);
         const int r = 2 * (lane & 7);
         const int64_t nb = unit * 128 + ep.n_offset;
         const int sec = (int)(nb / ep.hidden);
         const int64_t head = (nb % ep.hidden) / 128;
         const int64_t S = ep.seq, H = ep.heads;
-        constexpr int TB = 8, CB = 4;
+        constexpr int TB = MT == 1 ? 8 : 16, CB = 4;
         for (int m0 = 0; m0 < M; m0 += TB) {
             float sx[TB][2];
 #pragma unroll
@@ -662,32 +676,47 @@ __device__ void unit_epilogue(const float *part, const Plan &p, int64_t unit, in
         }
     } else if constexpr (EPI == EPI_SWIGLU) {
         // hidden columns 64 blk + 16 q + l16: gate group 8 blk + q, up group 8 blk + 4 + q
+        // (every token tile's partials were stored, so all MT tiles load)
         const int64_t blk = unit >> 2, q = unit & 3;
         const int64_t gg = 8 * blk + q, gu = gg + 4;
+        int64_t gs[2 * MT];
+        int tts[2 * MT];
 #pragma unroll
         for (int tt = 0; tt < MT; tt++) {
-            if (16 * tt >= M) break;
-            const f32x4 gt = psum4(part, p.C, p.G, IS, gg, tt, kg, l16);
-            const f32x4 up = psum4(part, p.C, p.G, IS, gu, tt, kg, l16);
+            gs[2 * tt] = gg;
+            gs[2 * tt + 1] = gu;
+            tts[2 * tt] = tts[2 * tt + 1] = tt;
+        }
+        f32x4 sum[2 * MT];
+        psum_slices<2 * MT, MT == 1 ? 64 : 128>(part, p.C, p.G, IS, gs, tts, kg, l16, sum);
+#pragma unroll
+        for (int tt = 0; tt < MT; tt++) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int m = 16 * tt + 4 * kg + e;
                 if (m < M)
                     ep.hmid[m * ep.ldh + 64 * blk + 16 * q + l16] =
-                        (uint16_t)(pack_bf16x2(silu(gt[e]) * up[e], 0.f) & 0xffffu);
+                        (uint16_t)(pack_bf16x2(silu(sum[2 * tt][e]) * sum[2 * tt + 1][e], 0.f) & 0xffffu);
             }
         }
     } else {
         const int64_t n = unit * 16 + l16;
+        int64_t gs[MT];
+        int tts[MT];
 #pragma unroll
         for (int tt = 0; tt < MT; tt++) {
-            if (16 * tt >= M) break;
-            const f32x4 sum = psum4(part, p.C, p.G, IS, unit, tt, kg, l16);
+            gs[tt] = unit;
+            tts[tt] = tt;
+        }
+        f32x4 sum[MT];
+        psum_slices<MT, MT == 1 ? 64 : 128>(part, p.C, p.G, IS, gs, tts, kg, l16, sum);
+#pragma unroll
+        for (int tt = 0; tt < MT; tt++) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int m = 16 * tt + 4 * kg + e;
                 if (m < M) {
-                    const float v = sum[e];
+                    const float v = sum[tt][e];
                     if constexpr (EPI == EPI_F32) {
                         ((float *)ep.out)[m * ep.ldo + n] = v;
                     } else if constexpr (EPI == EPI_BF16) {

@@ -317,8 +317,9 @@ __device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcp
 // window of the weight matrix (the pattern of a plain streaming read). Raw
 // tiles go straight to registers, four in flight per wave, one item ahead.
 //
-// Q4_K uses the exact code products described above (the sub-block sums X_j
-// of the chunk are computed once per wave and token tile). Q6_K dequantizes
+// Q4_K uses the exact code products described above up to 16 tokens (the
+// sub-block sums X_j of the chunk are computed once per wave and token tile)
+// and beyond that decodes each value once for all token tiles. Q6_K dequantizes
 // each lane's 8 values of a step with v_fma_mix (the 6-bit codes as f16
 // subnormals, scales carrying 2^24; RNE to bf16) once for all token tiles; a
 // lane's 8 values of a step are 8 consecutive k of one 16-value sub-block and
@@ -559,6 +560,49 @@ __device__ __forceinline__ void tile_q4(TileQ4 r, const uint8_t *xrow, int kg, c
     }
 }
 
+// One Q4_K tile by dequantization into acc[0..MT): the 8 B fragments of a
+// lane (sub-block j = 2 cc + nib, its 8 values k = 32 j + 8 kg + i) are
+// decoded once with v_fma_mix and serve every token tile. A nibble masked into
+// an f16 half is the subnormal q 2^-24 (low, bits 0-3) or q 2^-20 (high, bits
+// 4-7), so with the scale carrying 2^24 or 2^20 one fma gives d sc q - dmin m
+// with a single rounding, then RNE to bf16 (the value every other Q4_K path
+// here feeds the MFMA). Cheaper than the code products once the fragment
+// serves two or more token tiles.
+template <int MT>
+__device__ __forceinline__ void tile_q4d(TileQ4 r, const uint8_t *xrow, int kg, f32x4 *acc) {
+    pin(r);
+    const uint32_t hx = r.h[0], hy = r.h[1], hz = r.h[2], hw = r.h[3];
+    const float d = m16::cvt_f16_lo(hx), dmin = m16::cvt_f16_hi(hx);
+    const uint32_t sc_lo = hy & 0x3F3F3F3Fu, m_lo = hz & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (hw & 0x0F0F0F0Fu) | ((hy >> 2) & 0x30303030u);
+    const uint32_t m_hi = ((hw >> 4) & 0x0F0F0F0Fu) | ((hz >> 2) & 0x30303030u);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int cc = j >> 1, nib = j & 1;
+        const uint32_t scw = j < 4 ? sc_lo : sc_hi, mw = j < 4 ? m_lo : m_hi;
+        const float a = d * (float)((scw >> (8 * (j & 3))) & 0xffu) * (nib ? 0x1p20f : 0x1p24f);
+        const float b = -(dmin * (float)((mw >> (8 * (j & 3))) & 0xffu));
+        const uint32_t msk = nib ? 0x00F000F0u : 0x000F000Fu;
+        const uint32_t y0 = r.q[cc][0], y1 = r.q[cc][1];
+        const uint32_t p0 = y0 & msk, p1 = (y0 >> 8) & msk, p2 = y1 & msk, p3 = (y1 >> 8) & msk;
+        const u32x4 bw = {pack_bf16x2(mix_lo(p0, a, b), mix_lo(p1, a, b)), pack_bf16x2(mix_hi(p0, a, b), mix_hi(p1, a, b)),
+                          pack_bf16x2(mix_lo(p2, a, b), mix_lo(p3, a, b)), pack_bf16x2(mix_hi(p2, a, b), mix_hi(p3, a, b))};
+#pragma unroll
+        for (int tt = 0; tt < MT; tt++) {
+            const bf16x8 av = *(const bf16x8 *)(xrow + tt * 16 * XROW + 64 * j + 16 * kg);
+            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bw), acc[tt], 0, 0, 0);
+        }
+    }
+}
+
+// Q4_K tiles by code products up to this many token tiles, by dequantization
+// beyond (the code products' per-tile-and-token-tile scaling outgrows one
+// decode per value).
+#ifndef QIMM_Q4_CP_MAX_MT
+#define QIMM_Q4_CP_MAX_MT 1
+#endif
+constexpr bool q4_code_products(int mt) { return mt <= QIMM_Q4_CP_MAX_MT; }
+
 // Partial sums cross workgroups on different XCDs: stored and loaded with
 // system scope (sc0 sc1: written through to, and read from, memory).
 __device__ __forceinline__ void put_coherent(float *p, float v) {
@@ -769,8 +813,9 @@ __global__ __launch_bounds__(64 * nwaves(MT), wg_per_cu(MT) * nwaves(MT) / 4) vo
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(SBC * TL) : "memory");
 
     const uint8_t *xrow = xs + l16 * XROW;
+    constexpr bool CP = FMT == WF_Q4_K && q4_code_products(MT);
     float xq0[SBC][MT], xq1[SBC][MT];
-    if constexpr (FMT == WF_Q4_K) {
+    if constexpr (CP) {
         // X_kg and X_{4+kg} of token 16 tt + l16 for the chunk's four
         // super-blocks, in the A layout of the f32 MFMA (bf16 MFMA against
         // row-selector ones)
@@ -808,7 +853,8 @@ __global__ __launch_bounds__(64 * nwaves(MT), wg_per_cu(MT) * nwaves(MT) / 4) vo
         for (int tt = 0; tt < MT; tt++) acc[tt] = accM[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < SBC; t++) {
-            if constexpr (FMT == WF_Q4_K) tile_q4<MT>(ring[t], xrow + 512 * t, kg, xq0[t], xq1[t], acc, accM);
+            if constexpr (CP) tile_q4<MT>(ring[t], xrow + 512 * t, kg, xq0[t], xq1[t], acc, accM);
+            else if constexpr (FMT == WF_Q4_K) tile_q4d<MT>(ring[t], xrow + 512 * t, kg, acc);
             else if constexpr (FMT == WF_Q6_K) tile_q6<MT>(ring[t], xrow + 512 * t, kg, acc);
             else tile_q8<MT>(ring[t], xrow + 512 * t, kg, acc);
             // finish this tile's arithmetic here: left alone, the compiler sinks
@@ -824,7 +870,7 @@ __global__ __launch_bounds__(64 * nwaves(MT), wg_per_cu(MT) * nwaves(MT) / 4) vo
         float *dst = part + ((int64_t)c * p.G + g) * IS;
 #pragma unroll
         for (int tt = 0; tt < MT; tt++) {
-            if constexpr (FMT == WF_Q4_K) acc[tt] -= accM[tt];
+            if constexpr (CP) acc[tt] -= accM[tt];
 #pragma unroll
             for (int e = 0; e < 4; e++) put_coherent(dst + (16 * tt + 4 * kg + e) * 16 + l16, acc[tt][e]);
         }

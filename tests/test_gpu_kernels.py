@@ -79,13 +79,13 @@ def _gemm_case(torch, qctx, t, m, n, k, seed, out_type=synth.F32, std=0.02):
 def test_qmatmul_matches_bf16_weight_products(torch_cuda, qctx, t, m, n, k):
     """Products of the bf16 activations and the weights each path multiplies:
     bf16-rounded dequantized weights on the MFMA dequant paths, the exact Q4_K
-    weights on the code-product path (Q4_K, M <= 64, K % 1024 == 0)."""
+    weights on the code-product path (Q4_K, M <= 16, K % 1024 == 0)."""
     got, a, w = _gemm_case(torch_cuda, qctx, t, m, n, k, seed=m * 7 + n + k + t)
     Wd = O.dequantize(t, w, n * k).reshape(n, k)
     Wb = O.bf16_round(Wd).astype(np.float64)
     want = a.astype(np.float64) @ Wb.T
     scale = np.abs(a).astype(np.float64) @ np.abs(Wb).T
-    if t == synth.Q4_K and m <= 64 and k % 1024 == 0:
+    if t == synth.Q4_K and m <= 16 and k % 1024 == 0:
         want = a.astype(np.float64) @ Wd.astype(np.float64).T
     assert np.all(np.abs(got - want) <= 2e-4 * scale + 1e-6)
     # against the oracle: exact weights (exact mode) and candle's int8 activations
@@ -105,12 +105,18 @@ def test_qmatmul_matches_bf16_weight_products(torch_cuda, qctx, t, m, n, k):
                                    (33, 4096, 4096),    # three 16-token tiles of 64 (one padded)
                                    (24, 2048, 2048),    # two 16-token tiles
                                    (64, 6144, 4096)])   # four full token tiles
-def test_qmatmul_q4k_short_m_exact_weights(torch_cuda, qctx, m, n, k):
-    """Q4_K at M <= 64 and K % 1024 == 0 multiplies the raw codes and applies the
-    scales afterwards: the product of the bf16 activations and the exact
-    (not bf16-rounded) Q4_K weights, up to f32 summation order."""
+def test_qmatmul_q4k_short_m_one_launch(torch_cuda, qctx, m, n, k):
+    """Q4_K at M <= 64 and K % 1024 == 0 takes the one-launch kernel. Up to 16
+    tokens it multiplies the raw codes and applies the scales afterwards: the
+    product of the bf16 activations and the exact (not bf16-rounded) Q4_K
+    weights, up to f32 summation order. From 17 tokens each weight is decoded
+    once to bf16 for every token tile: the product with the bf16-rounded
+    weights."""
     got, a, w = _gemm_case(torch_cuda, qctx, synth.Q4_K, m, n, k, seed=m + n + k)
-    Wd = O.dequantize(synth.Q4_K, w, n * k).reshape(n, k).astype(np.float64)
+    Wd = O.dequantize(synth.Q4_K, w, n * k).reshape(n, k)
+    if m > 16:
+        Wd = O.bf16_round(Wd)
+    Wd = Wd.astype(np.float64)
     want = a.astype(np.float64) @ Wd.T
     scale = np.abs(a).astype(np.float64) @ np.abs(Wd).T
     assert np.all(np.abs(got - want) <= 2e-5 * scale + 1e-6), np.max(np.abs(got - want) / (scale + 1e-9))
@@ -125,8 +131,8 @@ def test_qmatmul_short_m_one_launch_repeats(torch_cuda, qctx):
     the same launch, counting arrivals per output unit in counters that every
     call leaves at zero: calls in a row over different shapes, token counts and
     weights give bit-identical results to a first call, and match the
-    products of the bf16 activations and the (bf16-rounded for Q6_K and Q8_0,
-    exact for Q4_K) weights."""
+    products of the bf16 activations and the (bf16-rounded for Q6_K, Q8_0 and
+    Q4_K beyond 16 tokens, exact for Q4_K up to 16) weights."""
     torch = torch_cuda
     cases = [(synth.Q6_K, 16, 4096, 3072), (synth.Q4_K, 16, 2048, 4096), (synth.Q6_K, 5, 1024, 12288),
              (synth.Q4_K, 1, 3072, 2048), (synth.Q6_K, 64, 4096, 3072), (synth.Q4_K, 40, 2048, 4096),
@@ -148,7 +154,7 @@ def test_qmatmul_short_m_one_launch_repeats(torch_cuda, qctx):
             continue
         first[key] = got
         Wd = O.dequantize(t, w, n * k).reshape(n, k)
-        if t != synth.Q4_K:
+        if t != synth.Q4_K or m > 16:
             Wd = O.bf16_round(Wd)
         want = a.astype(np.float64) @ Wd.astype(np.float64).T
         scale = np.abs(a).astype(np.float64) @ np.abs(Wd).astype(np.float64).T

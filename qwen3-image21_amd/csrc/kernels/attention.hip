@@ -53,8 +53,6 @@ struct KeyMask {
     int64_t kv_len;
 };
 
-typedef __attribute__((address_space(3))) void *lds_ptr_t;
-
 // v_permlane32_swap exchanges the upper 32 lanes of its first operand with
 // the lower 32 lanes of its second; with both operands holding x, each lane
 // ends up with x and x of lane ^ 32 in the pair. Inline asm because the
@@ -443,7 +441,7 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *_
             half_step(stg, 0, b.lo, b.hi, kmask, kid, kb0, partial);
             half_step(stg, 1, b.lo, b.hi, kmask, kid, kb0, partial);
         }
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): block j+1 landed
+        __builtin_amdgcn_s_waitcnt(WAIT_VM0);  // vmcnt(0): block j+1 landed
         __syncthreads();
     };
 
@@ -451,7 +449,7 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *_
         if constexpr (MASKED) mask_load(blk_of(0));
         dma(blk_of(0), 0);
     }
-    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __builtin_amdgcn_s_waitcnt(WAIT_VM0);
     __syncthreads();
     int j = 0;
     for (; j + 1 < nblk; j += 2) {

@@ -29,6 +29,15 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return __uint_as_float(e == 0 ? sub : (e == 31 ? inf : norm));
 }
 
+// The same by the hardware convert (v_cvt_f32_f16): exact for every finite
+// input, subnormals included, because HIP kernels run with f16 denormals
+// preserved (FLOAT_DENORM_MODE_16_64 = 3 in every kernel descriptor here). A
+// single instruction, so the GEMM loops that decode block scales every k step
+// keep one basic block.
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xffffu));
+}
+
 // Round-to-nearest-even f32 -> bf16 (lowers to v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     bf16x2 r;
@@ -48,6 +57,39 @@ __device__ __forceinline__ const uint8_t *q4k_block(const uint8_t *q, int64_t n,
 __device__ __forceinline__ const uint8_t *q6k_block(const uint8_t *q, int64_t n, int64_t sb, int64_t sbs) {
     return q + (((n >> 4) * sbs + sb) * 16 + (n & 15)) * 224;
 }
+
+// f32 fma with src0 read as f16 from the low / high half of x: a code q held
+// as the f16 subnormal q * 2^-24 (exact) times a scale pre-multiplied by 2^24
+// gives q*scale + off with a single rounding, no separate integer convert.
+__device__ __forceinline__ float mix_lo(uint32_t x, float s, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(s), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float mix_hi(uint32_t x, float s, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(s), "v"(c));
+    return r;
+}
+
+// MFMA operand tiles in LDS: dense 128 B rows (64 bf16 of a k step), 16 B
+// chunk c of row r at slot c ^ key(r), key = (r & 7) ^ ((r >> 3) & 1).
+// Measured on gfx950: 16 B reads are served 16 lanes (256 B) per cycle and are
+// conflict free when the 16 rows of a group cover all 16 slots of a 256 B
+// window (same-parity rows need distinct keys); 16 B writes are served 8 lanes
+// (128 B) per cycle and need distinct keys on each aligned group of 8 rows.
+// This key satisfies both.
+__device__ __forceinline__ int swz_key(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ swz_key(r)) << 4); }
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+// s_waitcnt immediates for __builtin_amdgcn_s_waitcnt (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt in 6:4, lgkmcnt in 11:8; an all-ones field does
+// not wait on that counter).
+constexpr unsigned WAIT_VM0 = 0x0f70;        // vmcnt(0)
+constexpr unsigned WAIT_LGKM0 = 0xc07f;      // lgkmcnt(0)
+constexpr unsigned WAIT_VM0_LGKM0 = 0x0070;  // vmcnt(0) lgkmcnt(0)
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
     return __uint_as_float(b << 16);

@@ -1,16 +1,24 @@
-// Dequant-GEMM for gfx950: C[M,N] = A[M,K] (bf16) x W[N,K]^T (GGUF blocks).
+// Dequant-GEMM for gfx950: C[M,N] = A[M,K] (bf16) x W[N,K]^T (GGUF blocks),
+// the tile for 64 < M < 512 token rows (and the split-K shares of short
+// products).
 //
 // Replaces candle's QMatMul::forward as called through Linear::forward
 // (src/quantized_transformer.rs:19-33; call sites 133-135, 151, 194-199, 202).
 //
 // Tile 128x128x64, 256 threads = 4 waves in a 2x2 grid, each wave 64x64 as
-// 2x2 v_mfma_f32_32x32x16_bf16 tiles. A is staged to LDS as bf16; W is read
-// as raw quantized bytes with 128-bit loads, dequantized in registers
-// (exact f32 value d*sc*q - dmin*m, then round-to-nearest-even to bf16) and
-// staged to LDS next to A. Two LDS stages: the global loads for step k+1 are
-// in flight while the MFMAs of step k run. The epilogue goes through LDS as
-// an f32 tile so each variant (plain store, fused QKV RmsNorm+RoPE, gated
-// residual, SwiGLU) writes whole rows with 128-bit stores.
+// 2x2 v_mfma_f32_32x32x16_bf16 tiles, two workgroups per CU. Operand tiles
+// live in LDS as dense 128 B rows with XOR-swizzled 16 B chunks (swz in
+// device_common.h: conflict-free staging writes and fragment reads), two
+// stages per operand. Both operands are loaded into register rings three k
+// steps ahead (activation rows as bf16, weight half-rows as raw GGUF bytes);
+// while the MFMAs of step k run, step k+1 goes from the ring to the other LDS
+// stage, the weights dequantized on the way (v_fma_mix: exact f32
+// d*sc*q - dmin*m, then round-to-nearest-even to bf16). One barrier per step.
+// Every load goes to registers (no direct-to-LDS loads), so the compiler
+// waits for each ring slot by an exact count and the loads of the next three
+// steps stay in flight. The epilogue goes through LDS as an f32 tile so each
+// variant (plain store, fused QKV RmsNorm+RoPE, gated residual, SwiGLU)
+// writes whole rows with 128-bit stores.
 #include "device_common.h"
 #include "kernels.h"
 
@@ -18,51 +26,32 @@ namespace qimm {
 namespace {
 
 constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int LP = 72;                 // bf16 pitch of an A/B stage row (64 + 8 pad)
-constexpr int CP = 132;                // f32 pitch of the epilogue tile row
-constexpr int STAGE = 2 * 128 * LP;    // bf16 elements per stage (A rows, then B rows)
-constexpr int LDS_ELEMS = 2 * STAGE;   // 73728 B
+constexpr int TILEB = 128 * 128;        // bytes of one 128-row operand tile
+constexpr int STAGE = 2 * TILEB;        // A tile then W tile
+constexpr int RING = 2;                 // k steps in flight in registers
+constexpr int CP = 132;                 // f32 pitch of the epilogue tile row
+constexpr int LDS_BYTES = BM * CP * 4;  // 67.6 KB (the two 64 KB operand stages fit): two workgroups per CU
+static_assert(2 * STAGE <= LDS_BYTES, "operand stages fit the epilogue tile");
+static_assert(RING == 2, "the step loop is unrolled by the ring size");
 
+// Raw bytes of one half row (32 values) of a k step.
 struct WRaw {
     u32x4 v[4];
     uint32_t s;
 };
 
+// A word whose value the optimizer must not look through.
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 __device__ __forceinline__ uint32_t byte_of(const u32x4 &x, int i) {
     return (x[i >> 2] >> (8 * (i & 3))) & 0xffu;
 }
 
-// Q4_K 6-bit scale and min of sub-block j from the 12 packed bytes, which
-// sit at bytes 4..15 of the block header word h (GGML layout).
-__device__ __forceinline__ void q4k_sc_m(const u32x4 &h, int j, float &sc, float &mn) {
-    uint32_t s, m;
-    if (j < 4) {
-        s = byte_of(h, 4 + j) & 63u;
-        m = byte_of(h, 8 + j) & 63u;
-    } else {
-        s = (byte_of(h, 8 + j) & 0xFu) | ((byte_of(h, j) >> 6) << 4);
-        m = (byte_of(h, 8 + j) >> 4) | ((byte_of(h, 4 + j) >> 6) << 4);
-    }
-    sc = (float)s;
-    mn = (float)m;
-}
-
-// 4 unsigned bytes of x -> 4 floats v*ds + off, packed to 2 bf16x2 words.
-__device__ __forceinline__ u32x2 cvt4(uint32_t x, float ds, float off) {
-    float f0 = (float)(x & 0xffu), f1 = (float)((x >> 8) & 0xffu);
-    float f2 = (float)((x >> 16) & 0xffu), f3 = (float)(x >> 24);
-    return u32x2{pack_bf16x2(__builtin_fmaf(f0, ds, off), __builtin_fmaf(f1, ds, off)),
-                 pack_bf16x2(__builtin_fmaf(f2, ds, off), __builtin_fmaf(f3, ds, off))};
-}
-
-// 16 codes held as bytes of a u32x4 -> 16 bf16 (two u32x4).
-__device__ __forceinline__ void cvt16(const u32x4 &x, float ds, float off, u32x4 &o0, u32x4 &o1) {
-    const u32x2 a = cvt4(x[0], ds, off), b = cvt4(x[1], ds, off);
-    const u32x2 c = cvt4(x[2], ds, off), d = cvt4(x[3], ds, off);
-    o0 = u32x4{a[0], a[1], b[0], b[1]};
-    o1 = u32x4{c[0], c[1], d[0], d[1]};
-}
-
+// Half h of row n for the k step at k0: Q8_0 / BF16 values [32h, 32h+32) of
+// the step; Q4_K / Q6_K values [16h, 16h+16) and [32+16h, 32+16h+16).
 template <int FMT>
 __device__ __forceinline__ void load_w(const GemmWeight &w, int64_t n, int64_t k0, int h, WRaw &r) {
     const int64_t K = w.k;
@@ -86,70 +75,108 @@ __device__ __forceinline__ void load_w(const GemmWeight &w, int64_t n, int64_t k
         r.s = *(const uint16_t *)(blk + 208);
     } else {
         const uint8_t *p = w.q + (n * K + k0 + 32 * h) * 2;
-        r.v[0] = *(const u32x4 *)p;
-        r.v[1] = *(const u32x4 *)(p + 16);
-        r.v[2] = *(const u32x4 *)(p + 32);
-        r.v[3] = *(const u32x4 *)(p + 48);
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.v[i] = *(const u32x4 *)(p + 16 * i);
     }
 }
 
-// Dequantize one thread's 32 values of row n_local and store them as bf16 in
-// the B stage: Q8_0/BF16 cover k in [32h, 32h+32); Q4_K/Q6_K cover
-// [16h, 16h+16) and [32+16h, 32+16h+16).
+// Global loads load_w issues per thread (the pipeline's wait counts).
 template <int FMT>
-__device__ __forceinline__ void store_w(uint16_t *bs, int nl, int h, int64_t k0, const WRaw &r) {
-    uint16_t *row = bs + nl * LP;
+constexpr int w_loads() { return FMT == WF_Q8_0 ? 3 : FMT == WF_Q4_K ? 2 : FMT == WF_Q6_K ? 5 : 4; }
+
+// Step dequant constants of a half row.
+struct WScale {
+    float a0, b0, a1, b1;
+};
+
+template <int FMT>
+__device__ __forceinline__ WScale w_scales(const WRaw &r, int64_t k0, int h) {
+    WScale s{};
     if constexpr (FMT == WF_Q8_0) {
-        const float d = f16_bits_to_f32(r.s);
-        const float off = -128.f * d;  // codes biased to unsigned: (q+128)*d - 128*d, exact
-        u32x4 a = r.v[0] ^ 0x80808080u, b = r.v[1] ^ 0x80808080u;
-        u32x4 o0, o1, o2, o3;
-        cvt16(a, d, off, o0, o1);
-        cvt16(b, d, off, o2, o3);
-        *(u32x4 *)(row + 32 * h) = o0;
-        *(u32x4 *)(row + 32 * h + 8) = o1;
-        *(u32x4 *)(row + 32 * h + 16) = o2;
-        *(u32x4 *)(row + 32 * h + 24) = o3;
+        const float d = f16_to_f32(r.s & 0xffffu);
+        s.a0 = d * 0x1p24f;  // codes biased to unsigned: (q+128)*d - 128*d, exact
+        s.b0 = -128.f * d;
     } else if constexpr (FMT == WF_Q4_K) {
         const int c = (int)((k0 & 255) >> 6);
-        const float d = f16_bits_to_f32(r.v[0][0] & 0xffffu);
-        const float dmin = f16_bits_to_f32(r.v[0][0] >> 16);
-        float sc0, m0, sc1, m1;
-        q4k_sc_m(r.v[0], 2 * c, sc0, m0);
-        q4k_sc_m(r.v[0], 2 * c + 1, sc1, m1);
-        const float ds0 = d * sc0, dm0 = dmin * m0, ds1 = d * sc1, dm1 = dmin * m1;
-        u32x4 lo = r.v[1] & 0x0F0F0F0Fu, hi = (r.v[1] >> 4) & 0x0F0F0F0Fu;
-        u32x4 o0, o1, o2, o3;
-        cvt16(lo, ds0, -dm0, o0, o1);
-        cvt16(hi, ds1, -dm1, o2, o3);
-        *(u32x4 *)(row + 16 * h) = o0;
-        *(u32x4 *)(row + 16 * h + 8) = o1;
-        *(u32x4 *)(row + 32 + 16 * h) = o2;
-        *(u32x4 *)(row + 32 + 16 * h + 8) = o3;
+        const float d = f16_to_f32(r.v[0][0] & 0xffffu), dmin = f16_to_f32(r.v[0][0] >> 16);
+        // the 12 packed scale/min bytes sit at header bytes 4..15 (GGML layout);
+        // sub-blocks 2c (low nibbles) and 2c+1 (high nibbles). Both packings
+        // are decoded and one is kept by a mask: c is uniform but known only at
+        // run time, and a select on it compiles to a branch that would split the
+        // step into separately scheduled blocks.
+        const uint32_t hi = opaque(0u - (uint32_t)(c >> 1));  // all ones for sub-blocks 4-7
+        float sc[2], mn[2];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int jl = (2 * c + e) & 3;
+            const uint32_t b4 = byte_of(r.v[0], 4 + jl), b8 = byte_of(r.v[0], 8 + jl), b12 = byte_of(r.v[0], 12 + jl);
+            const uint32_t s_lo = b4 & 63u, m_lo = b8 & 63u;
+            const uint32_t s_hi = (b12 & 0xFu) | ((b4 >> 6) << 4), m_hi = (b12 >> 4) | ((b8 >> 6) << 4);
+            sc[e] = (float)((s_lo & ~hi) | (s_hi & hi));
+            mn[e] = (float)((m_lo & ~hi) | (m_hi & hi));
+        }
+        s.a0 = d * sc[0] * 0x1p24f;  // low nibbles at f16 bits 0-3
+        s.b0 = -(dmin * mn[0]);
+        s.a1 = d * sc[1] * 0x1p20f;  // high nibbles at f16 bits 4-7
+        s.b1 = -(dmin * mn[1]);
     } else if constexpr (FMT == WF_Q6_K) {
         const int hh = (int)((k0 & 255) >> 7), o = (int)((k0 & 127) >> 6);
-        const float d = f16_bits_to_f32(r.s);
-        const int ra = 2 * o, rb = 2 * o + 1;
-        const float sa = (float)(int8_t)byte_of(r.v[3], 8 * hh + 4 * o + h);
-        const float sb = (float)(int8_t)byte_of(r.v[3], 8 * hh + 4 * o + 2 + h);
-        const float dsa = d * sa, dsb = d * sb;
-        u32x4 la = o ? ((r.v[0] >> 4) & 0x0F0F0F0Fu) : (r.v[0] & 0x0F0F0F0Fu);
-        u32x4 lb = o ? ((r.v[1] >> 4) & 0x0F0F0F0Fu) : (r.v[1] & 0x0F0F0F0Fu);
-        u32x4 qa = la | (((r.v[2] >> (2 * ra)) & 0x03030303u) << 4);
-        u32x4 qb = lb | (((r.v[2] >> (2 * rb)) & 0x03030303u) << 4);
-        u32x4 o0, o1, o2, o3;
-        cvt16(qa, dsa, -32.f * dsa, o0, o1);  // (q+32)*ds - 32*ds, exact
-        cvt16(qb, dsb, -32.f * dsb, o2, o3);
-        *(u32x4 *)(row + 16 * h) = o0;
-        *(u32x4 *)(row + 16 * h + 8) = o1;
-        *(u32x4 *)(row + 32 + 16 * h) = o2;
-        *(u32x4 *)(row + 32 + 16 * h + 8) = o3;
-    } else {
-        *(u32x4 *)(row + 32 * h) = r.v[0];
-        *(u32x4 *)(row + 32 * h + 8) = r.v[1];
-        *(u32x4 *)(row + 32 * h + 16) = r.v[2];
-        *(u32x4 *)(row + 32 * h + 24) = r.v[3];
+        const float d = f16_to_f32(r.s);
+        const float da = d * (float)(int8_t)byte_of(r.v[3], 8 * hh + 4 * o + h);
+        const float db = d * (float)(int8_t)byte_of(r.v[3], 8 * hh + 4 * o + 2 + h);
+        s.a0 = da * 0x1p24f;  // (q)*ds - 32*ds with both products exact, one rounding
+        s.b0 = -32.f * da;
+        s.a1 = db * 0x1p24f;
+        s.b1 = -32.f * db;
     }
+    return s;
+}
+
+// Chunk j (8 values) of the half row as bf16 and the LDS chunk it fills:
+// Q8_0 / BF16 chunk 4h + j; Q4_K / Q6_K chunks 2h, 2h+1, 4+2h, 5+2h.
+template <int FMT>
+__device__ __forceinline__ u32x4 w_chunk(const WRaw &r, const WScale &s, int j, int64_t k0) {
+    if constexpr (FMT == WF_Q8_0) {
+        const uint32_t u0 = r.v[j >> 1][2 * (j & 1)] ^ 0x80808080u, u1 = r.v[j >> 1][2 * (j & 1) + 1] ^ 0x80808080u;
+        const uint32_t p0 = u0 & 0x00FF00FFu, p1 = __builtin_amdgcn_perm(0u, u0, 0x0C030C01u);
+        const uint32_t p2 = u1 & 0x00FF00FFu, p3 = __builtin_amdgcn_perm(0u, u1, 0x0C030C01u);
+        const float a = s.a0, b = s.b0;
+        return u32x4{pack_bf16x2(mix_lo(p0, a, b), mix_lo(p1, a, b)), pack_bf16x2(mix_hi(p0, a, b), mix_hi(p1, a, b)),
+                     pack_bf16x2(mix_lo(p2, a, b), mix_lo(p3, a, b)), pack_bf16x2(mix_hi(p2, a, b), mix_hi(p3, a, b))};
+    } else if constexpr (FMT == WF_Q4_K) {
+        // j < 2: low nibbles of qs bytes [8j, 8j+8); j >= 2: high nibbles of
+        // bytes [8(j-2), ...). The halves of (y & m) hold bytes 0 and 2, those
+        // of ((y >> 8) & m) bytes 1 and 3.
+        const int jb = j & 1;
+        const uint32_t y0 = r.v[1][2 * jb], y1 = r.v[1][2 * jb + 1];
+        const uint32_t m = j < 2 ? 0x000F000Fu : 0x00F000F0u;
+        const float a = j < 2 ? s.a0 : s.a1, b = j < 2 ? s.b0 : s.b1;
+        const uint32_t p0 = y0 & m, p1 = (y0 >> 8) & m, p2 = y1 & m, p3 = (y1 >> 8) & m;
+        return u32x4{pack_bf16x2(mix_lo(p0, a, b), mix_lo(p1, a, b)), pack_bf16x2(mix_hi(p0, a, b), mix_hi(p1, a, b)),
+                     pack_bf16x2(mix_lo(p2, a, b), mix_lo(p3, a, b)), pack_bf16x2(mix_hi(p2, a, b), mix_hi(p3, a, b))};
+    } else if constexpr (FMT == WF_Q6_K) {
+        // j < 2: value rows ra = 2o (ql piece v[0]), j >= 2: rb = 2o + 1 (v[1]);
+        // low nibbles when o == 0, high when o == 1; qh bits 2r .. 2r+1 of v[2]
+        const int o = (int)((k0 & 127) >> 6);
+        const int jb = j & 1, rr = 2 * o + (j >> 1);
+        const u32x4 &L = j < 2 ? r.v[0] : r.v[1];
+        const uint32_t q0 = L[2 * jb] >> (4 * o), q1 = L[2 * jb + 1] >> (4 * o);
+        const uint32_t c0 = (q0 & 0x0F0F0F0Fu) | (((r.v[2][2 * jb] >> (2 * rr)) & 0x03030303u) << 4);
+        const uint32_t c1 = (q1 & 0x0F0F0F0Fu) | (((r.v[2][2 * jb + 1] >> (2 * rr)) & 0x03030303u) << 4);
+        const float a = j < 2 ? s.a0 : s.a1, b = j < 2 ? s.b0 : s.b1;
+        const uint32_t p0 = c0 & 0x00FF00FFu, p1 = __builtin_amdgcn_perm(0u, c0, 0x0C030C01u);
+        const uint32_t p2 = c1 & 0x00FF00FFu, p3 = __builtin_amdgcn_perm(0u, c1, 0x0C030C01u);
+        return u32x4{pack_bf16x2(mix_lo(p0, a, b), mix_lo(p1, a, b)), pack_bf16x2(mix_hi(p0, a, b), mix_hi(p1, a, b)),
+                     pack_bf16x2(mix_lo(p2, a, b), mix_lo(p3, a, b)), pack_bf16x2(mix_hi(p2, a, b), mix_hi(p3, a, b))};
+    } else {
+        return r.v[j];
+    }
+}
+
+template <int FMT>
+__device__ __forceinline__ int w_slot(int j, int h) {
+    if constexpr (FMT == WF_Q4_K || FMT == WF_Q6_K) return (j < 2 ? 2 * h : 4 + 2 * h) + (j & 1);
+    else return 4 * h + j;
 }
 
 // silu with the hardware reciprocal (about 1 ulp) instead of an IEEE divide
@@ -158,34 +185,45 @@ __device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcp
 template <int FMT, int EPI>
 __global__ __launch_bounds__(256, 2) void qgemm_kernel(const uint16_t *__restrict__ A, int64_t M,
                                                        int64_t lda, GemmWeight w, EpiParams ep) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave >> 1, wn = wave & 1, l32 = lane & 31, g = lane >> 5;
     const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
     const int64_t K = w.k;
     // split K (gridDim.z > 1): this workgroup covers k steps [kt0, kt0 + KT)
     // and writes its f32 partial sums to slice blockIdx.z of ep.out
     const int KT = (int)(K / BK / gridDim.z);
     const int kt0 = (int)blockIdx.z * KT;
+    // step q of this share, clamped to the last (redundant loads, no branches)
+    auto kofs = [&](int q) __attribute__((always_inline)) { return (int64_t)(kt0 + min(q, KT - 1)) * BK; };
 
-    // loader roles
-    const int a_row = tid >> 3, a_kc = (tid & 7) * 8;
+    // A: chunk a_kc of rows a_row + 32 i (rows past M clamped to row M-1: they
+    // only feed output rows the epilogue never writes)
+    const int a_row = tid >> 3, a_kc = tid & 7;
+    const uint16_t *asrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) asrc[i] = A + min(m0 + a_row + 32 * i, M - 1) * lda + 8 * a_kc;
+    // W: half w_h of row n0 + w_nl
     const int w_nl = tid >> 1, w_h = tid & 1;
+    const int64_t wrow = n0 + w_nl;
 
-    u32x4 ra[4];
-    WRaw rw;
-
-    // rows past M are clamped to row M-1: they only feed unwritten output rows
-    auto load_a = [&](int64_t k0) {
+    u32x4 ra[RING][4];
+    WRaw rw[RING];
+    auto load = [&](int slot, int q) __attribute__((always_inline)) {
+        const int64_t k0 = kofs(q);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int64_t gm = min(m0 + a_row + 32 * i, M - 1);
-            ra[i] = *(const u32x4 *)(A + gm * lda + k0 + a_kc);
-        }
+        for (int i = 0; i < 4; i++) ra[slot][i] = *(const u32x4 *)(asrc[i] + k0);
+        load_w<FMT>(w, wrow, k0, w_h, rw[slot]);
     };
-    auto store_a = [&](uint16_t *as) {
+    // ring slot -> LDS stage (the weights dequantized on the way)
+    auto stage_in = [&](int slot, int q, int stage) __attribute__((always_inline)) {
+        uint8_t *as = lds + stage * STAGE, *bs = as + TILEB;
 #pragma unroll
-        for (int i = 0; i < 4; i++) *(u32x4 *)(as + (a_row + 32 * i) * LP + a_kc) = ra[i];
+        for (int i = 0; i < 4; i++) *(u32x4 *)(as + swz(a_row + 32 * i, a_kc)) = ra[slot][i];
+        const int64_t k0 = kofs(q);
+        const WScale sc = w_scales<FMT>(rw[slot], k0, w_h);
+#pragma unroll
+        for (int j = 0; j < 4; j++) *(u32x4 *)(bs + swz(w_nl, w_slot<FMT>(j, w_h))) = w_chunk<FMT>(rw[slot], sc, j, k0);
     };
 
     f32x16 acc[2][2];
@@ -196,43 +234,62 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(const uint16_t *__restric
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-    load_a((int64_t)kt0 * BK);
-    load_w<FMT>(w, n0 + w_nl, (int64_t)kt0 * BK, w_h, rw);
-    store_a(lds);
-    store_w<FMT>(lds + 128 * LP, w_nl, w_h, (int64_t)kt0 * BK, rw);
-    __syncthreads();
-
-    for (int kt = kt0; kt < kt0 + KT; kt++) {
-        const int cur = (kt - kt0) & 1;
-        const bool more = kt + 1 < kt0 + KT;
-        if (more) {
-            load_a((int64_t)(kt + 1) * BK);
-            load_w<FMT>(w, n0 + w_nl, (int64_t)(kt + 1) * BK, w_h, rw);
-        }
-        const uint16_t *as = lds + cur * STAGE;
-        const uint16_t *bs = as + 128 * LP;
+    // operand fragments of one 16-wide k slice, double-buffered across slices
+    bf16x8 fa[2][2], fb[2][2];
+    auto rd = [&](int buf, int stage, int kk) __attribute__((always_inline)) {
+        const uint8_t *as = lds + stage * STAGE, *bs = as + TILEB;
 #pragma unroll
-        for (int kk = 0; kk < BK / 16; kk++) {
-            bf16x8 af[2], bf[2];
+        for (int i = 0; i < 2; i++) fa[buf][i] = *(const bf16x8 *)(as + swz(wm * 64 + i * 32 + l32, 2 * kk + g));
 #pragma unroll
-            for (int i = 0; i < 2; i++)
-                af[i] = *(const bf16x8 *)(as + (wm * 64 + i * 32 + (lane & 31)) * LP + kk * 16 + (lane >> 5) * 8);
+        for (int j = 0; j < 2; j++) fb[buf][j] = *(const bf16x8 *)(bs + swz(wn * 64 + j * 32 + l32, 2 * kk + g));
+    };
+    auto mm = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int j = 0; j < 2; j++)
-                bf[j] = *(const bf16x8 *)(bs + (wn * 64 + j * 32 + (lane & 31)) * LP + kk * 16 + (lane >> 5) * 8);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[buf][i], fb[buf][j], acc[i][j], 0, 0, 0);
+    };
+
+    // prologue: steps 0 .. RING-1 in flight, step 0 staged, its slice 0 read
 #pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (more) {
-            uint16_t *an = lds + (cur ^ 1) * STAGE;
-            store_a(an);
-            store_w<FMT>(an + 128 * LP, w_nl, w_h, (int64_t)(kt + 1) * BK, rw);
-        }
+    for (int q = 0; q < RING; q++) load(q, q);
+    stage_in(0, 0, 0);
+    __syncthreads();
+    rd(0, 0, 0);
+
+    // Step q: ring slot c = q % RING (compile time after unrolling) held step
+    // q, already staged; it now receives step q + RING. On entry fa/fb[0] hold
+    // slice 0 of step q. The next slice is read while the current one
+    // computes, and step q+1 goes from slot (q+1) % RING into the other stage
+    // (its loads were issued two steps ago). ONE barrier per step, before the
+    // last slice, whose operands are then in registers: it publishes the
+    // other stage and frees this one, whose slice 0 of step q+1 is read while
+    // the last two slices compute.
+    auto step = [&](int q, auto c_) __attribute__((always_inline)) {
+        constexpr int c = decltype(c_)::value, c1 = (c + 1) % RING;
+        const int st = q & 1;
+        load(c, q + RING);
+        __builtin_amdgcn_sched_barrier(0);  // the loads issue here, ahead of the staging that waits on older ones
+        rd(1, st, 1);
+        mm(0);
+        stage_in(c1, q + 1, st ^ 1);
+        rd(0, st, 2);
+        mm(1);
+        rd(1, st, 3);
+        __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
         __syncthreads();
+        mm(0);
+        rd(0, st ^ 1, 0);
+        mm(1);
+    };
+    int q = 0;
+    for (; q + 2 <= KT; q += 2) {
+        step(q, std::integral_constant<int, 0>{});
+        step(q + 1, std::integral_constant<int, 1>{});
     }
+    if (q < KT) step(q, std::integral_constant<int, 0>{});
+    __syncthreads();  // every wave is done reading the operand stages
 
     // accumulators -> f32 tile in LDS
     float *cs = (float *)lds;

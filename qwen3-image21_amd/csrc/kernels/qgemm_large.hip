@@ -33,17 +33,6 @@ constexpr int STAGE = 2 * 256 * ROWB;          // A rows then B rows: 64 KB
 constexpr int LDS_BYTES = 2 * STAGE;           // 128 KB
 constexpr int GROUP_M = 4;
 
-// 16 B chunk c of LDS row r sits at slot c ^ key(r), key = (r & 7) ^ ((r >> 3) & 1).
-// Measured on gfx950: 16 B reads are served 16 lanes (256 B) per cycle and are
-// conflict free when the 16 rows of a group cover all 16 slots of a 256 B
-// window (same-parity rows need distinct keys); 16 B writes are served 8 lanes
-// (128 B) per cycle and need distinct keys on each aligned group of 8 rows.
-// This key satisfies both.
-__device__ __forceinline__ int swz_key(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-__device__ __forceinline__ int swz(int r, int c) { return r * ROWB + ((c ^ swz_key(r)) << 4); }
-
-typedef __attribute__((address_space(3))) void *lds_ptr_t;
-
 // A word whose value the optimizer must not look through (keeps nibble masks as
 // whole-word ops so the byte converts below stay v_cvt_f32_ubyte{0..3}).
 __device__ __forceinline__ uint32_t opaque(uint32_t x) {
@@ -76,20 +65,6 @@ __device__ __forceinline__ u32x4 cvt8(uint32_t x0, uint32_t x1, float ds, float 
     auto f = [&](uint32_t x, int i) { return __builtin_fmaf((float)((x >> (8 * i)) & 0xffu), ds, off); };
     return u32x4{pack_bf16x2(f(x0, 0), f(x0, 1)), pack_bf16x2(f(x0, 2), f(x0, 3)),
                  pack_bf16x2(f(x1, 0), f(x1, 1)), pack_bf16x2(f(x1, 2), f(x1, 3))};
-}
-
-// f32 fma with src0 read as f16 from the low / high half of x: a code q held
-// as the f16 subnormal q * 2^-24 (exact) times a scale pre-multiplied by 2^24
-// gives q*scale + off with a single rounding, no separate integer convert.
-__device__ __forceinline__ float mix_lo(uint32_t x, float s, float c) {
-    float r;
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(s), "v"(c));
-    return r;
-}
-__device__ __forceinline__ float mix_hi(uint32_t x, float s, float c) {
-    float r;
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(s), "v"(c));
-    return r;
 }
 
 __device__ __forceinline__ uint32_t word(const u32x4 *v, int byte_off) {
@@ -309,7 +284,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
     // loads, no branches)
     load_w<FMT>(w, wrow, 0, rw[0]);
     dma_a(0, 0);
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __builtin_amdgcn_s_waitcnt(WAIT_VM0);  // vmcnt(0)
     {
         const WScale sc = w_scales<FMT>(rw[0], 0);
         uint8_t *bn = lds + 256 * ROWB;
@@ -319,7 +294,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
     load_w<FMT>(w, wrow, (int64_t)min(1, KT - 1) * BK, rw[1]);
     dma_a(1, (int64_t)min(1, KT - 1) * BK);
     load_w<FMT>(w, wrow, (int64_t)min(2, KT - 1) * BK, rw[0]);
-    __builtin_amdgcn_s_waitcnt(0xc070);  // vmcnt(0) lgkmcnt(0)
+    __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);  // vmcnt(0) lgkmcnt(0)
     __syncthreads();
     rd(0, 0, 0);
 
@@ -349,7 +324,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
         mm(0);
 #pragma unroll
         for (int c = 6; c < 8; c++) *(u32x4 *)(bn + swz(tid, c)) = w_chunk<FMT>(rw[t], sc, c, knext);
-        __builtin_amdgcn_s_waitcnt(0xc070);  // vmcnt(0) lgkmcnt(0)
+        __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);  // vmcnt(0) lgkmcnt(0)
         __syncthreads();
         dma_a(s, (int64_t)min(kt + 2, KT - 1) * BK);
         load_w<FMT>(w, wrow, (int64_t)min(kt + 3, KT - 1) * BK, rw[t]);
@@ -362,7 +337,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
         step(kt + 1, std::integral_constant<int, 1>{});
     }
     if (kt < KT) step(kt, std::integral_constant<int, 0>{});
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): no load into LDS still in flight
+    __builtin_amdgcn_s_waitcnt(WAIT_VM0);  // vmcnt(0): no load into LDS still in flight
 
     // ---- epilogue, straight from the accumulators ----
     // acc[i][j][r] holds row wm*128 + 32i + 8(r/4) + 4g + (r%4) and column
@@ -472,14 +447,14 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
                                       acc[a][j][4 * q + 3]};
                         }
                     }
-                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes landed
+                __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);  // lgkmcnt(0): the wave's LDS writes landed
                 __builtin_amdgcn_wave_barrier();
                 float v[128], ss4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int c = 0; c < 128; c++) v[c] = ft[c * 64 + (((lane >> 2) ^ (c & 15)) << 2) + (lane & 3)];
 #pragma unroll
                 for (int c = 0; c < 128; c++) ss4[c & 3] += v[c] * v[c];
-                __builtin_amdgcn_s_waitcnt(0xc07f);
+                __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
                 __builtin_amdgcn_wave_barrier();  // the half is read before the next one is written
                 const int64_t m = mw + h * 64 + lane;
                 const uint32_t mc = min((uint32_t)m, Mlast);
@@ -521,7 +496,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
                                   pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])};
                     }
                 }
-            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
             __builtin_amdgcn_wave_barrier();
             // one d row (128 tokens = 256 B) per 16 lanes, 16 B (8 tokens) per lane
 #pragma unroll 4

@@ -33,8 +33,6 @@ constexpr int MAXM = 64;         // token rows per workgroup
 constexpr int XROWB = SK * 2;    // bytes per activation row in LDS (256)
 constexpr int XSTAGE = MAXM * XROWB;  // 16 KB
 
-typedef __attribute__((address_space(3))) void *lds_ptr_t;
-
 __device__ __forceinline__ uint32_t byte_of(const u32x4 &x, int i) {
     return (x[i >> 2] >> (8 * (i & 3))) & 0xffu;
 }
@@ -105,7 +103,7 @@ template <int FMT>
 __device__ __forceinline__ bf16x8 frag(const WStep &r, int s, int64_t k0, int kg) {
     if constexpr (FMT == WF_Q4_K) {
         const int c = (int)((k0 & 255) >> 6);
-        const float d = f16_bits_to_f32(r.a[0] & 0xffffu), dmin = f16_bits_to_f32(r.a[0] >> 16);
+        const float d = f16_to_f32(r.a[0] & 0xffffu), dmin = f16_to_f32(r.a[0] >> 16);
         float sc, mn;
         q4k_sc_m(r.a, 2 * c + s, sc, mn);
         const uint32_t sh = 4u * (uint32_t)s;  // sub-block 2c: low nibbles, 2c+1: high
@@ -119,10 +117,10 @@ __device__ __forceinline__ bf16x8 frag(const WStep &r, int s, int64_t k0, int kg
         const uint32_t q0 = r.b[2 * s] >> qsh, q1 = r.b[2 * s + 1] >> qsh;
         const uint32_t c0 = (q0 & 0x0F0F0F0Fu) | (((r.c[0] >> hsh) & 0x03030303u) << 4);
         const uint32_t c1 = (q1 & 0x0F0F0F0Fu) | (((r.c[1] >> hsh) & 0x03030303u) << 4);
-        const float ds = f16_bits_to_f32(r.s) * (float)(int8_t)byte_of(r.a, 8 * hh + 2 * r6 + (kg >> 1));
+        const float ds = f16_to_f32(r.s) * (float)(int8_t)byte_of(r.a, 8 * hh + 2 * r6 + (kg >> 1));
         return cvt8(c0, c1, ds, -32.f * ds);  // (q+32)*ds - 32*ds, exact
     } else if constexpr (FMT == WF_Q8_0) {
-        const float d = f16_bits_to_f32(s ? (r.s >> 16) : (r.s & 0xffffu));
+        const float d = f16_to_f32(s ? (r.s >> 16) : (r.s & 0xffffu));
         return cvt8(r.a[2 * s] ^ 0x80808080u, r.a[2 * s + 1] ^ 0x80808080u, d, -128.f * d);  // biased codes
     } else {
         return __builtin_bit_cast(bf16x8, s ? r.b : r.a);
@@ -422,17 +420,6 @@ __device__ __forceinline__ void load_tile(const GemmWeight &w, int64_t g, int64_
     r.h1 = *(const u32x4 *)(b + ho + 32);
     r.sc = *(const u32x4 *)(b + 192);
     r.d = *(const uint32_t *)(b + 208);  // d and two pad bytes
-}
-
-__device__ __forceinline__ float mix_lo(uint32_t x, float s, float c) {
-    float r;
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(s), "v"(c));
-    return r;
-}
-__device__ __forceinline__ float mix_hi(uint32_t x, float s, float c) {
-    float r;
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(s), "v"(c));
-    return r;
 }
 
 // The raw registers pass through an empty asm first, so no decoding of a tile

@@ -943,6 +943,232 @@ hipError_t launch(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, in
 
 }  // namespace ws
 
+// ---------------------------------------------------------------------------
+// M <= 16, Q4_K / Q6_K / Q8_0, K <= 4096 with K % 1024 == 0, plain, residual or
+// SwiGLU outputs with at least one workgroup step per CU: the split-K sum of a
+// unit inside one workgroup.
+//
+// All of x (16 rows x K) sits in LDS (132 KB at K = 4096), so one workgroup of
+// eight waves per CU holds every k chunk. Wave v always takes chunk v % C of
+// group slot v / C; a step covers NW / (C * per_unit) whole epilogue units
+// (a SwiGLU unit's gate and up groups, or single groups), and the workgroup
+// walks its steps (grid-strided over the units) with the next step's tiles in
+// registers, as in the cross-workgroup kernel. The partial sums of a step go
+// to LDS (double-buffered by step), one barrier, and the chunk-0 wave of each
+// unit adds them in chunk order (deterministic) and applies the epilogue.
+// Against the cross-workgroup kernel this drops the partial-sum stores and
+// loads through memory, the arrival counters and the three memory round trips
+// at the tail.
+namespace wl {
+
+constexpr int NW = 8;    // waves per workgroup (one workgroup per CU)
+constexpr int MAXC = 4;  // k chunks of x held in LDS
+
+struct Plan {
+    int C, G, UPS, per_unit, total, steps;
+};
+
+bool plan(const GemmWeight &w, int64_t m, int epi, int cus, Plan &p) {
+    if ((w.fmt != WF_Q4_K && w.fmt != WF_Q6_K && w.fmt != WF_Q8_0) || m < 1 || m > 16 || w.k % ws::KCH ||
+        w.n % 16 || cus <= 0 || epi == EPI_QKV)
+        return false;
+    if (epi == EPI_SWIGLU && w.n % 128) return false;
+    p.C = (int)(w.k / ws::KCH);
+    p.per_unit = epi == EPI_SWIGLU ? 2 : 1;
+    const int items = p.C * p.per_unit;  // items per unit
+    if (p.C > MAXC || NW % items) return false;
+    p.UPS = NW / items;
+    p.G = (int)(w.n / 16);
+    const int units = p.G / p.per_unit;
+    if (units % p.UPS) return false;
+    p.total = units / p.UPS;
+    // fewer workgroup steps than CUs leave CUs idle: the cross-workgroup
+    // kernel spreads such products wider
+    if (p.total < cus) return false;
+    p.steps = (p.total + cus - 1) / cus;
+    return p.steps <= ws::MAX_STEPS;
+}
+
+template <int FMT, int EPI, int STEPS>
+__global__ __launch_bounds__(64 * NW, 1) void wl_kernel(const uint16_t *__restrict__ A, int M, int64_t lda, GemmWeight w,
+                                                        Plan p, EpiParams ep) {
+    using namespace ws;
+    __shared__ __attribute__((aligned(16))) uint8_t xs[MAXC * 16 * XROW];
+    __shared__ __attribute__((aligned(16))) float red[2][NW][256];
+    const int lane = threadIdx.x & 63, l16 = lane & 15, kg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = wave % p.C, gi = wave / p.C;  // this wave's chunk and group slot
+    const int64_t SB = w.k / 256, N = w.n;
+    const int64_t grid = gridDim.x;
+    // group of this wave at workgroup step st
+    auto group_of = [&](int64_t st) __attribute__((always_inline)) {
+        const int64_t unit = st * p.UPS + gi / p.per_unit;
+        if constexpr (EPI == EPI_SWIGLU) return 8 * (unit >> 2) + (unit & 3) + 4 * (gi & 1);  // gate, then up
+        else return unit;
+    };
+
+    // all of x -> LDS by direct loads: instruction i of wave v fills 64
+    // consecutive 16 B pieces of one row of one chunk; rows past M repeat row M - 1
+    const int pieces = p.C * 16 * (KCH / 8);
+    for (int q0 = wave * 64; q0 < pieces; q0 += NW * 64) {
+        const int cc = q0 / (16 * (KCH / 8)), rem = q0 % (16 * (KCH / 8));
+        const int m = rem / (KCH / 8), s0 = rem % (KCH / 8);
+        const uint16_t *src = A + (int64_t)min(m, M - 1) * lda + (int64_t)cc * KCH + 8 * (s0 + lane);
+        __builtin_amdgcn_global_load_lds((const void *)src, (lds_ptr_t)(xs + (cc * 16 + m) * XROW + 16 * s0), 16, 0, 0);
+    }
+    int64_t st = blockIdx.x;
+    int64_t g = group_of(st);
+    Tile<FMT> ring[SBC];
+#pragma unroll
+    for (int t = 0; t < SBC; t++) {
+        load_tile(w, g, (int64_t)c * SBC + t, SB, l16, kg, ring[t]);
+        __builtin_amdgcn_sched_barrier(0);  // tiles issue in order: each wait covers one tile
+    }
+    // the x pieces were issued before the tiles: wait for them alone, then for
+    // every wave's pieces
+    constexpr int TL = FMT == WF_Q6_K ? 6 : 5;  // loads per tile
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(SBC * TL) : "memory");
+
+    const uint8_t *xrow = xs + (c * 16 + l16) * XROW;
+    constexpr bool CP = FMT == WF_Q4_K && q4_code_products(1);
+    float xq0[SBC], xq1[SBC];
+    if constexpr (CP) {
+        // X_kg and X_{4+kg} of token l16 for the chunk's four super-blocks
+        bf16x8 ones[4];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const uint32_t v = (l16 >> 2) == s ? 0x3F803F80u : 0u;
+            ones[s] = __builtin_bit_cast(bf16x8, u32x4{v, v, v, v});
+        }
+#pragma unroll
+        for (int t = 0; t < SBC; t++) {
+            const uint8_t *xr = xrow + 512 * t;
+            f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const bf16x8 f0 = *(const bf16x8 *)(xr + 64 * j + 16 * kg);
+                const bf16x8 f1 = *(const bf16x8 *)(xr + 64 * (4 + j) + 16 * kg);
+                a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], f0, a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], f1, a1, 0, 0, 0);
+            }
+            xq0[t] = a0[0];
+            xq1[t] = a1[0];
+        }
+    }
+
+    // one workgroup step: this wave's item, its partial sums to LDS, the
+    // barrier, then the unit's chunk-0 wave reduces and stores
+    auto step = [&](int s, auto prefetch) __attribute__((always_inline)) {
+        const int64_t gn = group_of(min(st + grid, (int64_t)p.total - 1));
+        f32x4 acc[1], accM[1];
+        acc[0] = accM[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < SBC; t++) {
+            if constexpr (CP) tile_q4<1>(ring[t], xrow + 512 * t, kg, &xq0[t], &xq1[t], acc, accM);
+            else if constexpr (FMT == WF_Q4_K) tile_q4d<1>(ring[t], xrow + 512 * t, kg, acc);
+            else if constexpr (FMT == WF_Q6_K) tile_q6<1>(ring[t], xrow + 512 * t, kg, acc);
+            else tile_q8<1>(ring[t], xrow + 512 * t, kg, acc);
+#pragma unroll
+            for (int e = 0; e < 4; e++) asm volatile("" : "+v"(acc[0][e]));
+            if constexpr (decltype(prefetch)::value) load_tile(w, gn, (int64_t)c * SBC + t, SB, l16, kg, ring[t]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (CP) acc[0] -= accM[0];
+        float *mine = red[s & 1][wave];
+#pragma unroll
+        for (int e = 0; e < 4; e++) mine[(4 * kg + e) * 16 + l16] = acc[0][e];
+        __syncthreads();
+        // chunk sums in chunk order; lane holds tokens 4 kg + e of column l16
+        auto csum = [&](int slot) __attribute__((always_inline)) {
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            for (int cc = 0; cc < p.C; cc++) {
+                const float *r = red[s & 1][slot * p.C + cc];
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] += r[(4 * kg + e) * 16 + l16];
+            }
+            return v;
+        };
+        if (c == 0 && (EPI != EPI_SWIGLU || (gi & 1) == 0)) {
+            const f32x4 v = csum(gi);
+            if constexpr (EPI == EPI_SWIGLU) {
+                const f32x4 up = csum(gi + 1);
+                const int64_t unit = st * p.UPS + gi / 2, blk = unit >> 2, q = unit & 3;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int m = 4 * kg + e;
+                    if (m < M)
+                        ep.hmid[m * ep.ldh + 64 * blk + 16 * q + l16] =
+                            (uint16_t)(pack_bf16x2(silu(v[e]) * up[e], 0.f) & 0xffffu);
+                }
+            } else {
+                const int64_t n = g * 16 + l16;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int m = 4 * kg + e;
+                    if (m < M) {
+                        if constexpr (EPI == EPI_F32) {
+                            ((float *)ep.out)[m * ep.ldo + n] = v[e];
+                        } else if constexpr (EPI == EPI_BF16) {
+                            ((uint16_t *)ep.out)[m * ep.ldo + n] = (uint16_t)(pack_bf16x2(v[e], 0.f) & 0xffffu);
+                        } else {  // EPI_RESID
+                            const float *grow = ep.gvec + (int64_t)(m / (int)ep.g_rows_per) * ep.g_stride;
+                            ep.x_out[m * N + n] = ep.x_in[m * N + n] + grow[n] * v[e];
+                        }
+                    }
+                }
+            }
+        }
+        st += grid;
+        g = gn;
+    };
+    // straight-line over the compile-time step count (see the cross-workgroup
+    // kernel); the guard is uniform over the workgroup, so every wave meets
+    // the same barriers
+    static_assert(STEPS >= 1 && STEPS <= MAX_STEPS, "steps");
+    step(0, std::integral_constant<bool, (STEPS > 1)>{});
+    if constexpr (STEPS > 1) {
+        if (st < p.total) {
+            step(1, std::integral_constant<bool, (STEPS > 2)>{});
+            if constexpr (STEPS > 2) {
+                if (st < p.total) {
+                    step(2, std::integral_constant<bool, (STEPS > 3)>{});
+                    if constexpr (STEPS > 3) {
+                        if (st < p.total) step(3, std::false_type{});
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int FMT, int STEPS>
+hipError_t launch_steps(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, int epi, const EpiParams &ep,
+                        const Plan &p, int grid, hipStream_t stream) {
+    const dim3 g((unsigned)grid), block(64 * NW);
+    switch (epi) {
+    case EPI_F32: wl_kernel<FMT, EPI_F32, STEPS><<<g, block, 0, stream>>>(a, m, lda, w, p, ep); break;
+    case EPI_BF16: wl_kernel<FMT, EPI_BF16, STEPS><<<g, block, 0, stream>>>(a, m, lda, w, p, ep); break;
+    case EPI_RESID: wl_kernel<FMT, EPI_RESID, STEPS><<<g, block, 0, stream>>>(a, m, lda, w, p, ep); break;
+    case EPI_SWIGLU: wl_kernel<FMT, EPI_SWIGLU, STEPS><<<g, block, 0, stream>>>(a, m, lda, w, p, ep); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t launch(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, int epi, const EpiParams &ep,
+                  const Plan &p, int cus, hipStream_t stream) {
+    switch (p.steps) {
+    case 1: return launch_steps<FMT, 1>(w, a, m, lda, epi, ep, p, cus, stream);
+    case 2: return launch_steps<FMT, 2>(w, a, m, lda, epi, ep, p, cus, stream);
+    case 3: return launch_steps<FMT, 3>(w, a, m, lda, epi, ep, p, cus, stream);
+    case 4: return launch_steps<FMT, 4>(w, a, m, lda, epi, ep, p, cus, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace wl
+
 // Sum of the split-K partials of C[m][n], in split order.
 __device__ __forceinline__ float csum(const float *part, int splits, int64_t MN, int64_t idx) {
     float v = 0.f;
@@ -1057,6 +1283,15 @@ hipError_t launch_qgemm_stream(const GemmWeight &w, const uint16_t *a, int64_t m
                                const EpiParams &ep, float *work, hipStream_t stream) {
     uint32_t *counters = (uint32_t *)work;
     float *part = (float *)((char *)work + STREAM_COUNTER_BYTES);
+    const int cus = m16::device_cus();
+    wl::Plan lp;
+    if (wl::plan(w, m, epi, cus, lp)) {
+        switch (w.fmt) {
+        case WF_Q4_K: return wl::launch<WF_Q4_K>(w, a, (int)m, lda, epi, ep, lp, cus, stream);
+        case WF_Q6_K: return wl::launch<WF_Q6_K>(w, a, (int)m, lda, epi, ep, lp, cus, stream);
+        default: return wl::launch<WF_Q8_0>(w, a, (int)m, lda, epi, ep, lp, cus, stream);
+        }
+    }
     ws::Plan wp;
     if (ws::plan(w, m, epi, m16::device_cus(), wp)) {
         switch (w.fmt) {

@@ -1176,32 +1176,50 @@ __device__ __forceinline__ float csum(const float *part, int splits, int64_t MN,
     return v;
 }
 
-// Elementwise epilogues: one thread per output element (SwiGLU: per output
-// column of the hidden, gate and up read from the interleaved layout).
+// Sum of the split-K partials of 4 consecutive outputs at idx (16 B aligned),
+// in split order; every share's 16 B load is issued before the adds.
+constexpr int MAX_SPLITS = 16;  // qgemm_stream_splits and qgemm_mid_splits stay within it
+__device__ __forceinline__ f32x4 csum4(const float *part, int splits, int64_t MN, int64_t idx) {
+    f32x4 p[MAX_SPLITS];
+#pragma unroll
+    for (int s = 0; s < MAX_SPLITS; s++)
+        if (s < splits) p[s] = *(const f32x4 *)(part + s * MN + idx);
+    f32x4 v = p[0];
+#pragma unroll
+    for (int s = 1; s < MAX_SPLITS; s++)
+        if (s < splits) v += p[s];
+    return v;
+}
+
+// Elementwise epilogues: one thread per 4 consecutive outputs (SwiGLU: per 4
+// output columns of the hidden, gate and up read from the interleaved layout).
 template <int EPI>
 __global__ __launch_bounds__(256) void stream_epi_kernel(const float *__restrict__ part, int splits, int64_t M,
                                                          int64_t N, EpiParams ep) {
     const int64_t MN = M * N;
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint32_t q = blockIdx.x * 256u + threadIdx.x;  // quad index (M * N < 2^31, N % 4 == 0)
     if constexpr (EPI == EPI_SWIGLU) {
         // hidden column h = 64 g + j (j < 64): gate at device column 128 g + j, up at 128 g + 64 + j
-        const int64_t F = N / 2;
-        if (idx >= M * F) return;
-        const int64_t m = idx / F, h = idx % F;
-        const int64_t cg = (h >> 6) * 128 + (h & 63);
-        const float gt = csum(part, splits, MN, m * N + cg), up = csum(part, splits, MN, m * N + cg + 64);
-        ep.hmid[m * ep.ldh + h] = (uint16_t)(pack_bf16x2(silu(gt) * up, 0.f) & 0xffffu);
+        const uint32_t F = (uint32_t)(N / 2);
+        if ((int64_t)q * 4 >= M * F) return;
+        const uint32_t m = q * 4 / F, h = q * 4 % F;
+        const int64_t cg = (int64_t)(h >> 6) * 128 + (h & 63);
+        const f32x4 gt = csum4(part, splits, MN, (int64_t)m * N + cg), up = csum4(part, splits, MN, (int64_t)m * N + cg + 64);
+        *(u32x2 *)(ep.hmid + (int64_t)m * ep.ldh + h) =
+            u32x2{pack_bf16x2(silu(gt[0]) * up[0], silu(gt[1]) * up[1]), pack_bf16x2(silu(gt[2]) * up[2], silu(gt[3]) * up[3])};
     } else {
+        const int64_t idx = (int64_t)q * 4;
         if (idx >= MN) return;
-        const int64_t m = idx / N, n = idx % N;
-        const float v = csum(part, splits, MN, idx);
+        const uint32_t m = (uint32_t)(idx / N), n = (uint32_t)(idx % N);
+        const f32x4 v = csum4(part, splits, MN, idx);
         if constexpr (EPI == EPI_F32) {
-            ((float *)ep.out)[m * ep.ldo + n] = v;
+            *(f32x4 *)((float *)ep.out + (int64_t)m * ep.ldo + n) = v;
         } else if constexpr (EPI == EPI_BF16) {
-            ((uint16_t *)ep.out)[m * ep.ldo + n] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
+            *(u32x2 *)((uint16_t *)ep.out + (int64_t)m * ep.ldo + n) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         } else {  // EPI_RESID
             const float *grow = ep.gvec + (int64_t)((int)m / (int)ep.g_rows_per) * ep.g_stride;
-            ep.x_out[m * N + n] = ep.x_in[m * N + n] + grow[n] * v;
+            const f32x4 x = *(const f32x4 *)(ep.x_in + idx), gv = *(const f32x4 *)(grow + n);
+            *(f32x4 *)(ep.x_out + idx) = x + gv * v;
         }
     }
 }
@@ -1315,8 +1333,9 @@ hipError_t launch_qgemm_stream(const GemmWeight &w, const uint16_t *a, int64_t m
 
 hipError_t launch_split_epilogue(const float *part, int splits, int64_t m, int64_t N, int epi, const EpiParams &ep,
                                  hipStream_t stream) {
-    const int64_t elems = epi == EPI_SWIGLU ? m * N / 2 : m * N;
-    const dim3 grid((unsigned)((elems + 255) / 256)), block(256);
+    if (splits < 1 || splits > MAX_SPLITS || N % 4 || m * N >= (int64_t)1 << 31) return hipErrorInvalidValue;
+    const int64_t quads = (epi == EPI_SWIGLU ? m * N / 2 : m * N) / 4;
+    const dim3 grid((unsigned)((quads + 255) / 256)), block(256);
     switch (epi) {
     case EPI_F32: stream_epi_kernel<EPI_F32><<<grid, block, 0, stream>>>(part, splits, m, N, ep); break;
     case EPI_BF16: stream_epi_kernel<EPI_BF16><<<grid, block, 0, stream>>>(part, splits, m, N, ep); break;

@@ -132,7 +132,9 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *_
                                                                float sl2, uint16_t *__restrict__ out, KeyMask km,
                                                                const int32_t *__restrict__ lim) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
+    // the wave index as a scalar (the DMA destinations then go to M0 without a lane read)
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), g = lane >> 5,
+              l32 = lane & 31;
 
     // XCD-aware order: workgroups are dealt round-robin over 8 XCDs; each XCD
     // gets a contiguous range of (batch, head, query tile) so the query tiles

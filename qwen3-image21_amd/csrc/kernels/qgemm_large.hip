@@ -211,7 +211,9 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
                                                              int64_t lda, GemmWeight w, EpiParams ep,
                                                              int mt, int nt) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index as a scalar: the LDS destinations of the direct loads are
+    // then scalar values set into M0 without a lane read per load
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1, l32 = lane & 31, g = lane >> 5;
 
     // XCD-aware, M-grouped tile order

@@ -30,7 +30,9 @@ namespace {
 constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int ROWB = 128;                      // bytes per LDS row: 64 bf16
 constexpr int STAGE = 2 * 256 * ROWB;          // A rows then B rows: 64 KB
-constexpr int LDS_BYTES = 2 * STAGE;           // 128 KB
+constexpr int QP = 132;                        // f32 pitch of the q/k epilogue rows (128 + 4: conflict free)
+constexpr int LDS_BYTES = 4 * 64 * QP * 4;     // 132 KB: the two operand stages (128 KB) or four waves' q/k rows
+static_assert(LDS_BYTES >= 2 * STAGE, "operand stages fit");
 constexpr int GROUP_M = 4;
 
 // A word whose value the optimizer must not look through (keeps nibble masks as
@@ -420,73 +422,100 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
             // q/k: RMSNorm over the head's 128 columns, RoPE on (2i, 2i+1), q
             // also scaled, bf16 rows to [B,H,S,128]; one 64-row half at a
             // time with one token row per lane. The half's accumulators go to
-            // this wave's 32 KB of LDS as f32 [column][row] in 16 B pieces of
-            // 4 rows (piece p of column c at slot p ^ (c & 15): conflict free
-            // for the 16 B writes and for the 4 B reads of one row by 64
-            // lanes), then each lane reads its row back, so the row reduction
-            // and the RoPE partner stay inside the lane. The code stays
-            // compact: the same work done in the accumulator layout unrolls to
-            // ~10K instructions that stream through the instruction cache once
-            // per tile.
-            float *ft = (float *)lds + wave * 64 * 128;
-            const float *nwt = sec == 0 ? ep.norm_q : ep.norm_k;
+            // this wave's 33 KB of LDS as f32 rows with a pitch of 132 floats
+            // (16 B reads of 16 rows then cover all 64 banks once), and each
+            // lane reads its row back 16 B at a time, so the row reduction and
+            // the RoPE partner stay inside the lane. The code stays compact:
+            // the same work done in the accumulator layout unrolls to ~10K
+            // instructions that stream through the instruction cache once per
+            // tile.
+            float *ft = (float *)lds + wave * 64 * QP;
+            // the norm weights are the same for every lane and unchanged by the
+            // kernel: read through the constant address space (scalar loads)
+            typedef __attribute__((address_space(4))) const f32x4 cf32x4;
+            const __attribute__((address_space(4))) float *nwt =
+                (const __attribute__((address_space(4))) float *)(sec == 0 ? ep.norm_q : ep.norm_k);
             const float osc = sec == 0 ? ep.q_scale : 1.0f;
             uint16_t *dst = sec == 0 ? ep.q : ep.k;
             const uint32_t Su = (uint32_t)S, Mlast = (uint32_t)(M - 1);
 #pragma unroll
             for (int h = 0; h < 2; h++) {
+                // the second half's accumulators stay in place until the first is done
+                __builtin_amdgcn_sched_barrier(0);
+                // rows of the half to LDS, row-major with a pitch of QP floats:
+                // register 4q + k of tile (ii, j) is row 32 ii + 8 q + 4 g + k,
+                // column 32 j + l32
 #pragma unroll
                 for (int ii = 0; ii < 2; ii++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const int c = j * 32 + l32;
+                    for (int j = 0; j < 4; j++)
 #pragma unroll
-                        for (int q = 0; q < 4; q++) {
-                            const int p = ii * 8 + 2 * q + g;  // rows 4p .. 4p+3 of the half
-                            const int a = 2 * h + ii;
-                            *(f32x4 *)(ft + c * 64 + ((p ^ (c & 15)) << 2)) =
-                                f32x4{acc[a][j][4 * q], acc[a][j][4 * q + 1], acc[a][j][4 * q + 2],
-                                      acc[a][j][4 * q + 3]};
-                        }
-                    }
-                __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);  // lgkmcnt(0): the wave's LDS writes landed
-                __builtin_amdgcn_wave_barrier();
-                float v[128], ss4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int c = 0; c < 128; c++) v[c] = ft[c * 64 + (((lane >> 2) ^ (c & 15)) << 2) + (lane & 3)];
-#pragma unroll
-                for (int c = 0; c < 128; c++) ss4[c & 3] += v[c] * v[c];
-                __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
-                __builtin_amdgcn_wave_barrier();  // the half is read before the next one is written
+                        for (int r = 0; r < 16; r++)
+                            ft[(ii * 32 + 8 * (r >> 2) + 4 * g + (r & 3)) * QP + j * 32 + l32] = acc[2 * h + ii][j][r];
                 const int64_t m = mw + h * 64 + lane;
                 const uint32_t mc = min((uint32_t)m, Mlast);
                 const uint32_t s = mc % Su, b = mc / Su;
-                const float rs = 1.0f / sqrtf(((ss4[0] + ss4[1]) + (ss4[2] + ss4[3])) * (1.0f / 128.0f) + 1e-6f);
                 const float *pr = ep.pe + (int64_t)s * 128;  // (cos, sin) of pair i at 2i, 2i + 1
                 uint16_t *orow = dst + (((int64_t)b * H + head) * S + s) * 128;
+                // the row's RoPE table in four batches of 32 columns, each
+                // batch's loads issued a batch ahead (the first before the sum
+                // of squares)
+                f32x4 pt[2][8];
 #pragma unroll
-                for (int c0 = 0; c0 < 128; c0 += 8) {
-                    const f32x4 cs0 = *(const f32x4 *)(pr + c0), cs1 = *(const f32x4 *)(pr + c0 + 4);
-                    const f32x4 w0 = *(const f32x4 *)(nwt + c0), w1 = *(const f32x4 *)(nwt + c0 + 4);
-                    const float cs[8] = {cs0.x, cs0.y, cs0.z, cs0.w, cs1.x, cs1.y, cs1.z, cs1.w};
-                    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-                    u32x4 o;
+                for (int e = 0; e < 8; e++) pt[0][e] = *(const f32x4 *)(pr + 4 * e);
+                __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);  // lgkmcnt(0): the wave's LDS writes landed
+                __builtin_amdgcn_wave_barrier();
+                // each lane reads its own row back, 16 B at a time, twice: for
+                // the sum of squares, then for the rotation
+                const float *frow = ft + lane * QP;
+                float ss4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const float x0 = v[c0 + 2 * e] * rs * wv[2 * e];
-                        const float x1 = v[c0 + 2 * e + 1] * rs * wv[2 * e + 1];
-                        const float co = cs[2 * e], sn = cs[2 * e + 1];
-                        o[e] = pack_bf16x2((x0 * co - x1 * sn) * osc, (x0 * sn + x1 * co) * osc);
-                    }
-                    if (m < M) *(u32x4 *)(orow + c0) = o;
+                for (int c = 0; c < 128; c += 4) {
+                    const f32x4 x = *(const f32x4 *)(frow + c);
+                    ss4[0] += x.x * x.x;
+                    ss4[1] += x.y * x.y;
+                    ss4[2] += x.z * x.z;
+                    ss4[3] += x.w * x.w;
                 }
+                const float rs = 1.0f / sqrtf(((ss4[0] + ss4[1]) + (ss4[2] + ss4[3])) * (1.0f / 128.0f) + 1e-6f);
+#pragma unroll
+                for (int bt = 0; bt < 4; bt++) {
+                    if (bt < 3) {
+#pragma unroll
+                        for (int e = 0; e < 8; e++) pt[(bt + 1) & 1][e] = *(const f32x4 *)(pr + 32 * (bt + 1) + 4 * e);
+                    }
+#pragma unroll
+                    for (int cc = 0; cc < 4; cc++) {
+                        const int c0 = 32 * bt + 8 * cc;
+                        const f32x4 x0v = *(const f32x4 *)(frow + c0), x1v = *(const f32x4 *)(frow + c0 + 4);
+                        const f32x4 cs0 = pt[bt & 1][2 * cc], cs1 = pt[bt & 1][2 * cc + 1];
+                        const f32x4 w0 = *(const cf32x4 *)(nwt + c0), w1 = *(const cf32x4 *)(nwt + c0 + 4);
+                        const float xv[8] = {x0v.x, x0v.y, x0v.z, x0v.w, x1v.x, x1v.y, x1v.z, x1v.w};
+                        const float cs[8] = {cs0.x, cs0.y, cs0.z, cs0.w, cs1.x, cs1.y, cs1.z, cs1.w};
+                        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                        u32x4 o;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const float x0 = xv[2 * e] * rs * wv[2 * e];
+                            const float x1 = xv[2 * e + 1] * rs * wv[2 * e + 1];
+                            const float co = cs[2 * e], sn = cs[2 * e + 1];
+                            o[e] = pack_bf16x2((x0 * co - x1 * sn) * osc, (x0 * sn + x1 * co) * osc);
+                        }
+                        if (m < M) *(u32x4 *)(orow + c0) = o;
+                    }
+                }
+                __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
+                __builtin_amdgcn_wave_barrier();  // the half is read before the next one is written
             }
         } else {
             // V^T: tile[d][t], 8-token groups XOR-swizzled by d. Registers
             // 4q .. 4q+3 hold 4 consecutive tokens (4-aligned; the swizzle
-            // only flips bits 3-6): one 8 B write each.
+            // only flips bits 3-6): one 8 B write each. One 32-row block of
+            // accumulators at a time (a scheduling fence each), so they are
+            // not all copied out of the accumulator registers at once.
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < 4; i++) {
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const int d = j * 32 + l32;
@@ -498,6 +527,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
                                   pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])};
                     }
                 }
+            }
             __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
             __builtin_amdgcn_wave_barrier();
             // one d row (128 tokens = 256 B) per 16 lanes, 16 B (8 tokens) per lane
@@ -520,7 +550,8 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
             }
             if (ep.v_bhsd) {
 #pragma unroll
-                for (int i = 0; i < 4; i++)
+                for (int i = 0; i < 4; i++) {
+                    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                     for (int r = 0; r < 16; r++) {
                         const int64_t m = mw + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -531,6 +562,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
                             ep.v_bhsd[((b * H + head) * S + s) * 128 + j * 32 + l32] =
                                 (uint16_t)(pack_bf16x2(acc[i][j][r], 0.f) & 0xffffu);
                     }
+                }
             }
         }
     }

@@ -454,9 +454,8 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
                             ft[(ii * 32 + 8 * (r >> 2) + 4 * g + (r & 3)) * QP + j * 32 + l32] = acc[2 * h + ii][j][r];
                 const int64_t m = mw + h * 64 + lane;
                 const uint32_t mc = min((uint32_t)m, Mlast);
-                const uint32_t s = mc % Su, b = mc / Su;
+                const uint32_t s = mc % Su;
                 const float *pr = ep.pe + (int64_t)s * 128;  // (cos, sin) of pair i at 2i, 2i + 1
-                uint16_t *orow = dst + (((int64_t)b * H + head) * S + s) * 128;
                 // the row's RoPE table in four batches of 32 columns, each
                 // batch's loads issued a batch ahead (the first before the sum
                 // of squares)
@@ -501,7 +500,23 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
                             const float co = cs[2 * e], sn = cs[2 * e + 1];
                             o[e] = pack_bf16x2((x0 * co - x1 * sn) * osc, (x0 * sn + x1 * co) * osc);
                         }
-                        if (m < M) *(u32x4 *)(orow + c0) = o;
+                        // back into the lane's own row (bytes already read)
+                        *(u32x4 *)((uint16_t *)frow + c0) = o;
+                    }
+                }
+                __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
+                __builtin_amdgcn_wave_barrier();
+                // the half's bf16 rows out with 16 lanes per 256 B row, so every
+                // store covers whole lines (row-per-lane stores leave partial
+                // lines that reach memory more than once)
+#pragma unroll 4
+                for (int it = 0; it < 16; it++) {
+                    const int rr = it * 4 + (lane >> 4), ch = lane & 15;
+                    const int64_t mr = mw + h * 64 + rr;
+                    if (mr < M) {
+                        const uint32_t sr = (uint32_t)mr % Su, br = (uint32_t)mr / Su;
+                        *(u32x4 *)(dst + (((int64_t)br * H + head) * S + sr) * 128 + ch * 8) =
+                            *(const u32x4 *)((const uint16_t *)(ft + rr * QP) + ch * 8);
                     }
                 }
                 __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);

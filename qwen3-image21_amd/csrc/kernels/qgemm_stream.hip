@@ -387,6 +387,28 @@ template <int FMT>
 using Tile = typename std::conditional<FMT == WF_Q4_K, TileQ4,
                                        typename std::conditional<FMT == WF_Q6_K, TileQ6, TileQ8>::type>::type;
 
+// The A fragment of step s of a 256-k tile for lane group kg (8 consecutive
+// k, 16 B): its byte offset in a tile row. Q4_K steps are the 32-k
+// sub-blocks; a Q6_K or Q8_0 step pair covers a 64-k block, in which group
+// kg holds 16 consecutive k and the step's parity picks 8 of them.
+template <int FMT>
+__device__ __forceinline__ int xoff(int s, int kg) {
+    return FMT == WF_Q4_K ? 64 * s + 16 * kg : 128 * (s >> 1) + 32 * kg + 16 * (s & 1);
+}
+
+// A fragments from an activation row in LDS (token tile tt 16 rows further).
+template <int FMT>
+struct XLds {
+    const uint8_t *row;
+    int kg;
+    __device__ __forceinline__ bf16x8 operator()(int s, int tt) const {
+        if constexpr (FMT == WF_Q4_K) return *(const bf16x8 *)(row + tt * 16 * XROW + 64 * s + 16 * kg);
+        else if constexpr (FMT == WF_Q6_K)
+            return *(const bf16x8 *)(row + tt * 16 * XROW + 256 * (s >> 2) + 128 * ((s >> 1) & 1) + 32 * kg + 16 * (s & 1));
+        else return *(const bf16x8 *)(row + tt * 16 * XROW + 128 * (s >> 1) + 32 * kg + 16 * (s & 1));
+    }
+};
+
 // Q8_0 (device layout: codes [N][K], f16 scales [N][K/32]): lane kg holds the
 // 16-code pieces at k = 64 q + 16 kg (q < 4) of its row and the row's 8
 // scales of the super-block-sized tile.
@@ -438,8 +460,8 @@ __device__ __forceinline__ void pin(TileQ8 &r) {
 // k = 64 q + 16 kg + 8 h + i, all in 32-value block 2 q + kg / 2; codes biased
 // to unsigned (q + 128) sit in f16 halves as subnormals, one v_fma_mix each
 // gives (q + 128) d - 128 d = q d exactly, then RNE to bf16.
-template <int MT>
-__device__ __forceinline__ void tile_q8(TileQ8 r, const uint8_t *xrow, int kg, f32x4 *acc) {
+template <int MT, class XF>
+__device__ __forceinline__ void tile_q8(TileQ8 r, XF xf, int kg, f32x4 *acc) {
     pin(r);
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -456,7 +478,7 @@ __device__ __forceinline__ void tile_q8(TileQ8 r, const uint8_t *xrow, int kg, f
                               pack_bf16x2(mix_lo(p2, a, b), mix_lo(p3, a, b)), pack_bf16x2(mix_hi(p2, a, b), mix_hi(p3, a, b))};
 #pragma unroll
             for (int tt = 0; tt < MT; tt++) {
-                const bf16x8 av = *(const bf16x8 *)(xrow + tt * 16 * XROW + 128 * q + 32 * kg + 16 * h);
+                const bf16x8 av = xf(2 * q + h, tt);
                 acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bw), acc[tt], 0, 0, 0);
             }
         }
@@ -468,8 +490,8 @@ __device__ __forceinline__ void tile_q8(TileQ8 r, const uint8_t *xrow, int kg, f
 // 8-byte half h8 = s % 2 of the lane's 16 B pieces; the values are
 // k = 128 hh + 32 (r1 + 2 n) + 16 h' + 8 h8 + i of the super-block, scale
 // index 8 hh + 4 n + kg. Each step's B fragment serves every token tile.
-template <int MT>
-__device__ __forceinline__ void tile_q6(TileQ6 r, const uint8_t *xrow, int kg, f32x4 *acc) {
+template <int MT, class XF>
+__device__ __forceinline__ void tile_q6(TileQ6 r, XF xf, int kg, f32x4 *acc) {
     pin(r);
     const float d = m16::cvt_f16_lo(r.d);
     const uint32_t hsh = 2u * (uint32_t)(kg >> 1);  // qh bit pair of quadrant r1 (+4 for n = 1)
@@ -493,7 +515,7 @@ __device__ __forceinline__ void tile_q6(TileQ6 r, const uint8_t *xrow, int kg, f
                           pack_bf16x2(mix_lo(p2, a, b), mix_lo(p3, a, b)), pack_bf16x2(mix_hi(p2, a, b), mix_hi(p3, a, b))};
 #pragma unroll
         for (int tt = 0; tt < MT; tt++) {
-            const bf16x8 av = *(const bf16x8 *)(xrow + tt * 16 * XROW + 256 * hh + 128 * n + 32 * kg + 16 * h8);
+            const bf16x8 av = xf(s, tt);
             acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bw), acc[tt], 0, 0, 0);
         }
     }
@@ -502,8 +524,8 @@ __device__ __forceinline__ void tile_q6(TileQ6 r, const uint8_t *xrow, int kg, f
 // One Q4_K tile by code products (see the m16 notes above) into accA / accM
 // of each token tile; xq0[tt] / xq1[tt] hold the sub-block sums X_kg,
 // X_{4+kg} of token 16 tt + l16 for this super-block.
-template <int MT>
-__device__ __forceinline__ void tile_q4(TileQ4 r, const uint8_t *xrow, int kg, const float *xq0, const float *xq1,
+template <int MT, class XF>
+__device__ __forceinline__ void tile_q4(TileQ4 r, XF xf, int kg, const float *xq0, const float *xq1,
                                         f32x4 *accA, f32x4 *accM) {
     pin(r);
     const uint32_t hx = r.h[0], hy = r.h[1], hz = r.h[2], hw = r.h[3];
@@ -532,7 +554,7 @@ __device__ __forceinline__ void tile_q4(TileQ4 r, const uint8_t *xrow, int kg, c
             f32x4 tv[4];
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) {
-                const bf16x8 av = *(const bf16x8 *)(xrow + tt * 16 * XROW + 64 * (4 * hf + jj) + 16 * kg);
+                const bf16x8 av = xf(4 * hf + jj, tt);
                 tv[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bq[jj]),
                                                                  f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
             }
@@ -555,8 +577,8 @@ __device__ __forceinline__ void tile_q4(TileQ4 r, const uint8_t *xrow, int kg, c
 // with a single rounding, then RNE to bf16 (the value every other Q4_K path
 // here feeds the MFMA). Cheaper than the code products once the fragment
 // serves two or more token tiles.
-template <int MT>
-__device__ __forceinline__ void tile_q4d(TileQ4 r, const uint8_t *xrow, int kg, f32x4 *acc) {
+template <int MT, class XF>
+__device__ __forceinline__ void tile_q4d(TileQ4 r, XF xf, int kg, f32x4 *acc) {
     pin(r);
     const uint32_t hx = r.h[0], hy = r.h[1], hz = r.h[2], hw = r.h[3];
     const float d = m16::cvt_f16_lo(hx), dmin = m16::cvt_f16_hi(hx);
@@ -576,7 +598,7 @@ __device__ __forceinline__ void tile_q4d(TileQ4 r, const uint8_t *xrow, int kg, 
                           pack_bf16x2(mix_lo(p2, a, b), mix_lo(p3, a, b)), pack_bf16x2(mix_hi(p2, a, b), mix_hi(p3, a, b))};
 #pragma unroll
         for (int tt = 0; tt < MT; tt++) {
-            const bf16x8 av = *(const bf16x8 *)(xrow + tt * 16 * XROW + 64 * j + 16 * kg);
+            const bf16x8 av = xf(j, tt);
             acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bw), acc[tt], 0, 0, 0);
         }
     }
@@ -840,10 +862,11 @@ __global__ __launch_bounds__(64 * nwaves(MT), wg_per_cu(MT) * nwaves(MT) / 4) vo
         for (int tt = 0; tt < MT; tt++) acc[tt] = accM[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < SBC; t++) {
-            if constexpr (CP) tile_q4<MT>(ring[t], xrow + 512 * t, kg, xq0[t], xq1[t], acc, accM);
-            else if constexpr (FMT == WF_Q4_K) tile_q4d<MT>(ring[t], xrow + 512 * t, kg, acc);
-            else if constexpr (FMT == WF_Q6_K) tile_q6<MT>(ring[t], xrow + 512 * t, kg, acc);
-            else tile_q8<MT>(ring[t], xrow + 512 * t, kg, acc);
+            const XLds<FMT> xt{xrow + 512 * t, kg};
+            if constexpr (CP) tile_q4<MT>(ring[t], xt, kg, xq0[t], xq1[t], acc, accM);
+            else if constexpr (FMT == WF_Q4_K) tile_q4d<MT>(ring[t], xt, kg, acc);
+            else if constexpr (FMT == WF_Q6_K) tile_q6<MT>(ring[t], xt, kg, acc);
+            else tile_q8<MT>(ring[t], xt, kg, acc);
             // finish this tile's arithmetic here: left alone, the compiler sinks
             // it past the loads and keeps every tile's products live
 #pragma unroll
@@ -1064,10 +1087,11 @@ __global__ __launch_bounds__(64 * NW, 1) void wl_kernel(const uint16_t *__restri
         acc[0] = accM[0] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < SBC; t++) {
-            if constexpr (CP) tile_q4<1>(ring[t], xrow + 512 * t, kg, &xq0[t], &xq1[t], acc, accM);
-            else if constexpr (FMT == WF_Q4_K) tile_q4d<1>(ring[t], xrow + 512 * t, kg, acc);
-            else if constexpr (FMT == WF_Q6_K) tile_q6<1>(ring[t], xrow + 512 * t, kg, acc);
-            else tile_q8<1>(ring[t], xrow + 512 * t, kg, acc);
+            const XLds<FMT> xt{xrow + 512 * t, kg};
+            if constexpr (CP) tile_q4<1>(ring[t], xt, kg, &xq0[t], &xq1[t], acc, accM);
+            else if constexpr (FMT == WF_Q4_K) tile_q4d<1>(ring[t], xt, kg, acc);
+            else if constexpr (FMT == WF_Q6_K) tile_q6<1>(ring[t], xt, kg, acc);
+            else tile_q8<1>(ring[t], xt, kg, acc);
 #pragma unroll
             for (int e = 0; e < 4; e++) asm volatile("" : "+v"(acc[0][e]));
             if constexpr (decltype(prefetch)::value) load_tile(w, gn, (int64_t)c * SBC + t, SB, l16, kg, ring[t]);
@@ -1168,6 +1192,173 @@ hipError_t launch(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, in
 }
 
 }  // namespace wl
+
+// ---------------------------------------------------------------------------
+// M <= 16, Q4_K / Q6_K / Q8_0, plain or residual outputs with about one 16-row
+// group per CU (the 4096-row down and out projections: 256 groups) and K a
+// multiple of 2048: one workgroup per group over the whole K, so no partial
+// sums leave the workgroup.
+//
+// The eight waves split K into slices of TPW consecutive 256-k tiles (which
+// wave takes which slice rotates with the workgroup, so that CUs running in
+// step read different x lines). Every A fragment then serves one wave only, so
+// x is not staged in LDS:
+// a wave loads its fragments from global memory (16 x K bf16, L2-resident after
+// the first workgroups touch it) straight into registers, XD tiles ahead, while
+// its weight tiles (up to RD) are all requested at the start. The eight
+// partial sums meet in LDS; wave 0 adds them in K order (deterministic) and
+// applies the epilogue. Against the cross-workgroup kernel this drops the
+// partial-sum stores and loads through memory and the arrival counters, and
+// every CU keeps all of its weight bytes in flight from the first instruction.
+namespace wx {
+
+constexpr int NW = 8;    // waves per workgroup (one workgroup per CU)
+constexpr int RD = 6;    // weight tiles in flight per wave
+constexpr int XD = 2;    // x tiles loaded ahead
+constexpr int MAXT = 8;  // tiles per wave
+
+bool plan(const GemmWeight &w, int64_t m, int epi, int cus, int &tpw) {
+    if ((w.fmt != WF_Q4_K && w.fmt != WF_Q6_K && w.fmt != WF_Q8_0) || m < 1 || m > 16 || w.n % 16 || cus <= 0 ||
+        (epi != EPI_F32 && epi != EPI_BF16 && epi != EPI_RESID) || w.k % (256 * NW))
+        return false;
+    const int64_t G = w.n / 16;
+    tpw = (int)(w.k / (256 * NW));
+    // Every workgroup reads all of x (M x K bf16). Beyond K = 4096, once that
+    // passes about twice the group's weight bytes it costs more than the
+    // cross-workgroup kernel's partial sums (measured: Q6_K at K = 12288 wins
+    // up to 13 tokens, Q8_0 at K = 16384 up to 16).
+    const int wb = w.fmt == WF_Q4_K ? 144 : w.fmt == WF_Q6_K ? 224 : 272;  // device bytes per 256 weights
+    if (w.k > 4096 && m * 2 * 256 >= 2 * 16 * wb) return false;
+    // more groups than CUs share x better in the LDS-staged kernels; far fewer
+    // leave CUs idle
+    return tpw >= 1 && tpw <= MAXT && 2 * G >= cus && G <= cus;
+}
+
+// A fragments of one tile held in registers (step s -> fragment s)
+struct XReg {
+    const bf16x8 *f;
+    __device__ __forceinline__ bf16x8 operator()(int s, int) const { return f[s]; }
+};
+
+template <int FMT, int EPI, int TPW>
+__global__ __launch_bounds__(64 * NW, 1) void wx_kernel(const uint16_t *__restrict__ A, int M, int64_t lda, GemmWeight w,
+                                                        EpiParams ep) {
+    using namespace ws;
+    constexpr int R = TPW < RD ? TPW : RD, X = TPW < XD ? TPW : XD;
+    __shared__ __attribute__((aligned(16))) float red[NW][256];
+    const int lane = threadIdx.x & 63, l16 = lane & 15, kg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t g = blockIdx.x, SB = w.k / 256, N = w.n;
+    // K slice of this wave, rotated by workgroup: the same wave of every CU
+    // would otherwise read the same x lines at the same time
+    const int slice = (wave + (int)(g % NW)) % NW;
+    const int64_t sb0 = (int64_t)slice * TPW;
+    // this lane's token row (rows past M repeat row M - 1) at the wave's first tile
+    const uint8_t *xr = (const uint8_t *)(A + (int64_t)min(l16, M - 1) * lda) + sb0 * 512;
+    Tile<FMT> ring[R];
+    bf16x8 xf[X][8];
+    auto load_x = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < 8; s++) xf[t % X][s] = *(const bf16x8 *)(xr + t * 512 + xoff<FMT>(s, kg));
+    };
+    // issue order x0 w0 x1 w1 w2 ...: the first tile waits for its own bytes only
+#pragma unroll
+    for (int t = 0; t < R; t++) {
+        if (t < X) load_x(t);
+        load_tile(w, g, sb0 + t, SB, l16, kg, ring[t]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // Q4_K by code products (exact weights, as in the other kernels up to 16
+    // tokens): X_kg and X_{4+kg} of token l16 from the tile's fragments by
+    // bf16 MFMA against row-selector ones
+    constexpr bool CP = FMT == WF_Q4_K && q4_code_products(1);
+    bf16x8 ones[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const uint32_t v = (l16 >> 2) == s ? 0x3F803F80u : 0u;
+        ones[s] = __builtin_bit_cast(bf16x8, u32x4{v, v, v, v});
+    }
+    f32x4 acc[1], accM[1];
+    acc[0] = accM[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        const XReg xt{xf[t % X]};
+        if constexpr (CP) {
+            f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], xf[t % X][j], a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones[j], xf[t % X][4 + j], a1, 0, 0, 0);
+            }
+            const float xq0 = a0[0], xq1 = a1[0];
+            tile_q4<1>(ring[t % R], xt, kg, &xq0, &xq1, acc, accM);
+        } else if constexpr (FMT == WF_Q4_K) tile_q4d<1>(ring[t % R], xt, kg, acc);
+        else if constexpr (FMT == WF_Q6_K) tile_q6<1>(ring[t % R], xt, kg, acc);
+        else tile_q8<1>(ring[t % R], xt, kg, acc);
+#pragma unroll
+        for (int e = 0; e < 4; e++) asm volatile("" : "+v"(acc[0][e]));
+        if (t + R < TPW) load_tile(w, g, sb0 + t + R, SB, l16, kg, ring[t % R]);
+        if (t + X < TPW) load_x(t + X);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (CP) acc[0] -= accM[0];
+    // acc[0][e] = token 4 kg + e, row 16 g + l16
+#pragma unroll
+    for (int e = 0; e < 4; e++) red[slice][(4 * kg + e) * 16 + l16] = acc[0][e];
+    __syncthreads();
+    if (wave != 0) return;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NW; c++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] += red[c][(4 * kg + e) * 16 + l16];
+    const int64_t n = g * 16 + l16;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int m = 4 * kg + e;
+        if (m < M) {
+            if constexpr (EPI == EPI_F32) {
+                ((float *)ep.out)[m * ep.ldo + n] = v[e];
+            } else if constexpr (EPI == EPI_BF16) {
+                ((uint16_t *)ep.out)[m * ep.ldo + n] = (uint16_t)(pack_bf16x2(v[e], 0.f) & 0xffffu);
+            } else {  // EPI_RESID
+                const float *grow = ep.gvec + (int64_t)(m / (int)ep.g_rows_per) * ep.g_stride;
+                ep.x_out[m * N + n] = ep.x_in[m * N + n] + grow[n] * v[e];
+            }
+        }
+    }
+}
+
+template <int FMT, int TPW>
+hipError_t launch_tpw(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, int epi, const EpiParams &ep,
+                      hipStream_t stream) {
+    const dim3 grid((unsigned)(w.n / 16)), block(64 * NW);
+    switch (epi) {
+    case EPI_F32: wx_kernel<FMT, EPI_F32, TPW><<<grid, block, 0, stream>>>(a, m, lda, w, ep); break;
+    case EPI_BF16: wx_kernel<FMT, EPI_BF16, TPW><<<grid, block, 0, stream>>>(a, m, lda, w, ep); break;
+    case EPI_RESID: wx_kernel<FMT, EPI_RESID, TPW><<<grid, block, 0, stream>>>(a, m, lda, w, ep); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t launch(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, int epi, const EpiParams &ep, int tpw,
+                  hipStream_t stream) {
+    switch (tpw) {
+    case 1: return launch_tpw<FMT, 1>(w, a, m, lda, epi, ep, stream);
+    case 2: return launch_tpw<FMT, 2>(w, a, m, lda, epi, ep, stream);
+    case 3: return launch_tpw<FMT, 3>(w, a, m, lda, epi, ep, stream);
+    case 4: return launch_tpw<FMT, 4>(w, a, m, lda, epi, ep, stream);
+    case 5: return launch_tpw<FMT, 5>(w, a, m, lda, epi, ep, stream);
+    case 6: return launch_tpw<FMT, 6>(w, a, m, lda, epi, ep, stream);
+    case 7: return launch_tpw<FMT, 7>(w, a, m, lda, epi, ep, stream);
+    case 8: return launch_tpw<FMT, 8>(w, a, m, lda, epi, ep, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace wx
 
 // Sum of the split-K partials of C[m][n], in split order.
 __device__ __forceinline__ float csum(const float *part, int splits, int64_t MN, int64_t idx) {
@@ -1308,6 +1499,14 @@ hipError_t launch_qgemm_stream(const GemmWeight &w, const uint16_t *a, int64_t m
         case WF_Q4_K: return wl::launch<WF_Q4_K>(w, a, (int)m, lda, epi, ep, lp, cus, stream);
         case WF_Q6_K: return wl::launch<WF_Q6_K>(w, a, (int)m, lda, epi, ep, lp, cus, stream);
         default: return wl::launch<WF_Q8_0>(w, a, (int)m, lda, epi, ep, lp, cus, stream);
+        }
+    }
+    int tpw;
+    if (wx::plan(w, m, epi, cus, tpw)) {
+        switch (w.fmt) {
+        case WF_Q4_K: return wx::launch<WF_Q4_K>(w, a, (int)m, lda, epi, ep, tpw, stream);
+        case WF_Q6_K: return wx::launch<WF_Q6_K>(w, a, (int)m, lda, epi, ep, tpw, stream);
+        default: return wx::launch<WF_Q8_0>(w, a, (int)m, lda, epi, ep, tpw, stream);
         }
     }
     ws::Plan wp;

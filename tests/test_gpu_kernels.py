@@ -137,7 +137,10 @@ def test_qmatmul_short_m_one_launch_repeats(torch_cuda, qctx):
     cases = [(synth.Q6_K, 16, 4096, 3072), (synth.Q4_K, 16, 2048, 4096), (synth.Q6_K, 5, 1024, 12288),
              (synth.Q4_K, 1, 3072, 2048), (synth.Q6_K, 64, 4096, 3072), (synth.Q4_K, 40, 2048, 4096),
              (synth.Q6_K, 17, 1024, 2048), (synth.Q8_0, 16, 4096, 4096), (synth.Q8_0, 64, 2048, 2048),
-             (synth.Q8_0, 3, 1024, 16384), (synth.Q6_K, 16, 4096, 3072)]
+             (synth.Q8_0, 3, 1024, 16384), (synth.Q6_K, 16, 4096, 3072),
+             # one workgroup per 16-row group over the whole K (128-256 groups)
+             (synth.Q6_K, 13, 4096, 12288), (synth.Q4_K, 16, 4096, 4096), (synth.Q8_0, 5, 2048, 16384),
+             (synth.Q6_K, 1, 2048, 2048), (synth.Q4_K, 7, 3072, 6144)]
     first = {}
     for i, (t, m, n, k) in enumerate(cases * 2):
         rng = np.random.default_rng(100 + i % len(cases))

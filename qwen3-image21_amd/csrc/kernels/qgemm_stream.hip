@@ -347,6 +347,8 @@ struct Plan {
     int C, G, WPC, steps, units, per_unit, MT;
 };
 
+size_t part_bytes(const GemmWeight &w, int64_t m);
+
 bool plan(const GemmWeight &w, int64_t m, int epi, int cus, Plan &p) {
     if ((w.fmt != WF_Q4_K && w.fmt != WF_Q6_K && w.fmt != WF_Q8_0) || m < 1 || m > 64 || w.k % KCH || w.n % 16 ||
         cus <= 0)
@@ -361,10 +363,14 @@ bool plan(const GemmWeight &w, int64_t m, int epi, int cus, Plan &p) {
     p.steps = (p.G + nw * p.WPC - 1) / (nw * p.WPC);
     p.per_unit = epi == EPI_QKV ? 8 : epi == EPI_SWIGLU ? 2 : 1;
     p.units = p.G / p.per_unit;
-    return p.steps <= MAX_STEPS && (size_t)p.units * 4 <= STREAM_COUNTER_BYTES;
+    // partial sums addressed by 32-bit byte offsets
+    return p.steps <= MAX_STEPS && (size_t)p.units * 4 <= STREAM_COUNTER_BYTES && part_bytes(w, m) < ((size_t)1 << 31);
 }
 
-// partial sums: [C][G][16 MT tokens][16 rows] f32
+// partial sums: [C][G][item] f32, an item holding token m of row r at
+// pidx(m, r): the four consecutive tokens 4i .. 4i+3 of a row are contiguous,
+// the MFMA result of one lane, one 16 B access
+__host__ __device__ constexpr int pidx(int m, int r) { return ((m >> 2) * 16 + r) * 4 + (m & 3); }
 size_t part_bytes(const GemmWeight &w, int64_t m) {
     const int mt = m <= 16 ? 1 : m <= 32 ? 2 : 4;
     return (size_t)(w.k / KCH) * (size_t)w.n * 64 * mt;
@@ -614,9 +620,23 @@ constexpr bool q4_code_products(int mt) { return mt <= QIMM_Q4_CP_MAX_MT; }
 
 // Partial sums cross workgroups on different XCDs: stored and loaded with
 // system scope (sc0 sc1: written through to, and read from, memory).
-__device__ __forceinline__ void put_coherent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
+// The partial sums as a buffer resource: four consecutive floats per 16 B
+// access with the same system-scope bits (sc0 sc1), which a 16 B atomic or
+// volatile access does not give (volatile loads each wait for the one before).
+// Accesses past `bytes` read zero and drop their stores.
+struct PartBuf {
+    __amdgpu_buffer_rsrc_t r;
+    static constexpr int SYS = 1 | 16;  // cache policy sc0 | sc1
+    __device__ __forceinline__ PartBuf(const float *base, uint32_t bytes)
+        : r(__builtin_amdgcn_make_buffer_rsrc((void *)base, 0, (int)bytes, 0x00020000)) {}
+    __device__ __forceinline__ void put4(uint32_t idx, f32x4 v) const {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, idx * 4u, 0, SYS);
+    }
+    __device__ __forceinline__ f32x4 get4(uint32_t idx) const {
+        return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, idx * 4u, 0, SYS));
+    }
+};
+// one float with the same bits (the q/k/v gather reads column pairs)
 __device__ __forceinline__ float get_coherent(const float *p) {
     return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
@@ -628,13 +648,13 @@ __device__ __forceinline__ float get_coherent(const float *p) {
 // ceil(C / CB) memory round trips instead of one or more per slice.
 // IS = floats per item.
 template <int NS, int VB>
-__device__ __forceinline__ void psum_slices(const float *part, int C, int G, int IS, const int64_t (&gs)[NS],
+__device__ __forceinline__ void psum_slices(const PartBuf &pb, int C, int G, int IS, const int64_t (&gs)[NS],
                                             const int (&tts)[NS], int kg, int r, f32x4 (&out)[NS]) {
     constexpr int CB = VB / (4 * NS) > 0 ? VB / (4 * NS) : 1;
-    const float *base[NS];
+    uint32_t base[NS];
 #pragma unroll
     for (int s = 0; s < NS; s++) {
-        base[s] = part + gs[s] * IS + (16 * tts[s] + 4 * kg) * 16 + r;
+        base[s] = (uint32_t)(gs[s] * IS + pidx(16 * tts[s] + 4 * kg, r));
         out[s] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     for (int c0 = 0; c0 < C; c0 += CB) {
@@ -642,11 +662,13 @@ __device__ __forceinline__ void psum_slices(const float *part, int C, int G, int
 #pragma unroll
         for (int cc = 0; cc < CB; cc++) {
             if (c0 + cc >= C) break;  // wave-uniform: no loads past the last chunk
-            const int64_t off = (int64_t)(c0 + cc) * G * IS;
+            const uint32_t off = (uint32_t)(c0 + cc) * (uint32_t)G * (uint32_t)IS;
 #pragma unroll
-            for (int s = 0; s < NS; s++)
+            for (int s = 0; s < NS; s++) {
+                const f32x4 t = pb.get4(base[s] + off);
 #pragma unroll
-                for (int e = 0; e < 4; e++) v[s][cc][e] = get_coherent(base[s] + off + e * 16);
+                for (int e = 0; e < 4; e++) v[s][cc][e] = t[e];
+            }
         }
 #pragma unroll
         for (int cc = 0; cc < CB; cc++)
@@ -664,6 +686,7 @@ __device__ void unit_epilogue(const float *part, const Plan &p, int64_t unit, in
                               int lane) {
     constexpr int TOK = 16 * MT, IS = 16 * TOK;
     const int l16 = lane & 15, kg = lane >> 4;
+    const PartBuf pb(part, (uint32_t)p.C * (uint32_t)p.G * (uint32_t)IS * 4u);
     if constexpr (EPI == EPI_QKV) {
         // head unit: lane j holds columns (2j, 2j+1) of the head; TB tokens x
         // CB chunks per batch of loads (chunk sums in chunk order; 64 values
@@ -683,12 +706,12 @@ __device__ void unit_epilogue(const float *part, const Plan &p, int64_t unit, in
                 float v[CB][TB][2];
 #pragma unroll
                 for (int cc = 0; cc < CB; cc++) {
-                    const float *pc = part + ((int64_t)min(c0 + cc, p.C - 1) * p.G + g) * IS + r;
+                    const float *pc = part + ((int64_t)min(c0 + cc, p.C - 1) * p.G + g) * IS;
 #pragma unroll
                     for (int i = 0; i < TB; i++) {
                         const int m = min(m0 + i, TOK - 1);
-                        v[cc][i][0] = get_coherent(pc + m * 16);
-                        v[cc][i][1] = get_coherent(pc + m * 16 + 1);
+                        v[cc][i][0] = get_coherent(pc + pidx(m, r));
+                        v[cc][i][1] = get_coherent(pc + pidx(m, r + 1));
                     }
                 }
 #pragma unroll
@@ -741,7 +764,7 @@ __device__ void unit_epilogue(const float *part, const Plan &p, int64_t unit, in
             tts[2 * tt] = tts[2 * tt + 1] = tt;
         }
         f32x4 sum[2 * MT];
-        psum_slices<2 * MT, MT == 1 ? 64 : 128>(part, p.C, p.G, IS, gs, tts, kg, l16, sum);
+        psum_slices<2 * MT, MT == 1 ? 64 : 128>(pb, p.C, p.G, IS, gs, tts, kg, l16, sum);
 #pragma unroll
         for (int tt = 0; tt < MT; tt++) {
 #pragma unroll
@@ -762,7 +785,7 @@ __device__ void unit_epilogue(const float *part, const Plan &p, int64_t unit, in
             tts[tt] = tt;
         }
         f32x4 sum[MT];
-        psum_slices<MT, MT == 1 ? 64 : 128>(part, p.C, p.G, IS, gs, tts, kg, l16, sum);
+        psum_slices<MT, MT == 1 ? 64 : 128>(pb, p.C, p.G, IS, gs, tts, kg, l16, sum);
 #pragma unroll
         for (int tt = 0; tt < MT; tt++) {
 #pragma unroll
@@ -790,6 +813,7 @@ __global__ __launch_bounds__(64 * nwaves(MT), wg_per_cu(MT) * nwaves(MT) / 4) vo
                                                              uint32_t *__restrict__ counters, Plan p, EpiParams ep) {
     constexpr int NW = nwaves(MT), TOK = 16 * MT, IS = 16 * TOK;
     __shared__ __attribute__((aligned(16))) uint8_t xs[TOK * XROW];
+    const PartBuf pb(part, (uint32_t)p.C * (uint32_t)p.G * (uint32_t)IS * 4u);
     const int lane = threadIdx.x & 63, l16 = lane & 15, kg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = blockIdx.x % p.C, slot = blockIdx.x / p.C;
@@ -877,12 +901,11 @@ __global__ __launch_bounds__(64 * nwaves(MT), wg_per_cu(MT) * nwaves(MT) / 4) vo
             __builtin_amdgcn_sched_barrier(0);
         }
         // partial sums of the item: acc[tt][e] = token 16 tt + 4 kg + e, row 16 g + l16
-        float *dst = part + ((int64_t)c * p.G + g) * IS;
+        const uint32_t dst = ((uint32_t)c * (uint32_t)p.G + (uint32_t)g) * (uint32_t)IS;
 #pragma unroll
         for (int tt = 0; tt < MT; tt++) {
             if constexpr (CP) acc[tt] -= accM[tt];
-#pragma unroll
-            for (int e = 0; e < 4; e++) put_coherent(dst + (16 * tt + 4 * kg + e) * 16 + l16, acc[tt][e]);
+            pb.put4(dst + pidx(16 * tt + 4 * kg, l16), acc[tt]);
         }
     };
     // straight-line over the (compile-time) step count: a loop here makes the

@@ -936,13 +936,22 @@ __global__ __launch_bounds__(64 * nwaves(MT), wg_per_cu(MT) * nwaves(MT) / 4) vo
     // waiting for their completion publishes them to every XCD before the
     // counter moves; the completing wave reads them back the same way. (A
     // device-scope fence instead writes back and invalidates the whole L2.)
+    // All of the wave's counter increments go out as one instruction (lane i
+    // counts item i: one round trip), then the wave finishes every unit it
+    // completed.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    for (int64_t gi = g0; gi < p.G; gi += gstep) {
-        const int64_t unit = EPI == EPI_QKV ? gi / 8 : EPI == EPI_SWIGLU ? 4 * (gi / 8) + (gi & 3) : gi;
-        uint32_t old = 0;
-        if (lane == 0) old = atomicAdd(&counters[unit], 1u);
-        old = __shfl(old, 0);
-        if (old == (uint32_t)(p.C * p.per_unit - 1)) {
+    auto unit_of = [&](int64_t gi) { return EPI == EPI_QKV ? gi / 8 : EPI == EPI_SWIGLU ? 4 * (gi / 8) + (gi & 3) : gi; };
+    uint32_t old = 0;
+    {
+        const int64_t gl = g0 + (int64_t)lane * gstep;
+        if (lane < STEPS && gl < p.G) old = atomicAdd(&counters[unit_of(gl)], 1u);
+    }
+#pragma unroll
+    for (int i = 0; i < STEPS; i++) {
+        const int64_t gi = g0 + i * gstep;
+        if (gi >= p.G) break;
+        if (__shfl(old, i) == (uint32_t)(p.C * p.per_unit - 1)) {
+            const int64_t unit = unit_of(gi);
             unit_epilogue<EPI, MT>(part, p, unit, M, N, ep, lane);
             if (lane == 0) __hip_atomic_store(&counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }

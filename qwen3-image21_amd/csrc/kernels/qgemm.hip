@@ -473,16 +473,23 @@ hipError_t launch_any(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t
 }  // namespace
 
 // K split of the 128x128 kernel when its tiles alone would leave CUs idle:
-// doubled (up to 8) while the doubled grid still fits the two resident
-// workgroups per CU (a second one hides the first one's load waits) and each
-// share stays a whole number of 512-value groups. The partial sums cost
-// 8 s m N bytes of traffic (written once, read once); at these token counts
-// an idle CU costs more.
+// doubled (up to 8) while the grid stays within one workgroup per CU and each
+// share a whole number of 512-value groups. The partial sums cost 8 s m N
+// bytes of traffic (written once, read once) and a second launch that sums
+// them, which an unsplit product does not pay. One more doubling fills the
+// second resident workgroup slot of each CU (it hides the first one's load
+// waits) where the product is split already, the doubled grid fills nearly
+// both slots and each share keeps at least 1024 k. Measured on the Q8_0 sets
+// at 256 tokens: out 31 -> 27 us (8 -> 4 shares), qkv 57 -> 55 and up 65 -> 58
+// (2 -> 1), while down at K = 12288 and 16384 keeps its 8 shares.
 int qgemm_mid_splits(const GemmWeight &w, int64_t m) {
     if (m <= 0 || qgemm_large_fits(w, m) || qgemm_stream_fits(w, m)) return 1;
     const int64_t tiles = (w.n / BN) * ((m + BM - 1) / BM), cus = device_cus();
     int s = 1;
-    while (s < 8 && tiles * 2 * s <= 2 * cus && w.k % (512 * 2 * s) == 0) s *= 2;
+    while (s < 8 && tiles * 2 * s <= cus && w.k % (512 * 2 * s) == 0) s *= 2;
+    if (s > 1 && s < 8 && tiles * 2 * s <= 2 * cus && 10 * tiles * 2 * s >= 18 * cus && w.k / (2 * s) >= 1024 &&
+        w.k % (512 * 2 * s) == 0)
+        s *= 2;
     return s;
 }
 

@@ -60,11 +60,14 @@ struct GemmWeight {
 };
 
 // y = A[M,K] (bf16, row stride lda) x W[N,K]^T with the epilogue selected by epi.
-// Dispatches to the 256x256 large-M kernel when qgemm_large_fits, else to the
-// 128x128 kernel.
+// Dispatches to the 256x256 large-M kernel when qgemm_large_fits (at least 512
+// rows, and more 128x128 tiles than one wave of two workgroups per CU), else to
+// the 128x128 kernel.
 hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda,
                         int epi, const EpiParams &ep, hipStream_t stream);
 bool qgemm_large_fits(const GemmWeight &w, int64_t m);
+// Compute units of the current device (0 if the runtime cannot say), read once.
+int device_cu_count();
 
 // Short-M weight-streaming path (M <= 64): split-K partial sums, added in a
 // fixed order by the epilogue (in the same launch for Q4_K / Q6_K at M <= 16).

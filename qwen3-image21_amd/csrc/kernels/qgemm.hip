@@ -447,17 +447,7 @@ hipError_t launch_fmt(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t
     return hipGetLastError();
 }
 
-int device_cus() {
-    static int cus = -1;
-    if (cus < 0) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-            cus = v;
-        else
-            cus = 0;
-    }
-    return cus;
-}
+int device_cus() { return device_cu_count(); }
 
 hipError_t launch_any(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi, const EpiParams &ep,
                       hipStream_t stream, int splits) {
@@ -471,6 +461,18 @@ hipError_t launch_any(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t
 }
 
 }  // namespace
+
+int device_cu_count() {
+    static int cus = -1;
+    if (cus < 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+            cus = v;
+        else
+            cus = 0;
+    }
+    return cus;
+}
 
 // K split of the 128x128 kernel when its tiles alone would leave CUs idle:
 // doubled (up to 8) while the grid stays within one workgroup per CU and each

@@ -601,7 +601,19 @@ hipError_t launch_fmt(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t
 
 }  // namespace
 
-bool qgemm_large_fits(const GemmWeight &w, int64_t m) { return m >= 512 && w.n % BN == 0 && w.k % BK == 0; }
+// The 128x128 kernel (split over K where its tiles are still too few) is
+// faster whenever its whole grid runs as one wave of its two resident
+// workgroups per CU; beyond that its second, partial wave costs more than the
+// 256x256 kernel's idle CUs. Measured: Q4_K 4096 x 4096 at 1024 tokens 109 ->
+// 66 us and Q6_K 4096 x 12288 352 -> 215 us (256 tiles of 128x128), at 2048
+// tokens 2-4% faster (512 tiles); the block step at 1024 image tokens 0.90 ->
+// 0.71 ms. At 2304 tokens (576 tiles), 3072, and gate_up at 512 the 256x256
+// kernel is faster.
+bool qgemm_large_fits(const GemmWeight &w, int64_t m) {
+    if (m < 512 || w.n % BN || w.k % BK) return false;
+    const int64_t mid_tiles = ((m + 127) / 128) * (w.n / 128);
+    return mid_tiles > 2 * (int64_t)device_cu_count();
+}
 
 hipError_t launch_qgemm_large(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
                               const EpiParams &ep, hipStream_t stream) {

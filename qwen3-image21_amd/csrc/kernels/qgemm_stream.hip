@@ -285,17 +285,7 @@ __device__ __forceinline__ void codes8(uint32_t w0, uint32_t w1, u32x4 &lo, u32x
 __device__ __forceinline__ float cvt_f16_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu)); }
 __device__ __forceinline__ float cvt_f16_hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
 
-int device_cus() {
-    static int cus = -1;
-    if (cus < 0) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-            cus = v;
-        else
-            cus = 0;
-    }
-    return cus;
-}
+int device_cus() { return device_cu_count(); }
 
 }  // namespace m16
 

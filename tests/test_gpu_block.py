@@ -172,15 +172,19 @@ def test_block_hidden4096_short_m(torch_cuda, qctx, b, s, p, mlp):
 
 
 @pytest.mark.parametrize("b,s,p,mlp,attn_type,down_type", [
-    (1, 516, 16, 1024, synth.Q4_K, synth.Q6_K),   # a 4-row second tile row
-    (2, 264, 8, 1024, synth.Q4_K, synth.Q6_K),    # batch boundary inside the first 256-row tile
-    (1, 768, 0, 2048, synth.Q8_0, synth.Q8_0)])   # three full tile rows, no prefix
+    (1, 1028, 16, 1024, synth.Q4_K, synth.Q6_K),  # a 4-row last tile row
+    (2, 520, 8, 1024, synth.Q4_K, synth.Q6_K),    # batch boundary inside the third 256-row tile
+    (1, 1024, 0, 2048, synth.Q8_0, synth.Q8_0),   # four full tile rows, no prefix
+    (1, 2820, 0, 4096, synth.Q4_K, synth.Q6_K)])  # out, gate_up and down on 256 x 256 tiles too
 def test_block_hidden4096_large_m(torch_cuda, qctx, b, s, p, mlp, attn_type, down_type):
-    """Hidden 4096 (32 heads) at M >= 512 tokens: the 256 x 256 GEMM's fused
-    q/k/v epilogue over 32 heads (head = column / 128 across 48 column tiles, V
-    written transposed), its residual and SwiGLU epilogues and the XCD-aware tile
-    order, with partial tiles and a batch boundary inside a tile; output, k and v
-    against both oracle modes. Short MLPs keep the oracle quick."""
+    """Hidden 4096 (32 heads) at M >= 1024 tokens, where the q/k/v projection
+    has enough 256 x 256 tiles for the large-M GEMM: its fused q/k/v epilogue
+    over 32 heads (head = column / 128 across 48 column tiles, V written
+    transposed) and the XCD-aware tile order, with partial tiles and a batch
+    boundary inside a tile; at 2820 tokens (12 tile rows) also its residual
+    (out, Q6_K down) and SwiGLU epilogues, on a 4-row last tile row. The
+    products with fewer tiles take the 128 x 128 kernel. Output, k and v against
+    both oracle modes. Short MLPs keep the oracle quick."""
     cfg = dict(hidden=4096, heads=32, head_dim=128, mlp=mlp)
     w, x, mod, pe, kpre, vpre = make_case(61 + b + s, cfg, b, s, p, attn_type, down_type)
     got, (k, v) = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)
@@ -196,9 +200,9 @@ def test_block_hidden4096_large_m(torch_cuda, qctx, b, s, p, mlp, attn_type, dow
 @pytest.mark.parametrize("attn_type,down_type", [(synth.Q8_0, synth.Q8_0), (synth.Q4_K, synth.Q6_K)])
 def test_block_mid_m_split_k(torch_cuda, qctx, attn_type, down_type):
     """Hidden 1024 (8 heads), MLP 2048, 128 tokens over a 16-token prefix: every
-    projection's 128x128 tiles leave CUs idle, so each runs split over K (2 or
-    4 shares) with its partial sums added by the q/k/v, SwiGLU and residual
-    epilogues of the reduction kernel."""
+    projection's 128x128 tiles leave CUs idle, so each runs split over K (2
+    shares of whole 512-value groups) with its partial sums added by the q/k/v,
+    SwiGLU and residual epilogues of the reduction kernel."""
     cfg = dict(hidden=1024, heads=8, head_dim=128, mlp=2048)
     w, x, mod, pe, kpre, vpre = make_case(31, cfg, 1, 128, 16, attn_type, down_type)
     got, (k, v) = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)

@@ -112,26 +112,29 @@ __device__ __forceinline__ int wave_min_i(int v) {
 
 namespace fast {
 
-constexpr int NW = 8;            // waves per workgroup
-constexpr int QB = 32 * NW;      // queries per workgroup
-constexpr int DI = 16 / NW;      // DMA instructions per wave per 16 KB tile
+// A workgroup of NW waves (8, or 4 where 8-wave workgroups leave CUs idle)
+// takes 32 NW queries of one head; each wave owns 32 of them.
 constexpr int KB = 64;           // keys per block
 constexpr int HD = 128;
 constexpr int TILE = KB * HD * 2;     // 16 KB: K (64 rows x 256 B) or V^T (128 rows x 128 B)
 constexpr int STAGE = 2 * TILE;       // K tile then V^T tile
 constexpr int OP = 136;               // bf16 pitch of the output staging rows
-constexpr int LDS_BYTES = 2 * STAGE > NW * 32 * OP * 2 ? 2 * STAGE : NW * 32 * OP * 2;
+constexpr int lds_bytes(int nw) { return 2 * STAGE > nw * 32 * OP * 2 ? 2 * STAGE : nw * 32 * OP * 2; }
 constexpr float RESCALE_TH = 8.0f;    // log2 units
 
 // K tile: key row r holds 16 B chunk c at slot c ^ (r % 16); V^T tile: d row
 // holds 8-key chunk c at slot c ^ ((d / 2) % 8). A 16-lane phase of b128 reads
 // (16 rows, one chunk) then covers all 64 banks once.
-template <bool PRE, bool MASKED>
-__global__ __launch_bounds__(64 * NW, 1) void attn_fast_kernel(const uint16_t *__restrict__ q, Seg s0, Seg s1,
-                                                               int64_t H, int64_t Sq, int64_t nq, int64_t B,
-                                                               float sl2, uint16_t *__restrict__ out, KeyMask km,
-                                                               const int32_t *__restrict__ lim) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
+// Two waves per SIMD either way: one 8-wave or two 4-wave workgroups per CU.
+template <int NW, bool PRE, bool MASKED>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16_t *__restrict__ q, Seg s0, Seg s1,
+                                                                    int64_t H, int64_t Sq, int64_t nq, int64_t B,
+                                                                    float sl2, uint16_t *__restrict__ out,
+                                                                    KeyMask km, const int32_t *__restrict__ lim) {
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    constexpr int QB = 32 * NW;  // queries per workgroup
+    constexpr int DI = 16 / NW;  // DMA instructions per wave per 16 KB tile
+    __shared__ __attribute__((aligned(16))) uint8_t lds[lds_bytes(NW)];
     // the wave index as a scalar (the DMA destinations then go to M0 without a lane read)
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), g = lane >> 5,
               l32 = lane & 31;
@@ -710,6 +713,31 @@ __global__ __launch_bounds__(256, 2) void attn_any_kernel(const uint16_t *__rest
 
 }  // namespace anylen
 
+template <int NW, bool PRE, bool MASKED>
+void launch_fast(const uint16_t *q, Seg s0, Seg s1, int64_t h, int64_t sq, int64_t b, float sl2, uint16_t *out,
+                 const KeyMask &km, const int32_t *lim, hipStream_t stream) {
+    const int64_t nq = (sq + 32 * NW - 1) / (32 * NW);
+    fast::attn_fast_kernel<NW, PRE, MASKED><<<dim3((unsigned)(nq * h * b)), dim3(64 * NW), 0, stream>>>(
+        q, s0, s1, h, sq, nq, b, sl2, out, km, lim);
+}
+
+// Waves per workgroup of the unmasked fast kernel, from the rounds each form
+// takes. An 8-wave workgroup holds a CU alone; a round of them costs 1. Two
+// 4-wave workgroups share a CU and do the same work in 1.05 (one wave per
+// SIMD each, twice the K/V tile traffic per query); a round with at most one
+// 4-wave workgroup per CU, half the work, takes 0.84. Measured at 32 heads,
+// 256 prefix keys on 256 CUs: 1024 queries 42.3 -> 35.7 us and 2304 queries
+// 150 -> 133 us with 4 waves, 4096 queries 268 us with 8 against 282 with 4.
+int fast_waves(int64_t bh, int64_t sq) {
+    const int64_t cus = device_cu_count();
+    if (cus <= 0) return 8;
+    const int64_t n8 = (sq + 255) / 256 * bh, n4 = (sq + 127) / 128 * bh;
+    const int64_t c8 = 100 * ((n8 + cus - 1) / cus);
+    const int64_t r4 = n4 % (2 * cus);
+    const int64_t c4 = 105 * (n4 / (2 * cus)) + (r4 == 0 ? 0 : r4 <= cus ? 84 : 105);
+    return c4 < c8 ? 4 : 8;
+}
+
 // sl2 = softmax scale * log2(e) applied to raw scores, or 1 when q already
 // carries it (PRE)
 template <bool PRE>
@@ -724,9 +752,11 @@ hipError_t launch(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, in
         s1 = Seg{ko, vto, 0};
     }
     if ((p & 7) == 0 && (so & 7) == 0) {
-        const int64_t nq = (sq + fast::QB - 1) / fast::QB;
-        fast::attn_fast_kernel<PRE, false><<<dim3((unsigned)(nq * h * b)), dim3(64 * fast::NW), 0, stream>>>(
-            q, s0, s1, h, sq, nq, b, sl2, out, KeyMask{nullptr, nullptr, p + so}, nullptr);
+        const KeyMask km{nullptr, nullptr, p + so};
+        if (fast_waves(b * h, sq) == 4)
+            launch_fast<4, PRE, false>(q, s0, s1, h, sq, b, sl2, out, km, nullptr, stream);
+        else
+            launch_fast<8, PRE, false>(q, s0, s1, h, sq, b, sl2, out, km, nullptr, stream);
     } else {
         const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;
         anylen::attn_any_kernel<false><<<dim3((unsigned)(nq * h * b)), dim3(256), 0, stream>>>(
@@ -762,9 +792,7 @@ hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const 
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
-        const int64_t nq = (sq + fast::QB - 1) / fast::QB;
-        fast::attn_fast_kernel<false, true><<<dim3((unsigned)(nq * h * b)), dim3(64 * fast::NW), 0, stream>>>(
-            q, s0, s1, h, sq, nq, b, sl2, out, km, img ? lim_scratch : nullptr);
+        launch_fast<8, false, true>(q, s0, s1, h, sq, b, sl2, out, km, img ? lim_scratch : nullptr, stream);
         return hipGetLastError();
     }
     const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;

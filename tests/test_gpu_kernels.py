@@ -287,12 +287,15 @@ def test_attention_matches_oracle(torch_cuda, qctx, b, h, sq, p, so, qmul):
     assert max_abs_rel(got, want) <= 2e-2, max_abs_rel(got, want)
 
 
-def test_attention_config2_shape_sampled_rows(torch_cuda, qctx):
-    """B1 H32, 4096 image queries over 256 prefix + 4096 own keys; sampled query rows."""
+@pytest.mark.parametrize("sq", [4096, 2304])
+def test_attention_config2_shape_sampled_rows(torch_cuda, qctx, sq):
+    """B1 H32, sq image queries over 256 prefix + sq own keys; sampled query rows.
+    4096 queries take the 8-wave fast kernel, 2304 the 4-wave one (two
+    workgroups per CU)."""
     torch = torch_cuda
-    b, h, sq, p = 1, 32, 4096, 256
+    b, h, p = 1, 32, 256
     got, q, ko, vo, kp, vp = _attention_case(torch, qctx, b, h, sq, p, sq, seed=2)
-    rows = np.array([0, 1, 127, 128, 1000, 2047, 3000, 4094, 4095])
+    rows = np.array([0, 1, 127, 128, 1000, 2047, 2175, sq - 2, sq - 1])
     want = O.attention(q[:, :, rows], ko, vo, kp, vp, mode=O.EXACT)
     g = got[:, :, rows]
     assert cos_sim(g, want) >= 0.9999 and max_abs_rel(g, want) <= 2e-2

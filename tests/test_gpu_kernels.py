@@ -287,6 +287,22 @@ def test_attention_matches_oracle(torch_cuda, qctx, b, h, sq, p, so, qmul):
     assert max_abs_rel(got, want) <= 2e-2, max_abs_rel(got, want)
 
 
+@pytest.mark.parametrize("sq,p,so", [
+    (200, 64, 448),   # prefix shorter than a key block (clamped rows); own tail window slides back past two halves
+    (136, 40, 520),   # short prefix; own last window keeps only its last 32-key half
+    (256, 256, 96),   # own segment shorter than a block: halves past its end are skipped
+    (160, 0, 200),    # no prefix; the second window slides back past its first half
+])
+def test_attention_eight_wave_form_ragged_segments(torch_cuda, qctx, sq, p, so):
+    """Batch 2 x 128 heads with 129-256 queries: 256 workgroups of 8 waves fill
+    the CUs, so these ragged and short segments run through the 8-wave fast
+    kernel (the small cases above take the 4-wave form)."""
+    got, q, ko, vo, kp, vp = _attention_case(torch_cuda, qctx, 2, 128, sq, p, so, seed=sq + p + so)
+    want = O.attention(q, ko, vo, kp, vp, mode=O.EXACT)
+    assert cos_sim(got, want) >= 0.9999, cos_sim(got, want)
+    assert max_abs_rel(got, want) <= 2e-2, max_abs_rel(got, want)
+
+
 @pytest.mark.parametrize("sq", [4096, 2304])
 def test_attention_config2_shape_sampled_rows(torch_cuda, qctx, sq):
     """B1 H32, sq image queries over 256 prefix + sq own keys; sampled query rows.

@@ -1382,6 +1382,202 @@ hipError_t launch(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, in
 
 }  // namespace wx
 
+// ---------------------------------------------------------------------------
+// 17-64 tokens, K = 4096, plain or SwiGLU outputs with 4 or 6 weight
+// groups (16 rows each) per CU: each workgroup keeps its groups over the whole
+// K, so no partial sums leave it.
+//
+// Two waves per group, one for the even and one for the odd 256-k tiles. x
+// goes through LDS in 512-wide sub-chunks (one tile per wave), double-buffered
+// and staged through registers one sub-chunk ahead (register loads only, so the
+// compiler's load waits stay exact); each wave keeps R weight tiles in flight.
+// After the last sub-chunk the two waves of a group add their sums in LDS (even
+// wave first) and the epilogue runs per unit. Against the cross-workgroup
+// kernel this drops the split-K partial sums (C x 64 x N x 4 bytes written and
+// read back), the arrival counters and the memory round trips at the tail, for
+// eight x sub-chunk reads from L2 per workgroup instead of one chunk.
+namespace wk {
+
+constexpr int SKC = 512;           // k per x sub-chunk (two 256-k tiles)
+constexpr int XP = SKC * 2 + 16;   // padded LDS row: a fragment's 16 rows hit distinct bank groups
+constexpr int KS = 4096 / SKC;     // sub-chunks (K = 4096)
+
+struct Plan {
+    int GPW, UPW, per_unit;
+};
+
+bool plan(const GemmWeight &w, int64_t m, int epi, int cus, Plan &p) {
+    if ((w.fmt != WF_Q4_K && w.fmt != WF_Q6_K && w.fmt != WF_Q8_0) || m < 17 || m > 64 || cus <= 0 ||
+        (epi != EPI_F32 && epi != EPI_BF16 && epi != EPI_SWIGLU) || w.k != 4096 || w.n % 128)
+        return false;
+    const int64_t G = w.n / 16;
+    if (G % cus) return false;
+    p.GPW = (int)(G / cus);
+    p.per_unit = epi == EPI_SWIGLU ? 2 : 1;
+    p.UPW = p.GPW / p.per_unit;
+    return p.GPW == 4 || p.GPW == 6;
+}
+
+// A fragments from an x sub-chunk row in LDS (token tile tt 16 rows further)
+template <int FMT>
+struct XSub {
+    const uint8_t *row;
+    int kg;
+    __device__ __forceinline__ bf16x8 operator()(int s, int tt) const {
+        return *(const bf16x8 *)(row + tt * 16 * XP + ws::xoff<FMT>(s, kg));
+    }
+};
+
+template <int FMT, int EPI, int MT, int GPW>
+__global__ __launch_bounds__(128 * GPW, 1) void wk_kernel(const uint16_t *__restrict__ A, int M, int64_t lda,
+                                                          GemmWeight w, Plan p, EpiParams ep) {
+    constexpr int NWV = 2 * GPW, NT = 64 * NWV, TOK = 16 * MT;
+    constexpr int PIECES = TOK * (SKC / 8);  // 16 B pieces of a sub-chunk
+    constexpr int NP = (PIECES + NT - 1) / NT;
+    // weight tiles in flight per wave (Q8_0 tiles take 20 registers: two at
+    // 64 tokens with three waves per SIMD)
+    constexpr int R = FMT == WF_Q4_K ? 4 : (FMT == WF_Q8_0 && MT == 4 && GPW == 6) ? 2 : 3;
+    static_assert(2 * TOK * XP >= NWV * TOK * 16 * 4, "the reduction reuses the x buffers");
+    using ws::Tile;
+    using ws::load_tile;
+    __shared__ __attribute__((aligned(16))) uint8_t xs[2 * TOK * XP];
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, kg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gs = wave >> 1, par = wave & 1;  // group slot, tile parity
+    const int64_t unit = (int64_t)blockIdx.x * p.UPW + gs / p.per_unit;
+    int64_t g;
+    if constexpr (EPI == EPI_SWIGLU) g = 8 * (unit >> 2) + (unit & 3) + 4 * (gs & 1);  // gate, then up
+    else g = unit;
+    const int64_t SB = w.k / 256;
+
+    // x sub-chunk j <-> registers <-> LDS buffer; rows past M repeat row M - 1
+    u32x4 xr[NP];
+    auto x_load = [&](int j) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int pc = tid + i * NT;
+            if (PIECES % NT == 0 || pc < PIECES) {
+                const int m = pc / (SKC / 8), s = pc % (SKC / 8);
+                xr[i] = *(const u32x4 *)(A + (int64_t)min(m, M - 1) * lda + (int64_t)j * SKC + 8 * s);
+            }
+        }
+    };
+    auto x_store = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int pc = tid + i * NT;
+            if (PIECES % NT == 0 || pc < PIECES) {
+                const int m = pc / (SKC / 8), s = pc % (SKC / 8);
+                *(u32x4 *)(xs + buf * TOK * XP + m * XP + 16 * s) = xr[i];
+            }
+        }
+    };
+
+    // the tile of sub-chunk j for this wave is super-block 2 j + par
+    Tile<FMT> ring[R];
+    x_load(0);
+    x_store(0);
+    x_load(1);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        load_tile(w, g, 2 * r + par, SB, l16, kg, ring[r]);
+        __builtin_amdgcn_sched_barrier(0);  // tiles issue in order: each wait covers one tile
+    }
+    __syncthreads();
+
+    f32x4 acc[MT];
+#pragma unroll
+    for (int tt = 0; tt < MT; tt++) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // straight-line over the sub-chunks (ring slots are compile-time indices)
+#pragma unroll
+    for (int j = 0; j < KS; j++) {
+        if (j + 1 < KS) x_store((j + 1) & 1);  // buffer of sub-chunk j - 1: freed by the last barrier
+        if (j + 2 < KS) x_load(j + 2);
+        const XSub<FMT> xt{xs + (j & 1) * TOK * XP + l16 * XP + 512 * par, kg};
+        Tile<FMT> &t = ring[j % R];
+        if constexpr (FMT == WF_Q4_K) ws::tile_q4d<MT>(t, xt, kg, acc);
+        else if constexpr (FMT == WF_Q6_K) ws::tile_q6<MT>(t, xt, kg, acc);
+        else ws::tile_q8<MT>(t, xt, kg, acc);
+        // finish this tile's arithmetic here, not past the loads
+#pragma unroll
+        for (int tt = 0; tt < MT; tt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) asm volatile("" : "+v"(acc[tt][e]));
+        if (j + R < KS) load_tile(w, g, 2 * (j + R) + par, SB, l16, kg, t);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();  // sub-chunk j + 1 written, sub-chunk j's buffer free
+    }
+
+    // the waves' sums meet in LDS (the x buffers, free after the last barrier):
+    // red[wave][token][row], lane holding tokens 16 tt + 4 kg + e of row l16
+    float *red = (float *)xs;
+#pragma unroll
+    for (int tt = 0; tt < MT; tt++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) red[(wave * TOK + 16 * tt + 4 * kg + e) * 16 + l16] = acc[tt][e];
+    __syncthreads();
+    auto gsum = [&](int slot, int tt) __attribute__((always_inline)) {  // even wave, then odd
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int m = 16 * tt + 4 * kg + e;
+            v[e] = red[((2 * slot) * TOK + m) * 16 + l16] + red[((2 * slot + 1) * TOK + m) * 16 + l16];
+        }
+        return v;
+    };
+    if (par == 0 && (EPI != EPI_SWIGLU || (gs & 1) == 0)) {
+#pragma unroll
+        for (int tt = 0; tt < MT; tt++) {
+            const f32x4 v = gsum(gs, tt);
+            if constexpr (EPI == EPI_SWIGLU) {
+                const f32x4 up = gsum(gs + 1, tt);
+                const int64_t blk = unit >> 2, q = unit & 3;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int m = 16 * tt + 4 * kg + e;
+                    if (m < M)
+                        ep.hmid[m * ep.ldh + 64 * blk + 16 * q + l16] =
+                            (uint16_t)(pack_bf16x2(silu(v[e]) * up[e], 0.f) & 0xffffu);
+                }
+            } else {
+                const int64_t n = g * 16 + l16;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int m = 16 * tt + 4 * kg + e;
+                    if (m < M) {
+                        if constexpr (EPI == EPI_F32) ((float *)ep.out)[m * ep.ldo + n] = v[e];
+                        else ((uint16_t *)ep.out)[m * ep.ldo + n] = (uint16_t)(pack_bf16x2(v[e], 0.f) & 0xffffu);
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int FMT, int MT, int GPW>
+hipError_t launch_g(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, int epi, const EpiParams &ep,
+                    const Plan &p, hipStream_t stream) {
+    const dim3 grid((unsigned)(w.n / 16 / GPW)), block(128 * GPW);
+    switch (epi) {
+    case EPI_F32: wk_kernel<FMT, EPI_F32, MT, GPW><<<grid, block, 0, stream>>>(a, m, lda, w, p, ep); break;
+    case EPI_BF16: wk_kernel<FMT, EPI_BF16, MT, GPW><<<grid, block, 0, stream>>>(a, m, lda, w, p, ep); break;
+    case EPI_SWIGLU: wk_kernel<FMT, EPI_SWIGLU, MT, GPW><<<grid, block, 0, stream>>>(a, m, lda, w, p, ep); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t launch(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, int epi, const EpiParams &ep,
+                  const Plan &p, hipStream_t stream) {
+    if (m <= 32) return p.GPW == 4 ? launch_g<FMT, 2, 4>(w, a, m, lda, epi, ep, p, stream)
+                                   : launch_g<FMT, 2, 6>(w, a, m, lda, epi, ep, p, stream);
+    return p.GPW == 4 ? launch_g<FMT, 4, 4>(w, a, m, lda, epi, ep, p, stream)
+                      : launch_g<FMT, 4, 6>(w, a, m, lda, epi, ep, p, stream);
+}
+
+}  // namespace wk
+
 // Sum of the split-K partials of C[m][n], in split order.
 __device__ __forceinline__ float csum(const float *part, int splits, int64_t MN, int64_t idx) {
     float v = 0.f;
@@ -1529,6 +1725,14 @@ hipError_t launch_qgemm_stream(const GemmWeight &w, const uint16_t *a, int64_t m
         case WF_Q4_K: return wx::launch<WF_Q4_K>(w, a, (int)m, lda, epi, ep, tpw, stream);
         case WF_Q6_K: return wx::launch<WF_Q6_K>(w, a, (int)m, lda, epi, ep, tpw, stream);
         default: return wx::launch<WF_Q8_0>(w, a, (int)m, lda, epi, ep, tpw, stream);
+        }
+    }
+    wk::Plan kp;
+    if (wk::plan(w, m, epi, cus, kp)) {
+        switch (w.fmt) {
+        case WF_Q4_K: return wk::launch<WF_Q4_K>(w, a, (int)m, lda, epi, ep, kp, stream);
+        case WF_Q6_K: return wk::launch<WF_Q6_K>(w, a, (int)m, lda, epi, ep, kp, stream);
+        default: return wk::launch<WF_Q8_0>(w, a, (int)m, lda, epi, ep, kp, stream);
         }
     }
     ws::Plan wp;

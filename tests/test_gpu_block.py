@@ -19,7 +19,7 @@ import pytest
 import oracle as O
 import qimm
 import synth
-from gpu_util import cos_sim, dev, host, max_abs_rel, stream
+from gpu_util import check_block, cos_sim, dev, host, max_abs_rel, stream
 
 pytestmark = pytest.mark.gpu
 
@@ -151,21 +151,28 @@ def test_block_config1_shape(torch_cuda, qctx):
 
 
 @pytest.mark.parametrize("b,s,p,mlp", [(1, 8, 16, 512), (2, 6, 0, 1024), (2, 8, 8, 1024), (1, 16, 0, 2048),
-                                       (2, 20, 8, 1024), (1, 64, 16, 1024)])
+                                       (2, 20, 8, 1024), (1, 64, 16, 1024),
+                                       # MLP 12288: gate_up (24576 x 4096) keeps six groups per CU over the
+                                       # whole K (SwiGLU epilogue at 40 and at 2 x 12 tokens)
+                                       (1, 40, 16, 12288), (2, 12, 8, 12288)])
 def test_block_hidden4096_short_m(torch_cuda, qctx, b, s, p, mlp):
     """Hidden 4096 (32 heads) at M <= 64 tokens: the fused QKV (12288 x 4096),
     output (4096 x 4096) and gate_up (2 mlp x 4096) projections and, for
     mlp % 1024 == 0, the Q6_K down projection take the one-launch kernel with
     its q/k/v (RmsNorm + RoPE + layouts, batch boundaries inside the token
     tile), residual and SwiGLU epilogues; mlp 512 sends the down projection to
-    the split-K dequantizing kernel. Short MLPs keep the oracle quick."""
+    the split-K dequantizing kernel. Short MLPs keep the oracle quick; the
+    model's MLP 12288 runs at 40 and 24 tokens."""
     cfg = dict(hidden=4096, heads=32, head_dim=128, mlp=mlp)
     w, x, mod, pe, kpre, vpre = make_case(21 + b + s, cfg, b, s, p, synth.Q4_K, synth.Q6_K)
     got, (k, v) = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)
     ref, kr, vr = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
-    check(got, ref, x)
     ref_e, kre, vre = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
-    check(got, ref_e, x, exact=True)
+    if mlp == 12288:  # the candle path's own int8 SwiGLU hidden state: bars relative to it
+        check_block(*(a.reshape(b * s, -1) for a in (got, ref, ref_e, x)))
+    else:
+        check(got, ref, x)
+        check(got, ref_e, x, exact=True)
     for kk, vv in ((kr, vr), (kre, vre)):
         assert cos_sim(k, kk) >= 0.9999 and max_abs_rel(k, kk) <= 2e-2
         assert cos_sim(v, vv) >= 0.9999 and max_abs_rel(v, vv) <= 2e-2

@@ -34,7 +34,7 @@ import pytest
 
 import oracle as O
 import synth
-from gpu_util import bf16_dev, cos_sim, max_abs_rel, host, stream
+from gpu_util import bf16_dev, check_block, cos_sim, max_abs_rel, host, stream
 from test_gpu_block import make_case, run_block
 from test_gpu_kernels import _attention_case
 
@@ -49,19 +49,6 @@ def sampled_rows(rng, m, tile=256, extra=48):
     rows = np.concatenate([np.arange(0, 4), seams - 1, seams, rng.choice(m, extra, replace=False),
                            np.arange(m - 4, m)])
     return np.unique(rows)
-
-
-def check_block(got, cand, exact, x):
-    """got, cand, exact: the same token rows [R, hidden]; x: their inputs."""
-    c_ge, c_ce = cos_sim(got, exact), cos_sim(cand, exact)
-    u_ge, u_ce = cos_sim(got - x, exact - x), cos_sim(cand - x, exact - x)
-    c_gc = cos_sim(got, cand)
-    print(f"cos(gpu, exact) {c_ge:.7f} update {u_ge:.7f}; cos(candle, exact) {c_ce:.7f} update {u_ce:.7f}; "
-          f"cos(gpu, candle) {c_gc:.7f}; mar gpu-exact {max_abs_rel(got, exact):.2e} "
-          f"gpu-candle {max_abs_rel(got, cand):.2e}", flush=True)
-    assert c_ge >= 0.9999 and u_ge >= 0.9999 and max_abs_rel(got, exact) <= 2e-2
-    assert c_ge >= c_ce and u_ge >= u_ce        # closer to exact arithmetic than the candle path
-    assert c_gc >= min(0.9999, c_ce - 2e-5) and max_abs_rel(got, cand) <= 2e-2
 
 
 def kv_close(got, want):

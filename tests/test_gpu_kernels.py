@@ -165,6 +165,36 @@ def test_qmatmul_short_m_one_launch_repeats(torch_cuda, qctx):
         assert np.all(np.abs(got - want) <= 2e-5 * scale + 4e-3 * np.abs(want) + 1e-6), cases[key]
 
 
+@pytest.mark.parametrize("t,m,n,out", [(synth.Q4_K, 64, 24576, synth.BF16), (synth.Q4_K, 20, 16384, synth.F32),
+                                       (synth.Q6_K, 33, 16384, synth.BF16), (synth.Q8_0, 64, 16384, synth.BF16),
+                                       (synth.Q8_0, 50, 24576, synth.F32), (synth.Q6_K, 17, 24576, synth.F32)])
+def test_qmatmul_short_m_whole_k_per_workgroup(torch_cuda, qctx, t, m, n, out):
+    """17-64 tokens at K = 4096 with 4 or 6 groups of 16 weight rows per CU
+    (N 16384 or 24576 on 256 CUs): each workgroup keeps its groups over the
+    whole K, x passing through LDS in 512-wide pieces, and two waves per group
+    add their sums in a fixed order. Against the f64 product of the bf16
+    activations and the bf16-rounded weights; a second call is bit-identical."""
+    torch = torch_cuda
+    k = 4096
+    rng = np.random.default_rng(m + n)
+    _, w, _, _ = synth.weight(rng, t, n, k)
+    W = qctx.upload(t, n, k, w.tobytes())
+    a_dev, a = bf16_dev(torch, rng.standard_normal((m, k)).astype(np.float32))
+    dt = torch.bfloat16 if out == synth.BF16 else torch.float32
+    got = []
+    for _ in range(2):
+        y = torch.empty((m, n), dtype=dt, device="cuda")
+        qctx.qmatmul(W, a_dev.data_ptr(), m, k, y.data_ptr(), out, stream(torch))
+        got.append(host(y.float()))
+    W.free()
+    assert np.array_equal(got[0], got[1])
+    Wd = O.bf16_round(O.dequantize(t, w, n * k).reshape(n, k)).astype(np.float64)
+    want = a.astype(np.float64) @ Wd.T
+    scale = np.abs(a).astype(np.float64) @ np.abs(Wd).T
+    tol = 2e-5 * scale + 1e-6 + (4e-3 * np.abs(want) if out == synth.BF16 else 0)
+    assert np.all(np.abs(got[0] - want) <= tol), np.max(np.abs(got[0] - want) / (scale + 1e-9))
+
+
 @pytest.mark.parametrize("m", [64, 700])
 def test_qmatmul_bf16_output(torch_cuda, qctx, m):
     got, a, w = _gemm_case(torch_cuda, qctx, synth.Q4_K, m, 256, 512, seed=5, out_type=synth.BF16)

@@ -251,8 +251,26 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
             __builtin_amdgcn_global_load_lds((const void *)(asrc[i] + k0), (lds_ptr_t)(base + (8 * wave + i) * 8 * ROWB),
                                              16, 0, 0);
     };
-    // W staging: row n0 + tid, all 8 chunks, through registers (dequantized);
-    // raw weights double-buffered two steps ahead
+    // bf16 weights (a dequantized copy, [N][K]) take the A path: direct
+    // global->LDS loads into the B rows of the stage, same swizzle
+    const uint16_t *bsrc[8];
+    if constexpr (FMT == WF_BF16) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int row = 8 * (8 * wave + i) + (lane >> 3);
+            const int c = (lane & 7) ^ swz_key(row);
+            bsrc[i] = (const uint16_t *)w.q + (n0 + row) * K + 8 * c;
+        }
+    }
+    auto dma_b = [&](int stage, int64_t k0) {
+        uint8_t *base = lds + stage * STAGE + 256 * ROWB;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(bsrc[i] + k0), (lds_ptr_t)(base + (8 * wave + i) * 8 * ROWB),
+                                             16, 0, 0);
+    };
+    // W staging (quantized): row n0 + tid, all 8 chunks, through registers
+    // (dequantized); raw weights double-buffered two steps ahead
     const int64_t wrow = n0 + tid;
     WRaw rw[2];
 
@@ -283,6 +301,38 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
         }
     };
 
+    if constexpr (FMT == WF_BF16) {
+        // both operands of steps 0 and 1 in flight, then the same one-barrier
+        // step as below without the dequantization
+        dma_a(0, 0);
+        dma_b(0, 0);
+        dma_a(1, (int64_t)min(1, KT - 1) * BK);
+        dma_b(1, (int64_t)min(1, KT - 1) * BK);
+        __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);  // vmcnt(0) lgkmcnt(0)
+        __syncthreads();
+        rd(0, 0, 0);
+        auto step_b = [&](int kt, auto sc_) __attribute__((always_inline)) {
+            constexpr int s = decltype(sc_)::value, t = s ^ 1;
+            rd(1, s, 1);
+            mm(0);
+            rd(0, s, 2);
+            mm(1);
+            rd(1, s, 3);
+            mm(0);
+            __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);  // stage t's loads (issued a step ago) landed
+            __syncthreads();
+            dma_a(s, (int64_t)min(kt + 2, KT - 1) * BK);
+            dma_b(s, (int64_t)min(kt + 2, KT - 1) * BK);
+            rd(0, t, 0);
+            mm(1);
+        };
+        int kt = 0;
+        for (; kt + 1 < KT; kt += 2) {
+            step_b(kt, std::integral_constant<int, 0>{});
+            step_b(kt + 1, std::integral_constant<int, 1>{});
+        }
+        if (kt < KT) step_b(kt, std::integral_constant<int, 0>{});
+    } else {
     // prologue: step 0 staged in stage 0; raw weights of steps 1 and 2 and the
     // A tile of step 1 loaded (step indices clamped to the last step: redundant
     // loads, no branches)
@@ -341,6 +391,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
         step(kt + 1, std::integral_constant<int, 1>{});
     }
     if (kt < KT) step(kt, std::integral_constant<int, 0>{});
+    }
     __builtin_amdgcn_s_waitcnt(WAIT_VM0);  // vmcnt(0): no load into LDS still in flight
 
     // ---- epilogue, straight from the accumulators ----

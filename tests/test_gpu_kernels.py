@@ -75,7 +75,10 @@ def _gemm_case(torch, qctx, t, m, n, k, seed, out_type=synth.F32, std=0.02):
                                    # chunk, a partial 16-token tile, chunks longer than six stages)
                                    (16, 384, 4096), (33, 256, 1024), (64, 128, 8192),
                                    (130, 384, 1024), (300, 128, 4096),
-                                   (600, 512, 1024), (1024, 256, 768)])   # the last two: 256x256 kernel
+                                   (600, 512, 1024), (1024, 256, 768),
+                                   # 256x256 kernel (more 128x128 tiles than two per CU); bf16
+                                   # weights there take the direct global->LDS operand path
+                                   (2304, 4096, 256)])
 def test_qmatmul_matches_bf16_weight_products(torch_cuda, qctx, t, m, n, k):
     """Products of the bf16 activations and the weights each path multiplies:
     bf16-rounded dequantized weights on the MFMA dequant paths, the exact Q4_K

@@ -176,7 +176,7 @@ def main():
     streaming = None if args.no_weight_streaming else weight_streaming(ctx, torch, np, qimm, synth, stream, host_w0)
 
     # ---- the other measured configurations: Q8_0 dequant-GEMM sets, multi-reference attention ----
-    q8 = mref = mlp16k = pfill = cfg1 = sdpa = None
+    q8 = mref = mlp16k = pfill = cfg1 = sdpa = gemm_bar = None
     if not args.no_other_configs:
         q8 = q8_gemm_sets(ctx, torch, np, qimm, synth, stream)
         mref = multi_ref_attention(ctx, torch, qimm, stream)
@@ -184,6 +184,7 @@ def main():
         pfill = prefix_fill_8448(ctx, torch, np, qimm, synth, stream)
         cfg1 = config1_block(ctx, torch, np, qimm, synth, stream, cpu=not args.no_cpu_baseline)
         sdpa = torch_sdpa_bar(torch, stream)
+        gemm_bar = torch_gemm_bar(torch, stream)
 
     # ---- CPU baseline: the oracle in candle mode on a bounded sample ----
     cpu = None
@@ -225,6 +226,7 @@ def main():
         "prefix_fill_8448": pfill,
         "config1_block": cfg1,
         "attention_torch_sdpa": sdpa,
+        "gemm_torch_bf16": gemm_bar,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
@@ -584,6 +586,24 @@ def torch_sdpa_bar(torch, stream, iters=20):
     except Exception as e:  # no fused backend: report why, measure nothing
         log(f"bench: torch SDPA bar unavailable: {e}")
         return {"error": str(e)[:200]}
+
+
+def torch_gemm_bar(torch, stream, iters=10):
+    """torch's plain bf16 GEMM (hipBLASLt) at the block's four projection shapes
+    with 4096 token rows, y = x W^T with W already bf16 (no dequantization, no
+    fused epilogue): the practical bar for the dequant-GEMMs on this GPU."""
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(4)
+    for name, (n, k) in (("qkv", (3 * HID, HID)), ("out", (HID, HID)), ("gate_up", (2 * MLP, HID)),
+                         ("down", (HID, MLP))):
+        x = torch.randn((S_IMG, k), generator=g, device="cuda").to(torch.bfloat16)
+        w = torch.randn((n, k), generator=g, device="cuda").to(torch.bfloat16)
+        with torch.cuda.stream(stream):
+            ms = timed(torch, stream, lambda: torch.mm(x, w.t()), iters)
+        tflops = 2.0 * S_IMG * n * k / ms / 1e9
+        out[name] = {"ms": round(ms, 4), "tflops": round(tflops, 1), "frac_bf16_peak": round(tflops / PEAK_BF16_TFLOPS, 4)}
+        log(f"bench: torch bf16 GEMM {S_IMG}x{n}x{k}: {ms:.3f} ms, {tflops:.0f} TFLOP/s")
+    return out
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_block_q4km_1024.json")

@@ -292,6 +292,13 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
         for (int i = 0; i < 4; i++) fa[buf][i] = *(const bf16x8 *)(as + swz(wm * 128 + i * 32 + l32, 2 * kk + g));
 #pragma unroll
         for (int j = 0; j < 4; j++) fb[buf][j] = *(const bf16x8 *)(bs + swz(wn * 128 + j * 32 + l32, 2 * kk + g));
+        // bf16 weights: the reads stay ahead of the MFMAs that follow (those
+        // use the other buffer); left alone, the scheduler sinks each read to
+        // just before its first use and waits out the LDS latency there (q/k/v
+        // shape 441-458 -> 416-424 us). The dequantizing forms keep the
+        // scheduler's order: their decode VALU already fills that latency, and
+        // Q6_K measured 507 -> 585 us with the reads pinned.
+        if constexpr (FMT == WF_BF16) __builtin_amdgcn_sched_barrier(0);
     };
     auto mm = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll

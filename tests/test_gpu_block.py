@@ -204,6 +204,24 @@ def test_block_hidden4096_large_m(torch_cuda, qctx, b, s, p, mlp, attn_type, dow
         assert cos_sim(v, vv) >= 0.9999 and max_abs_rel(v, vv) <= 2e-2
 
 
+def test_block_hidden4096_large_m_bf16_weights(torch_cuda, qctx):
+    """Float-stored (bf16) weights at 2820 tokens, hidden 4096, MLP 4096: the
+    large-M GEMM's bf16 form, whose weight tile goes global -> LDS by direct
+    loads like the activations, under its fused q/k/v, residual and SwiGLU
+    epilogues (12 tile rows, a 4-row last one). Candle multiplies float-stored
+    weights in plain f32 (no int8 activations), so exact mode alone is the
+    reference here."""
+    cfg = dict(hidden=4096, heads=32, head_dim=128, mlp=4096)
+    b, s, p = 1, 2820, 0
+    w, x, mod, pe, kpre, vpre = make_case(67, cfg, b, s, p, synth.BF16, synth.BF16)
+    got, (k, v) = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)
+    ref_e, kre, vre = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
+    check(got, ref_e, x)
+    check(got, ref_e, x, exact=True)
+    assert cos_sim(k, kre) >= 0.9999 and max_abs_rel(k, kre) <= 2e-2
+    assert cos_sim(v, vre) >= 0.9999 and max_abs_rel(v, vre) <= 2e-2
+
+
 @pytest.mark.parametrize("attn_type,down_type", [(synth.Q8_0, synth.Q8_0), (synth.Q4_K, synth.Q6_K)])
 def test_block_mid_m_split_k(torch_cuda, qctx, attn_type, down_type):
     """Hidden 1024 (8 heads), MLP 2048, 128 tokens over a 16-token prefix: every

@@ -5,7 +5,8 @@ the second with fewer tokens, and interleaves calls of the allocating entry
 point; the paths that use the scratch are all covered: the one-launch short-M
 kernel (arrival counters + partial sums), the split 128x128 kernel (partials
 + the ordered reduction) and a large-M product whose last tile row goes to
-the split path."""
+the split path; the short-M kernels that keep their K sums inside a workgroup
+run there too (no scratch)."""
 import numpy as np
 import pytest
 
@@ -17,7 +18,9 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("t,m,m2,n,k,out", [
-    (synth.Q4_K, 64, 16, 24576, 4096, synth.BF16),   # gate_up at 64 then 16 tokens: one launch, 25 MB of partials
+    (synth.Q4_K, 64, 16, 24576, 4096, synth.BF16),   # gate_up at 64 then 16 tokens: whole K per workgroup,
+                                                     # then the in-workgroup K reduction (no partials)
+    (synth.Q8_0, 64, 33, 12288, 4096, synth.BF16),   # q/k/v shape: one launch, split-K partials and counters
     (synth.Q6_K, 40, 5, 4096, 12288, synth.F32),     # down: twelve k chunks
     (synth.Q8_0, 256, 130, 4096, 4096, synth.BF16),  # split 128x128 (8 and 4 shares)
     (synth.Q4_K, 4352, 4136, 4096, 4096, synth.F32),  # large M: tail rows to the split / short-M paths

@@ -190,6 +190,21 @@ int qimm_qk_norm_rope(qimm_ctx *ctx, const float *x, int64_t batch, int64_t seq,
 int qimm_v_transpose(qimm_ctx *ctx, const float *x, int64_t batch, int64_t seq,
                      int64_t heads, uint16_t *vt_out, void *stream);
 
+/* The activation rounding of QMatMul::forward (src/quantized_transformer.rs:19-29:
+ * candle's CPU QMatMul quantizes its f32 input rows to the weight's vec-dot
+ * type, candle-core 0.11 BlockQ8_0 / BlockQ8K::from_float): rows x[m][0:k] f32
+ * (row stride ldx) to out[m][0:k] bf16 (row stride ldo) = bf16(d * q), the
+ * quantized value rounded once to nearest even, in blocks of 32 values (Q8_0
+ * weights: d = f16(amax/127), q = round(x * (1/(amax/127)))) or 256 (Q4_K /
+ * Q6_K weights, Q8_K: iscale = -128/x_max with x_max the first value of largest
+ * magnitude, q = min(127, round(iscale * x)), d = 1/iscale); round() is half
+ * away from zero. Feeding out to qimm_qmatmul reproduces QMatMul::forward's
+ * rounding. weight_type: Q8_0, Q4_K or Q6_K (QIMM_ERR_TYPE otherwise); k a
+ * multiple of the block, ldx and ldo >= k and multiples of 4, x and out 16-byte
+ * aligned (device pointers). */
+int qimm_quantize_act(qimm_ctx *ctx, int weight_type, const float *x, int64_t m, int64_t k,
+                      int64_t ldx, uint16_t *out, int64_t ldo, void *stream);
+
 /* Unmasked joint attention of queries q [B,H,Sq,128] over keys
  * [prefix layer of kv ; own] with own keys k_own [B,H,So,128] and own values
  * transposed vt_own [B,H,128,So] (bf16, device). kv may be NULL (no prefix).
@@ -253,6 +268,26 @@ int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t ba
                        int64_t seq, const float *mod, const float *pe, const qimm_kv *kv,
                        int64_t layer, uint16_t *k_out, uint16_t *v_out, void *stream);
 
+/* Arithmetic at the inputs of the block's quantized matmuls (q/k/v, to_out,
+ * gate_up, down: Linear::forward, src/quantized_transformer.rs:19-29, called at
+ * 133-135, 151, 196-202).
+ *  QIMM_ACT_CANDLE, the default: each f32 input row is rounded as candle's CPU
+ *    QMatMul::forward rounds it before its integer dot products (candle-core
+ *    0.11 quantized/k_quants.rs, the weight's vec-dot type): to Q8_K per 256
+ *    values (scale -128 / the first value of largest magnitude) for Q4_K and
+ *    Q6_K weights, to Q8_0 per 32 values (scale amax/127 kept as f16) for Q8_0
+ *    weights; float-stored weights take the values unrounded, as candle's plain
+ *    matmul does. The MFMA operand is the quantized value d*q rounded once to
+ *    bf16 (qimm_quantize_act), so the block follows the reference CPU path's
+ *    rounding.
+ *  QIMM_ACT_BF16: the f32 values rounded to bf16, no int8 step: closer to exact
+ *    arithmetic than the reference, and slightly faster (no f32 staging of the
+ *    attention output and the SwiGLU hidden state). */
+#define QIMM_ACT_CANDLE 0
+#define QIMM_ACT_BF16 1
+int qimm_block_set_act_mode(qimm_block *blk, int mode);
+int qimm_block_act_mode(const qimm_block *blk);
+
 /* Sizes the context's device scratch for forwards of this block with up to
  * batch x seq tokens and mod_rows modulation rows (1 or seq). A forward that
  * needs more than the scratch holds grows it, which synchronizes the device
@@ -305,10 +340,13 @@ int qimm_attention_masked(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64
  * qimm_block_stage_times waits for the last forward and writes the durations
  * in ms of its QIMM_BLOCK_STAGES stages:
  *   0 modulation prep + norm1   1 q/k/v projection + norm + RoPE
- *   2 attention                 3 output projection + gated residual
- *   4 norm2                     5 gate_up projection + SwiGLU
- *   6 down projection + gated residual */
-#define QIMM_BLOCK_STAGES 7
+ *   2 attention                 3 rounding of the attention output (candle mode)
+ *   4 output projection + gated residual
+ *   5 norm2                     6 gate_up projection + SwiGLU
+ *   7 rounding of the SwiGLU hidden state (candle mode)
+ *   8 down projection + gated residual
+ * Stages 3 and 7 are empty under QIMM_ACT_BF16. */
+#define QIMM_BLOCK_STAGES 9
 int qimm_block_profile(qimm_block *blk, int enable);
 int qimm_block_stage_times(qimm_block *blk, float *ms_out, int n);
 

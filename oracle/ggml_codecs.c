@@ -359,6 +359,51 @@ static void dequant_q8_k(const blk_q8_k *x, int64_t n, float *y) {
         for (int i = 0; i < QK_K; i++) y[b * QK_K + i] = x[b].d * (float)x[b].qs[i];
 }
 
+/* bf16 (round to nearest even) of a double, rounded once: frexp gives
+ * v = f * 2^e with |f| in [0.5, 1); rint of f * 2^8 (the current rounding mode,
+ * nearest even) keeps bf16's 8 significant bits. Values below the bf16
+ * normal range round on its subnormal grid (spacing 2^-133). */
+static uint16_t f64_to_bf16(double v) {
+    if (v == 0.0) return 0u; /* a zero code: +0 whatever the scale's sign (the codes are integers) */
+    double r;
+    if (fabs(v) < 0x1p-126) {
+        r = ldexp(rint(ldexp(v, 133)), -133);
+    } else {
+        int e;
+        const double f = frexp(v, &e);
+        r = ldexp(rint(f * 256.0), e - 8);
+    }
+    return oq_f32_to_bf16((float)r); /* r has <= 8 significant bits: exact in f32 and bf16 */
+}
+
+/* The bf16 MFMA operands of candle's activation rounding (QMatMul::forward,
+ * src/quantized_transformer.rs:19-29 -> candle-core 0.11 BlockQ8_0 /
+ * BlockQ8K::from_float): each row of k values quantized to the vec-dot type of
+ * a wtype weight (Q8_0: 32-value blocks with an f16 scale; Q4_K / Q6_K: Q8_K
+ * 256-value blocks with an f32 scale), then out = bf16(d * q) with d * q exact
+ * in double and rounded once. */
+int oq_quant_act_bf16(int wtype, const float *x, int64_t m, int64_t k, uint16_t *out) {
+    const int kb = wtype == OQ_Q8_0 ? QK8_0 : (wtype == OQ_Q4_K || wtype == OQ_Q6_K) ? QK_K : 0;
+    if (!kb || k % kb || m < 0) return -1;
+    for (int64_t r = 0; r < m; r++) {
+        const float *xr = x + r * k;
+        uint16_t *o = out + r * k;
+        for (int64_t b = 0; b < k / kb; b++) {
+            if (kb == QK8_0) {
+                blk_q8_0 y;
+                quant_q8_0(xr + b * kb, kb, &y);
+                const double d = oq_f16_to_f32(y.d);
+                for (int i = 0; i < kb; i++) o[b * kb + i] = f64_to_bf16(d * y.qs[i]);
+            } else {
+                blk_q8_k y;
+                quant_q8_k(xr + b * kb, kb, &y);
+                for (int i = 0; i < kb; i++) o[b * kb + i] = f64_to_bf16((double)y.d * y.qs[i]);
+            }
+        }
+    }
+    return 0;
+}
+
 int oq_quantize(int type, const float *x, int64_t n, void *out) {
     int bs = oq_block_size(type);
     if (!bs || n % bs) return -1;

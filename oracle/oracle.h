@@ -55,6 +55,9 @@ int oq_block_bytes(int type);         /* bytes per block, 0 if unknown */
 int64_t oq_row_bytes(int type, int64_t n);
 /* x has n values (n a multiple of the block size). Returns 0 on success. */
 int oq_quantize(int type, const float *x, int64_t n, void *out);
+/* candle's activation rounding of m rows of k values for a wtype weight, as
+ * bf16 operands bf16(d * q) (rounded once from the exact product). */
+int oq_quant_act_bf16(int wtype, const float *x, int64_t m, int64_t k, uint16_t *out);
 int oq_dequantize(int type, const void *in, int64_t n, float *out);
 
 /* ---- quantized matmul: y[M,N] = x[M,K] * W[N,K]^T ---- */

@@ -42,6 +42,7 @@ def lib():
             "oq_block_bytes": (i32, [i32]),
             "oq_row_bytes": (i64, [i32, i64]),
             "oq_quantize": (i32, [i32, vp, i64, vp]),
+            "oq_quant_act_bf16": (i32, [i32, vp, i64, i64, vp]),
             "oq_dequantize": (i32, [i32, vp, i64, vp]),
             "oq_qmatmul": (i32, [i32, vp, i64, i64, vp, i64, vp, i32]),
             "oq_layernorm_mod": (None, [vp, i64, i64, vp, i64, i64, C.c_float, vp]),
@@ -116,6 +117,17 @@ def dequantize(t, data, n):
     out = np.empty(n, dtype=np.float32)
     rc = lib().oq_dequantize(t, _p(data), n, _p(out))
     assert rc == 0
+    return out
+
+
+def quant_act_bf16(wtype, x):
+    """candle's activation rounding of the rows of x [..., K] for a wtype weight
+    (Q8_0 / Q4_K / Q6_K), as the bf16 bits of d * q (uint16, same shape)."""
+    x = _c(x, np.float32)
+    k = x.shape[-1]
+    out = np.empty(x.shape, dtype=np.uint16)
+    rc = lib().oq_quant_act_bf16(wtype, _p(x), x.size // k, k, _p(out))
+    assert rc == 0, rc
     return out
 
 

@@ -168,11 +168,19 @@ int qimm_block_destroy(qimm_block *blk) {
 namespace {
 
 // Workspace of one forward: modp [B*mod_rows,4h] f32 | xn [M,h] | q | k | vt |
-// attn [M,h] | hmid [M,F] (bf16), and the split-K scratch of the short- and
-// mid-M GEMM paths, sized for the largest projection.
+// attn [M,h] | hmid [M,F] (bf16) | lim | f32 staging of the attention output
+// [M,h] and then of the SwiGLU hidden state [M,F] ahead of their activation
+// rounding (candle mode only), and the split-K scratch of the short- and mid-M
+// GEMM paths, sized for the largest projection.
 struct WsLayout {
-    size_t modp, xn, q, k, vt, att, h, lim, total, part;
+    size_t modp, xn, q, k, vt, att, h, lim, f32, total, part;
 };
+
+// The activation block of candle's vec-dot type for weight w under the
+// block's mode (0: bf16 operands, no int8 rounding).
+int act_qblk(const qimm_block *blk, const qimm_weight *w) {
+    return blk->act == QIMM_ACT_CANDLE ? qimm::act_block(w->gw.fmt) : 0;
+}
 
 WsLayout ws_layout(const qimm_block *blk, int64_t batch, int64_t seq, int64_t mod_rows) {
     const int64_t hid = blk->cfg.hidden, F = blk->cfg.mlp, M = batch * seq;
@@ -186,6 +194,9 @@ WsLayout ws_layout(const qimm_block *blk, int64_t batch, int64_t seq, int64_t mo
     L.att = off; off += align_up((size_t)(M * hid) * 2);
     L.h = off; off += align_up((size_t)(M * F) * 2);
     L.lim = off; off += align_up((size_t)seq * 4);  // per-query key limits of the block-causal mask
+    L.f32 = off;
+    if (act_qblk(blk, blk->out) || act_qblk(blk, blk->down))
+        off += align_up((size_t)(M * std::max(hid, F)) * 4);
     L.total = off;
     L.part = 0;
     const qimm_weight *ws_list[] = {blk->qkv, blk->q, blk->k, blk->v, blk->out, blk->gate_up, blk->down};
@@ -249,7 +260,11 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
     const int64_t rows_per = seq / mod_rows;  // tokens sharing one modulation row
     QIMM_HIP(ctx, qimm::launch_mod_prep(mod, batch * mod_rows, hid, modp, s));
     // norm1(x) * (1 + scale1)                                  (:267-269)
-    QIMM_HIP(ctx, qimm::launch_ln_mod(x, M, hid, modp, 4 * hid, rows_per, xn, s));
+    // In candle mode the output is already the q/k/v matmuls' quantized input
+    // (Linear::forward -> QMatMul::forward rounds its f32 input rows, :19-29).
+    const qimm_weight *qkv0 = blk->qkv_fused ? blk->qkv : blk->q;
+    int qb_norm1 = act_qblk(blk, qkv0);
+    QIMM_HIP(ctx, qimm::launch_ln_mod(x, M, hid, modp, 4 * hid, rows_per, xn, s, qb_norm1));
     STAGE_MARK(1);
     // to_q/to_k/to_v + per-head RmsNorm + RoPE                 (:133-142)
     qimm::EpiParams ep{};
@@ -276,6 +291,12 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
         const qimm_weight *parts[3] = {blk->q, blk->k, blk->v};
         for (int i = 0; i < 3; i++) {
             ep.n_offset = i * hid;
+            // q, k, v of different vec-dot types round the same norm1 output
+            // to their own blocks: norm1 again, in place of xn (stream order)
+            if (const int qb = act_qblk(blk, parts[i]); qb != qb_norm1) {
+                QIMM_HIP(ctx, qimm::launch_ln_mod(x, M, hid, modp, 4 * hid, rows_per, xn, s, qb));
+                qb_norm1 = qb;
+            }
             QIMM_HIP(ctx, qimm::launch_qgemm(parts[i]->gw, xn, M, hid, qimm::EPI_QKV, ep, s));
         }
     }
@@ -286,17 +307,22 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
         const int rc = kv_layer(kv, layer, s, &pk, &pvt);
         if (rc) return rc;
     }
+    // candle mode: the attention output leaves in f32 for to_out's activation rounding
+    const int qb_out = act_qblk(blk, blk->out);
+    float *stage_f32 = (float *)(ws + L.f32);
+    float *att_f32 = qb_out ? stage_f32 : nullptr;
     if (img || kvalid)
         QIMM_HIP(ctx, qimm::launch_attention_masked(qb, pk, pvt, P, kb, vt, seq, batch, H, seq, 1.0f, img, kvalid,
-                                                    (int32_t *)(ws + L.lim),
-                                                    att, s));
+                                                    (int32_t *)(ws + L.lim), att, s, att_f32));
     else
-        QIMM_HIP(ctx, qimm::launch_attention_log2(qb, pk, pvt, P, kb, vt, seq, batch, H, seq, att, s));
+        QIMM_HIP(ctx, qimm::launch_attention_log2(qb, pk, pvt, P, kb, vt, seq, batch, H, seq, att, s, att_f32));
     if (kv) {
         const int rc = kv_release(kv, layer, s);
         if (rc) return rc;
     }
     STAGE_MARK(3);
+    if (qb_out) QIMM_HIP(ctx, qimm::launch_quant_rows(att_f32, hid, M, hid, qb_out, att, hid, s));
+    STAGE_MARK(4);
     // x1 = x + tanh(gate1) * to_out(attn)                       (:150-151, 271-273)
     qimm::EpiParams er{};
     er.part_ws = part_ws;
@@ -307,18 +333,24 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
     er.g_stride = 4 * hid;
     er.g_rows_per = rows_per;
     QIMM_HIP(ctx, qimm::launch_qgemm(blk->out->gw, att, M, hid, qimm::EPI_RESID, er, s));
-    STAGE_MARK(4);
-    // norm2(x1) * (1 + scale2)                                 (:276-278)
-    QIMM_HIP(ctx, qimm::launch_ln_mod(x_out, M, hid, modp + 2 * hid, 4 * hid, rows_per, xn, s));
     STAGE_MARK(5);
+    // norm2(x1) * (1 + scale2)                                 (:276-278)
+    QIMM_HIP(ctx, qimm::launch_ln_mod(x_out, M, hid, modp + 2 * hid, 4 * hid, rows_per, xn, s,
+                                      act_qblk(blk, blk->gate_up)));
+    STAGE_MARK(6);
     // silu(gate) * up                                          (:191-201)
     qimm::EpiParams eg{};
     eg.part_ws = part_ws;
     eg.part_ws_bytes = part_bytes;
     eg.hmid = hm;
     eg.ldh = F;
+    // candle mode: the hidden state leaves in f32 for the down matmul's rounding
+    const int qb_down = act_qblk(blk, blk->down);
+    if (qb_down) eg.hmid_f32 = stage_f32;
     QIMM_HIP(ctx, qimm::launch_qgemm(blk->gate_up->gw, xn, M, hid, qimm::EPI_SWIGLU, eg, s));
-    STAGE_MARK(6);
+    STAGE_MARK(7);
+    if (qb_down) QIMM_HIP(ctx, qimm::launch_quant_rows(stage_f32, F, M, F, qb_down, hm, F, s));
+    STAGE_MARK(8);
     // x2 = x1 + tanh(gate2) * out(hidden)                       (:202, 280-282)
     qimm::EpiParams ed{};
     ed.part_ws = part_ws;
@@ -329,7 +361,7 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
     ed.g_stride = 4 * hid;
     ed.g_rows_per = rows_per;
     QIMM_HIP(ctx, qimm::launch_qgemm(blk->down->gw, hm, M, F, qimm::EPI_RESID, ed, s));
-    STAGE_MARK(7);
+    STAGE_MARK(9);
 #undef STAGE_MARK
     if (blk->profiling) blk->profiled_once = true;
     return QIMM_OK;
@@ -350,6 +382,16 @@ int qimm_block_reserve(qimm_block *blk, int64_t batch, int64_t seq, int64_t mod_
     if (rc) return rc;
     return L.part ? ensure_part_workspace(ctx, L.part) : QIMM_OK;
 }
+
+int qimm_block_set_act_mode(qimm_block *blk, int mode) {
+    if (!blk) return QIMM_ERR_ARG;
+    if (mode != QIMM_ACT_CANDLE && mode != QIMM_ACT_BF16)
+        return set_err(blk->ctx, QIMM_ERR_ARG, "block act mode: QIMM_ACT_CANDLE or QIMM_ACT_BF16");
+    blk->act = mode;
+    return QIMM_OK;
+}
+
+int qimm_block_act_mode(const qimm_block *blk) { return blk ? blk->act : -1; }
 
 int qimm_block_forward(qimm_block *blk, const float *x, float *x_out, int64_t batch, int64_t seq,
                        const float *mod, const float *pe, const qimm_kv *kv, int64_t layer, uint16_t *k_out,
@@ -399,6 +441,23 @@ int qimm_v_transpose(qimm_ctx *ctx, const float *x, int64_t batch, int64_t seq, 
     if (!ctx || !x || !vt_out) return QIMM_ERR_ARG;
     if (batch < 0 || seq < 0 || heads < 0) return set_err(ctx, QIMM_ERR_SHAPE, "v_transpose: negative size");
     QIMM_HIP(ctx, qimm::launch_qk_prep(x, batch, seq, heads, nullptr, nullptr, 1, vt_out, (hipStream_t)stream));
+    return QIMM_OK;
+}
+
+int qimm_quantize_act(qimm_ctx *ctx, int weight_type, const float *x, int64_t m, int64_t k, int64_t ldx,
+                      uint16_t *out, int64_t ldo, void *stream) {
+    if (!ctx || !x || !out) return QIMM_ERR_ARG;
+    const int qblk = weight_type == QIMM_TYPE_Q8_0 ? 32
+                     : (weight_type == QIMM_TYPE_Q4_K || weight_type == QIMM_TYPE_Q6_K) ? 256 : 0;
+    if (!qblk) return set_err(ctx, QIMM_ERR_TYPE, "quantize_act: weight type must be Q8_0, Q4_K or Q6_K");
+    if (m < 0 || k <= 0 || k % qblk || ldx < k || ldo < k || ldx % 4 || ldo % 4)
+        return set_err(ctx, QIMM_ERR_SHAPE, "quantize_act: k must be a positive multiple of the block (32 or 256), "
+                                            "ldx, ldo >= k and multiples of 4");
+    if (((uintptr_t)x | (uintptr_t)out) & 15)
+        return set_err(ctx, QIMM_ERR_ARG, "quantize_act: x and out must be 16-byte aligned");
+    if (m == 0) return QIMM_OK;
+    QIMM_HIP(ctx, hipSetDevice(ctx->device));
+    QIMM_HIP(ctx, qimm::launch_quant_rows(x, ldx, m, k, qblk, out, ldo, (hipStream_t)stream));
     return QIMM_OK;
 }
 

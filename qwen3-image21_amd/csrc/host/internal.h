@@ -64,6 +64,7 @@ struct qimm_block {
     qimm_weight *gate_up = nullptr;      // rows interleaved per 64: gate | up
     qimm_weight *down = nullptr;
     float *norm_q = nullptr, *norm_k = nullptr;  // device [128]
+    int act = QIMM_ACT_CANDLE;           // arithmetic at the quantized matmul inputs
     // stage timing (qimm_block_profile): events around the stages of a forward
     bool profiling = false;
     bool profiled_once = false;

@@ -110,6 +110,36 @@ __device__ __forceinline__ int wave_min_i(int v) {
     return v;
 }
 
+// f32 output of a wave's 32 queries x 128 d (O^T accumulators: lane l32 owns
+// query q0 + l32, o[dt][4 rq + e] is d = 32 dt + 8 rq + 4 g + e), in two
+// 64-wide passes through the wave's f32 staging rows (pitch PITCH floats) so
+// that every store covers 256 B of a row. All waves of the workgroup call it.
+template <int PITCH>
+__device__ __forceinline__ void store_out_f32(float *osf, const f32x16 (&o)[4], float inv, int lane,
+                                              float *__restrict__ outf, int64_t bb, int64_t Sq, int64_t row_len,
+                                              int64_t col0, int64_t q0) {
+    const int g = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+        __syncthreads();
+#pragma unroll
+        for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+            for (int rq = 0; rq < 4; rq++) {
+                const int t = 2 * hf + dt, d = dt * 32 + 8 * rq + 4 * g;
+                *(f32x4 *)(osf + l32 * PITCH + d) = f32x4{o[t][4 * rq] * inv, o[t][4 * rq + 1] * inv,
+                                                          o[t][4 * rq + 2] * inv, o[t][4 * rq + 3] * inv};
+            }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int r = i * 4 + (lane >> 4), c = (lane & 15) * 4;
+            const int64_t qi = q0 + r;
+            if (qi < Sq) *(f32x4 *)(outf + (bb * Sq + qi) * row_len + col0 + 64 * hf + c) = *(const f32x4 *)(osf + r * PITCH + c);
+        }
+    }
+}
+
 namespace fast {
 
 // A workgroup of NW waves (8, or 4 where 8-wave workgroups leave CUs idle)
@@ -119,6 +149,7 @@ constexpr int HD = 128;
 constexpr int TILE = KB * HD * 2;     // 16 KB: K (64 rows x 256 B) or V^T (128 rows x 128 B)
 constexpr int STAGE = 2 * TILE;       // K tile then V^T tile
 constexpr int OP = 136;               // bf16 pitch of the output staging rows
+constexpr int OPF = 68;               // f32 pitch of the f32 output staging rows (64 d per pass)
 constexpr int lds_bytes(int nw) { return 2 * STAGE > nw * 32 * OP * 2 ? 2 * STAGE : nw * 32 * OP * 2; }
 constexpr float RESCALE_TH = 8.0f;    // log2 units
 
@@ -130,7 +161,8 @@ template <int NW, bool PRE, bool MASKED>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16_t *__restrict__ q, Seg s0, Seg s1,
                                                                     int64_t H, int64_t Sq, int64_t nq, int64_t B,
                                                                     float sl2, uint16_t *__restrict__ out,
-                                                                    KeyMask km, const int32_t *__restrict__ lim) {
+                                                                    float *__restrict__ outf, KeyMask km,
+                                                                    const int32_t *__restrict__ lim) {
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int QB = 32 * NW;  // queries per workgroup
     constexpr int DI = 16 / NW;  // DMA instructions per wave per 16 KB tile
@@ -466,6 +498,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
     // normalize and stage O [32 q x 128 d] per wave through LDS for row stores
     const float l_tot = xsum32(l_run);
     const float inv = 1.0f / l_tot;
+    if (outf) {
+        store_out_f32<OPF>((float *)lds + wave * 32 * OPF, o, inv, lane, outf, bb, Sq, H * HD, hh * HD, q0);
+        return;
+    }
     uint16_t *os = (uint16_t *)lds + wave * 32 * OP;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
@@ -508,7 +544,8 @@ constexpr int OP = 136;     // bf16 pitch of the output staging rows
 template <bool MASKED>
 __global__ __launch_bounds__(256, 2) void attn_any_kernel(const uint16_t *__restrict__ q, Seg s0, Seg s1,
                                                       int64_t H, int64_t Sq, int64_t nq, int64_t B,
-                                                      float sl2, uint16_t *__restrict__ out, KeyMask km) {
+                                                      float sl2, uint16_t *__restrict__ out,
+                                                      float *__restrict__ outf, KeyMask km) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
 
@@ -689,6 +726,10 @@ __global__ __launch_bounds__(256, 2) void attn_any_kernel(const uint16_t *__rest
     // normalize and stage O [32 q x 128 d] per wave through LDS for row stores
     const float l_tot = l_run + __shfl_xor(l_run, 32);
     const float inv = 1.0f / l_tot;
+    if (outf) {
+        store_out_f32<68>((float *)lds + wave * 32 * 68, o, inv, lane, outf, bb, Sq, H * HD, hh * HD, q0);
+        return;
+    }
     uint16_t *os = lds + wave * 32 * OP;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
@@ -715,10 +756,10 @@ __global__ __launch_bounds__(256, 2) void attn_any_kernel(const uint16_t *__rest
 
 template <int NW, bool PRE, bool MASKED>
 void launch_fast(const uint16_t *q, Seg s0, Seg s1, int64_t h, int64_t sq, int64_t b, float sl2, uint16_t *out,
-                 const KeyMask &km, const int32_t *lim, hipStream_t stream) {
+                 float *outf, const KeyMask &km, const int32_t *lim, hipStream_t stream) {
     const int64_t nq = (sq + 32 * NW - 1) / (32 * NW);
     fast::attn_fast_kernel<NW, PRE, MASKED><<<dim3((unsigned)(nq * h * b)), dim3(64 * NW), 0, stream>>>(
-        q, s0, s1, h, sq, nq, b, sl2, out, km, lim);
+        q, s0, s1, h, sq, nq, b, sl2, out, outf, km, lim);
 }
 
 // Waves per workgroup of the unmasked fast kernel, from the rounds each form
@@ -743,7 +784,7 @@ int fast_waves(int64_t bh, int64_t sq) {
 template <bool PRE>
 hipError_t launch(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p, const uint16_t *ko,
                   const uint16_t *vto, int64_t so, int64_t b, int64_t h, int64_t sq, float sl2, uint16_t *out,
-                  hipStream_t stream) {
+                  float *outf, hipStream_t stream) {
     if (sq <= 0 || b <= 0 || h <= 0) return hipSuccess;
     if (p < 0 || so < 0 || p + so <= 0) return hipErrorInvalidValue;
     Seg s0{kp, vtp, p}, s1{ko, vto, so};
@@ -754,13 +795,13 @@ hipError_t launch(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, in
     if ((p & 7) == 0 && (so & 7) == 0) {
         const KeyMask km{nullptr, nullptr, p + so};
         if (fast_waves(b * h, sq) == 4)
-            launch_fast<4, PRE, false>(q, s0, s1, h, sq, b, sl2, out, km, nullptr, stream);
+            launch_fast<4, PRE, false>(q, s0, s1, h, sq, b, sl2, out, outf, km, nullptr, stream);
         else
-            launch_fast<8, PRE, false>(q, s0, s1, h, sq, b, sl2, out, km, nullptr, stream);
+            launch_fast<8, PRE, false>(q, s0, s1, h, sq, b, sl2, out, outf, km, nullptr, stream);
     } else {
         const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;
         anylen::attn_any_kernel<false><<<dim3((unsigned)(nq * h * b)), dim3(256), 0, stream>>>(
-            q, s0, s1, h, sq, nq, b, sl2, out, KeyMask{nullptr, nullptr, p + so});
+            q, s0, s1, h, sq, nq, b, sl2, out, outf, KeyMask{nullptr, nullptr, p + so});
     }
     return hipGetLastError();
 }
@@ -769,14 +810,14 @@ hipError_t launch(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, in
 
 hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
                             const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
-                            int64_t sq, float scale, uint16_t *out, hipStream_t stream) {
-    return launch<false>(q, kp, vtp, p, ko, vto, so, b, h, sq, scale * 1.4426950408889634f, out, stream);
+                            int64_t sq, float scale, uint16_t *out, hipStream_t stream, float *outf) {
+    return launch<false>(q, kp, vtp, p, ko, vto, so, b, h, sq, scale * 1.4426950408889634f, out, outf, stream);
 }
 
 hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
                                    const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
                                    int64_t sq, float sl2, const int32_t *img, const uint8_t *kvalid,
-                                   int32_t *lim_scratch, uint16_t *out, hipStream_t stream) {
+                                   int32_t *lim_scratch, uint16_t *out, hipStream_t stream, float *outf) {
     if (sq <= 0 || b <= 0 || h <= 0) return hipSuccess;
     if (p < 0 || so < 0 || p + so <= 0) return hipErrorInvalidValue;
     if (img && (p != 0 || so != sq)) return hipErrorInvalidValue;  // block-causal: one shared sequence
@@ -792,19 +833,19 @@ hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const 
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
-        launch_fast<8, false, true>(q, s0, s1, h, sq, b, sl2, out, km, img ? lim_scratch : nullptr, stream);
+        launch_fast<8, false, true>(q, s0, s1, h, sq, b, sl2, out, outf, km, img ? lim_scratch : nullptr, stream);
         return hipGetLastError();
     }
     const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;
     anylen::attn_any_kernel<true><<<dim3((unsigned)(nq * h * b)), dim3(256), 0, stream>>>(
-        q, s0, s1, h, sq, nq, b, sl2, out, km);
+        q, s0, s1, h, sq, nq, b, sl2, out, outf, km);
     return hipGetLastError();
 }
 
 hipError_t launch_attention_log2(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
                                  const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
-                                 int64_t sq, uint16_t *out, hipStream_t stream) {
-    return launch<true>(q, kp, vtp, p, ko, vto, so, b, h, sq, 1.0f, out, stream);
+                                 int64_t sq, uint16_t *out, hipStream_t stream, float *outf) {
+    return launch<true>(q, kp, vtp, p, ko, vto, so, b, h, sq, 1.0f, out, outf, stream);
 }
 
 }  // namespace qimm

@@ -106,4 +106,61 @@ __device__ __forceinline__ float group_sum(float v, int width) {
     return v;
 }
 
+// bf16 bits of the exact product d * q, rounded once to nearest even. p = d*q
+// is the f32 rounding and e = d*q - p its exact error (one fma); the bf16
+// rounding of p equals that of the exact product except when p sits exactly
+// halfway between two bf16 values, where the sign of e decides.
+__device__ __forceinline__ uint32_t bf16_of_product(float d, float q) {
+    const float p = d * q;
+    const float e = __builtin_fmaf(d, q, -p);
+    const uint32_t b = __float_as_uint(p);
+    uint32_t r = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+    if ((b & 0xffffu) == 0x8000u && e != 0.f) r = ((e > 0.f) == (p > 0.f)) ? (b >> 16) + 1u : (b >> 16);
+    return q == 0.f ? 0u : r;  // a zero code gives +0 whatever the signs (the codes are integers)
+}
+
+// The activation rounding of candle's CPU QMatMul (candle-core 0.11
+// quantized/k_quants.rs, the vec-dot type of the weight): each lane holds four
+// consecutive values of a row, consecutive lanes continue the row.
+//  QBLK 256, BlockQ8K::from_float: the wave's 256 values are one block; x_max is
+//    the first value (in row order) of largest magnitude, iscale = -128/x_max,
+//    q = min(127, round(iscale * x)) (round half away from zero), d = 1/iscale.
+//  QBLK 32, BlockQ8_0::from_float: each aligned group of 8 lanes is one block;
+//    d = amax/127, q = round(x / d) computed as x * (1/d), and the block keeps d
+//    as f16 (round to nearest even).
+// Returns the four bf16 operands bf16(d * q) (bf16_of_product), packed in
+// pairs. Every lane of the block must take part (whole waves for 256, whole
+// 8-lane groups for 32); all-zero blocks give zeros, as candle's d = 0 does.
+template <int QBLK>
+__device__ __forceinline__ u32x2 quant_act4(f32x4 v) {
+    static_assert(QBLK == 32 || QBLK == 256, "Q8_0 or Q8_K blocks");
+    float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    float d, s;  // value = d * q, q from x * s
+    if constexpr (QBLK == 256) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o));
+        const int e = fabsf(v[0]) == a ? 0 : fabsf(v[1]) == a ? 1 : fabsf(v[2]) == a ? 2 : fabsf(v[3]) == a ? 3 : -1;
+        const uint64_t hit = __ballot(e >= 0);
+        const int first = hit ? (int)__builtin_ctzll(hit) : 0;
+        const float mine = e == 0 ? v[0] : e == 1 ? v[1] : e == 2 ? v[2] : v[3];
+        const float xmax = __shfl(mine, first);
+        s = a == 0.f ? 0.f : -128.f / xmax;
+        d = a == 0.f ? 0.f : 1.f / s;
+    } else {
+#pragma unroll
+        for (int o = 4; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o));
+        const float d32 = a / 127.f;
+        s = d32 != 0.f ? 1.f / d32 : 0.f;
+        d = (float)(_Float16)d32;
+    }
+    float q[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        q[i] = roundf(v[i] * s);
+        if constexpr (QBLK == 256) q[i] = fminf(q[i], 127.f);
+    }
+    return u32x2{bf16_of_product(d, q[0]) | (bf16_of_product(d, q[1]) << 16),
+                 bf16_of_product(d, q[2]) | (bf16_of_product(d, q[3]) << 16)};
+}
+
 }  // namespace qimm

@@ -44,8 +44,10 @@ struct EpiParams {
     int64_t n_offset;
     float q_scale = 1.0f;  // multiplies q after RoPE, before the bf16 rounding
     // EPI_SWIGLU: tile columns [0,64) gate, [64,128) up -> hmid[m*ldh + n/2 + j]
+    // (bf16), or hmid_f32[m*ldh + n/2 + j] (f32) when hmid_f32 is set
     uint16_t *hmid;
     int64_t ldh;
+    float *hmid_f32 = nullptr;
     // f32 scratch of part_ws_bytes for the short-M split-K path (optional;
     // without it short M takes the 128x128 kernel)
     float *part_ws = nullptr;
@@ -117,16 +119,27 @@ hipError_t launch_mod_prep(const float *mod, int64_t rows, int64_t hidden, float
 // out[m][:] = bf16(LayerNorm(x[m][:]) * modp_scale[(m / rows_per) * stride + :]);
 // one workgroup keeps a row in registers, so hidden <= LN_MAX_HIDDEN
 // (hipErrorInvalidValue beyond).
+// qblk 32 / 256: the output is candle's activation rounding of the f32 values
+// instead (Q8_0 / Q8_K blocks along the row, quant_act4 of device_common.h;
+// hidden % 256 == 0); 0: plain bf16.
 constexpr int64_t LN_MAX_HIDDEN = 8192;
 hipError_t launch_ln_mod(const float *x, int64_t m, int64_t hidden, const float *scale,
-                         int64_t stride, int64_t rows_per, uint16_t *out, hipStream_t stream);
+                         int64_t stride, int64_t rows_per, uint16_t *out, hipStream_t stream, int qblk = 0);
+// out[m][:] (bf16, row stride ldo) = candle's activation rounding of the f32
+// rows x[m][:k] (row stride ldx) in blocks of qblk = 32 (Q8_0) or 256 (Q8_K).
+hipError_t launch_quant_rows(const float *x, int64_t ldx, int64_t m, int64_t k, int qblk, uint16_t *out,
+                             int64_t ldo, hipStream_t stream);
+// The activation block of candle's vec-dot type for a weight format: 32 for
+// Q8_0, 256 for Q4_K / Q6_K (Q8_K), 0 for float weights (a plain matmul).
+inline int act_block(int fmt) { return fmt == WF_Q8_0 ? 32 : (fmt == WF_Q4_K || fmt == WF_Q6_K) ? 256 : 0; }
 
 // Joint attention over [prefix ; own] keys. q, k_* : [B,H,S,128] bf16;
-// vt_* : [B,H,128,S] bf16; out [B,Sq,H*128] bf16.
+// vt_* : [B,H,128,S] bf16; out [B,Sq,H*128] bf16, or outf [B,Sq,H*128] f32
+// instead when outf is set (out is then not written).
 hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp,
                             int64_t p, const uint16_t *ko, const uint16_t *vto, int64_t so,
                             int64_t b, int64_t h, int64_t sq, float scale, uint16_t *out,
-                            hipStream_t stream);
+                            hipStream_t stream, float *outf = nullptr);
 // Masked attention (build_block_causal_mask semantics): img [sq] image block
 // ids (-1 text) for a prefix-less call where queries and keys are one
 // sequence (so == sq), kvalid [b][p + so] key validity; either may be null.
@@ -136,12 +149,14 @@ hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_
 hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
                                    const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
                                    int64_t sq, float sl2, const int32_t *img, const uint8_t *kvalid,
-                                   int32_t *lim_scratch, uint16_t *out, hipStream_t stream);
+                                   int32_t *lim_scratch, uint16_t *out, hipStream_t stream,
+                                   float *outf = nullptr);
 // The same with q already multiplied by scale * log2(e) (the QKV epilogue's
 // q_scale), so scores are in log2 units.
 hipError_t launch_attention_log2(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp,
                                  int64_t p, const uint16_t *ko, const uint16_t *vto, int64_t so,
-                                 int64_t b, int64_t h, int64_t sq, uint16_t *out, hipStream_t stream);
+                                 int64_t b, int64_t h, int64_t sq, uint16_t *out, hipStream_t stream,
+                                 float *outf = nullptr);
 
 // Per-head RmsNorm + RoPE of raw projections x [B,S,H,128] (f32) into the
 // attention layouts; mode 0: q/k -> [B,H,S,128]; mode 1: v -> vt [B,H,128,S].

@@ -340,14 +340,17 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(const uint16_t *__restric
             const int64_t m = m0 + row;
             if (m >= M) continue;
             const float *cr = cs + row * CP;
-            uint32_t pk[4];
+            float h[8];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float h0 = silu(cr[j0 + 2 * i]) * cr[64 + j0 + 2 * i];
-                float h1 = silu(cr[j0 + 2 * i + 1]) * cr[64 + j0 + 2 * i + 1];
-                pk[i] = pack_bf16x2(h0, h1);
+            for (int i = 0; i < 8; i++) h[i] = silu(cr[j0 + i]) * cr[64 + j0 + i];
+            const int64_t o = m * ep.ldh + n0 / 2 + j0;
+            if (ep.hmid_f32) {
+                *(f32x4 *)(ep.hmid_f32 + o) = f32x4{h[0], h[1], h[2], h[3]};
+                *(f32x4 *)(ep.hmid_f32 + o + 4) = f32x4{h[4], h[5], h[6], h[7]};
+            } else {
+                *(u32x4 *)(ep.hmid + o) = u32x4{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]),
+                                               pack_bf16x2(h[4], h[5]), pack_bf16x2(h[6], h[7])};
             }
-            *(u32x4 *)(ep.hmid + m * ep.ldh + n0 / 2 + j0) = u32x4{pk[0], pk[1], pk[2], pk[3]};
         }
     } else {  // EPI_QKV
         const int64_t nb = n0 + ep.n_offset;

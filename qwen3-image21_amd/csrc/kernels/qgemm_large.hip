@@ -459,7 +459,11 @@ __global__ __launch_bounds__(256, 1) void qgemm_large_kernel(const uint16_t *__r
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
                     const float h = silu(acc[i][j][r]) * acc[i][j + 2][r];
-                    ep.hmid[m * ep.ldh + nw / 2 + j * 32 + l32] = (uint16_t)(pack_bf16x2(h, 0.f) & 0xffffu);
+                    const int64_t o = m * ep.ldh + nw / 2 + j * 32 + l32;
+                    if (ep.hmid_f32)
+                        ep.hmid_f32[o] = h;
+                    else
+                        ep.hmid[o] = (uint16_t)(pack_bf16x2(h, 0.f) & 0xffffu);
                 }
             }
         }

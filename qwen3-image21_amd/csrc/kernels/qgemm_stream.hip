@@ -291,6 +291,13 @@ int device_cus() { return device_cu_count(); }
 
 // silu with the hardware reciprocal (about 1 ulp) instead of an IEEE divide
 __device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+// one SwiGLU hidden value: bf16 into hmid, or f32 into hmid_f32 when set
+__device__ __forceinline__ void store_hidden(const EpiParams &ep, int64_t o, float h) {
+    if (ep.hmid_f32)
+        ep.hmid_f32[o] = h;
+    else
+        ep.hmid[o] = (uint16_t)(pack_bf16x2(h, 0.f) & 0xffffu);
+}
 
 // ---------------------------------------------------------------------------
 // M <= 64, Q4_K / Q6_K / Q8_0, K % 1024 == 0: one launch per product.
@@ -760,9 +767,7 @@ __device__ void unit_epilogue(const float *part, const Plan &p, int64_t unit, in
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int m = 16 * tt + 4 * kg + e;
-                if (m < M)
-                    ep.hmid[m * ep.ldh + 64 * blk + 16 * q + l16] =
-                        (uint16_t)(pack_bf16x2(silu(sum[2 * tt][e]) * sum[2 * tt + 1][e], 0.f) & 0xffffu);
+                if (m < M) store_hidden(ep, m * ep.ldh + 64 * blk + 16 * q + l16, silu(sum[2 * tt][e]) * sum[2 * tt + 1][e]);
             }
         }
     } else {
@@ -1142,9 +1147,7 @@ __global__ __launch_bounds__(64 * NW, 1) void wl_kernel(const uint16_t *__restri
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int m = 4 * kg + e;
-                    if (m < M)
-                        ep.hmid[m * ep.ldh + 64 * blk + 16 * q + l16] =
-                            (uint16_t)(pack_bf16x2(silu(v[e]) * up[e], 0.f) & 0xffffu);
+                    if (m < M) store_hidden(ep, m * ep.ldh + 64 * blk + 16 * q + l16, silu(v[e]) * up[e]);
                 }
             } else {
                 const int64_t n = g * 16 + l16;
@@ -1535,9 +1538,7 @@ __global__ __launch_bounds__(128 * GPW, 1) void wk_kernel(const uint16_t *__rest
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int m = 16 * tt + 4 * kg + e;
-                    if (m < M)
-                        ep.hmid[m * ep.ldh + 64 * blk + 16 * q + l16] =
-                            (uint16_t)(pack_bf16x2(silu(v[e]) * up[e], 0.f) & 0xffffu);
+                    if (m < M) store_hidden(ep, m * ep.ldh + 64 * blk + 16 * q + l16, silu(v[e]) * up[e]);
                 }
             } else {
                 const int64_t n = g * 16 + l16;
@@ -1614,8 +1615,11 @@ __global__ __launch_bounds__(256) void stream_epi_kernel(const float *__restrict
         const uint32_t m = q * 4 / F, h = q * 4 % F;
         const int64_t cg = (int64_t)(h >> 6) * 128 + (h & 63);
         const f32x4 gt = csum4(part, splits, MN, (int64_t)m * N + cg), up = csum4(part, splits, MN, (int64_t)m * N + cg + 64);
-        *(u32x2 *)(ep.hmid + (int64_t)m * ep.ldh + h) =
-            u32x2{pack_bf16x2(silu(gt[0]) * up[0], silu(gt[1]) * up[1]), pack_bf16x2(silu(gt[2]) * up[2], silu(gt[3]) * up[3])};
+        const f32x4 hv{silu(gt[0]) * up[0], silu(gt[1]) * up[1], silu(gt[2]) * up[2], silu(gt[3]) * up[3]};
+        if (ep.hmid_f32)
+            *(f32x4 *)(ep.hmid_f32 + (int64_t)m * ep.ldh + h) = hv;
+        else
+            *(u32x2 *)(ep.hmid + (int64_t)m * ep.ldh + h) = u32x2{pack_bf16x2(hv[0], hv[1]), pack_bf16x2(hv[2], hv[3])};
     } else {
         const int64_t idx = (int64_t)q * 4;
         if (idx >= MN) return;

@@ -85,8 +85,13 @@ __global__ void mod_prep_kernel(const float *__restrict__ mod, int64_t n, int64_
 // ---- LayerNorm (weight 1, bias 0, eps 1e-6) * (1 + scale) -> bf16 ----
 // src/quantized_transformer.rs:231-237, 267-269, 276-278. One 256-thread
 // workgroup per row; the row stays in registers for the two-pass variance.
+// With QBLK 32 or 256 the output is the bf16 operand of candle's activation
+// quantization instead (quant_act4): thread t holds chunk t + 256 i, so for
+// iteration i wave w holds the 256 consecutive values of block 4 i + w (hidden
+// is a multiple of 256: whole waves are in or out of the row).
 constexpr int LN_MAXV = (int)(LN_MAX_HIDDEN / 4 / 256);  // float4 chunks per thread
 
+template <int QBLK>
 __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x, int64_t hidden,
                                                      const float *__restrict__ scale, int64_t stride,
                                                      int64_t rows_per, uint16_t *__restrict__ out) {
@@ -135,11 +140,33 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x
         const int c = tid + 256 * i;
         if (c < nv) {
             const f32x4 s4 = sv[i];
-            u32x2 pk{pack_bf16x2((v[i][0] - mean) * rstd * s4[0], (v[i][1] - mean) * rstd * s4[1]),
-                     pack_bf16x2((v[i][2] - mean) * rstd * s4[2], (v[i][3] - mean) * rstd * s4[3])};
-            *(u32x2 *)(orow + 4 * c) = pk;
+            const f32x4 y{(v[i][0] - mean) * rstd * s4[0], (v[i][1] - mean) * rstd * s4[1],
+                          (v[i][2] - mean) * rstd * s4[2], (v[i][3] - mean) * rstd * s4[3]};
+            if constexpr (QBLK == 0)
+                *(u32x2 *)(orow + 4 * c) = u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+            else
+                *(u32x2 *)(orow + 4 * c) = quant_act4<QBLK>(y);
         }
     }
+}
+
+// ---- candle's activation quantization of f32 rows (QMatMul::forward's
+// quantize step, src/quantized_transformer.rs:19-29 -> candle-core 0.11
+// BlockQ8_0 / BlockQ8K::from_float) to the bf16 operands bf16(d * q) ----
+// One wave per 256 values of a row (four per lane): a Q8_K block, or eight
+// Q8_0 blocks. Rows of k values (k % 256 == 0 for Q8_K, k % 32 == 0 for
+// Q8_0; a row's last wave may be partial, whole 8-lane groups then idle).
+template <int QBLK>
+__global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict__ x, int64_t ldx, int64_t m,
+                                                         int64_t k, uint16_t *__restrict__ out, int64_t ldo) {
+    const int64_t wpr = (k + 255) / 256;
+    const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gw >= m * wpr) return;  // whole waves
+    const int64_t row = gw / wpr, c = (gw % wpr) * 256 + 4 * (threadIdx.x & 63);
+    const bool ok = c < k;
+    const f32x4 v = ok ? *(const f32x4 *)(x + row * ldx + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const u32x2 r = quant_act4<QBLK>(v);
+    if (ok) *(u32x2 *)(out + row * ldo + c) = r;
 }
 
 // ---- per-head RmsNorm + RoPE prep (src/quantized_transformer.rs:137-142) ----
@@ -231,10 +258,33 @@ hipError_t launch_mod_prep(const float *mod, int64_t rows, int64_t hidden, float
 }
 
 hipError_t launch_ln_mod(const float *x, int64_t m, int64_t hidden, const float *scale, int64_t stride,
-                         int64_t rows_per, uint16_t *out, hipStream_t stream) {
+                         int64_t rows_per, uint16_t *out, hipStream_t stream, int qblk) {
     if (m <= 0) return hipSuccess;
     if (hidden > LN_MAX_HIDDEN || hidden % 4) return hipErrorInvalidValue;
-    ln_mod_kernel<<<dim3((unsigned)m), dim3(256), 0, stream>>>(x, hidden, scale, stride, rows_per, out);
+    if (qblk && hidden % 256) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)m), block(256);
+    if (qblk == 0)
+        ln_mod_kernel<0><<<grid, block, 0, stream>>>(x, hidden, scale, stride, rows_per, out);
+    else if (qblk == 32)
+        ln_mod_kernel<32><<<grid, block, 0, stream>>>(x, hidden, scale, stride, rows_per, out);
+    else if (qblk == 256)
+        ln_mod_kernel<256><<<grid, block, 0, stream>>>(x, hidden, scale, stride, rows_per, out);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_quant_rows(const float *x, int64_t ldx, int64_t m, int64_t k, int qblk, uint16_t *out, int64_t ldo,
+                             hipStream_t stream) {
+    if (m <= 0 || k <= 0) return hipSuccess;
+    if ((qblk != 32 && qblk != 256) || k % qblk || k % 4 || ldx % 4 || ldo % 4 || ldx < k || ldo < k)
+        return hipErrorInvalidValue;
+    const int64_t waves = m * ((k + 255) / 256);
+    const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+    if (qblk == 32)
+        quant_rows_kernel<32><<<grid, block, 0, stream>>>(x, ldx, m, k, out, ldo);
+    else
+        quant_rows_kernel<256><<<grid, block, 0, stream>>>(x, ldx, m, k, out, ldo);
     return hipGetLastError();
 }
 

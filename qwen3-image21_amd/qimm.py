@@ -66,6 +66,9 @@ SIGNATURES = [
     ("qimm_block_destroy", _i32, [_vp]),
     ("qimm_block_forward", _i32, [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp]),
     ("qimm_block_reserve", _i32, [_vp, _i64, _i64, _i64]),
+    ("qimm_block_set_act_mode", _i32, [_vp, _i32]),
+    ("qimm_block_act_mode", _i32, [_vp]),
+    ("qimm_quantize_act", _i32, [_vp, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     ("qimm_block_forward_masked", _i32, [_vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp,
                                          _vp]),
     ("qimm_block_profile", _i32, [_vp, _i32]),
@@ -94,7 +97,9 @@ SIGNATURES = [
     ("qimm_gguf_block_tensors", _i32, [_vp, _i64, _vp, C.c_char_p, C.c_size_t]),
     ("qimm_gguf_model_tensors", _i32, [_vp, _vp, C.c_char_p, C.c_size_t]),
 ]
-BLOCK_STAGES = ("norm1", "qkv", "attention", "out_proj", "norm2", "gate_up", "down")
+BLOCK_STAGES = ("norm1", "qkv", "attention", "attn_round", "out_proj", "norm2", "gate_up", "hidden_round", "down")
+# activation arithmetic at the block's quantized matmul inputs (qimm_block_set_act_mode)
+ACT_CANDLE, ACT_BF16 = 0, 1
 
 
 class BlockConfig(C.Structure):
@@ -211,6 +216,13 @@ class Context:
         self.check(self.lib.qimm_qmatmul_noalloc(self.h, w.h, x_dev, m, lda, y_dev, out_type, stream),
                    "qimm_qmatmul_noalloc")
 
+    def quantize_act(self, weight_type: int, x_dev: int, m: int, k: int, out_dev: int, ldx: int | None = None,
+                     ldo: int | None = None, stream: int = 0):
+        """candle's activation rounding of f32 rows x [m, k] to the bf16 operands of a matmul with a
+        weight of weight_type (qimm_quantize_act)."""
+        self.check(self.lib.qimm_quantize_act(self.h, weight_type, x_dev, m, k, ldx or k, out_dev, ldo or k, stream),
+                   "qimm_quantize_act")
+
     # -- cache --
     def kv_create(self, layers: int, batch: int, heads: int, prefix_len: int, head_dim: int = 128) -> "KvCache":
         h = C.c_void_p()
@@ -317,6 +329,14 @@ class Block:
     def reserve(self, batch, seq, mod_rows=1):
         """Pre-size the context scratch so forwards up to batch x seq tokens do not allocate."""
         self.ctx.check(self.ctx.lib.qimm_block_reserve(self.h, batch, seq, mod_rows), "qimm_block_reserve")
+
+    def set_act_mode(self, mode: int):
+        """ACT_CANDLE (default): the reference CPU path's int8 activation rounding; ACT_BF16: bf16 operands."""
+        self.ctx.check(self.ctx.lib.qimm_block_set_act_mode(self.h, mode), "qimm_block_set_act_mode")
+
+    @property
+    def act_mode(self) -> int:
+        return self.ctx.lib.qimm_block_act_mode(self.h)
 
     def forward(self, x_dev, x_out_dev, batch, seq, mod_dev, pe_dev, kv=None, layer=0, k_out=None, v_out=None,
                 stream=0):

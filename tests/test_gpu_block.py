@@ -1,15 +1,15 @@
 """GPU parity of the whole block step (TransformerBlock::forward on the cached
 step, src/quantized_transformer.rs:258-285) through qimm_block_create /
-qimm_block_forward, against the oracle on identical seeded inputs.
-
-Bars: against the oracle's f32 candle-mode output (int8 activations, the
-reference CPU path), the block output reaches cosine >= 0.9999 and
-max|a-b|/max|b| <= 2e-2. Against the oracle's exact mode (f32 activations, f64
-accumulation), the stricter cosine of the block's update x_out - x (the
-residual excluded) is >= 0.9999 as well; candle mode itself sits at update
-cosine ~0.99982-0.99994 from exact mode because of its int8 activations, so the
-update metric is only meaningful against exact mode. The own k / v the block
-returns are checked against both modes.
+qimm_block_forward, against the oracle on identical seeded inputs, in both
+activation modes of the block (gpu_util.check_block):
+- QIMM_ACT_CANDLE (the default: the reference CPU path's int8 rounding of every
+  quantized-matmul input) against the oracle's candle mode: the output reaches
+  cosine >= 0.9999 and max|a-b|/max|b| <= 2e-2, and its update x_out - x lies
+  at least as close to candle's as the bf16 mode's does;
+- QIMM_ACT_BF16 against the oracle's exact mode (f32 activations, f64
+  accumulation): cosine >= 0.9999 on the output and on the stricter update,
+  max|a-b|/max|b| <= 2e-2.
+The own k / v the block returns are checked against the matching oracle mode.
 """
 import ctypes as C
 
@@ -19,7 +19,7 @@ import pytest
 import oracle as O
 import qimm
 import synth
-from gpu_util import check_block, cos_sim, dev, host, max_abs_rel, stream
+from gpu_util import check_block, cos_sim, dev, host, kv_close, max_abs_rel, stream
 
 pytestmark = pytest.mark.gpu
 
@@ -38,10 +38,13 @@ def block_tensors(w, keep):
     return T
 
 
-def run_block(torch, qctx, cfg, w, x, mod, pe, kpre=None, vpre=None, alias=False, want_kv=False):
+def run_block(torch, qctx, cfg, w, x, mod, pe, kpre=None, vpre=None, alias=False, want_kv=False,
+              act=qimm.ACT_CANDLE):
     keep = []
     c = qimm.BlockConfig(cfg["hidden"], cfg["heads"], cfg["head_dim"], cfg["mlp"])
     blk = qctx.block_create(c, block_tensors(w, keep))
+    assert blk.act_mode == qimm.ACT_CANDLE  # the default
+    blk.set_act_mode(act)
     b, s, hid = x.shape
     x_dev = dev(torch, x)
     x_out = x_dev if alias else torch.empty_like(x_dev)
@@ -65,6 +68,25 @@ def run_block(torch, qctx, cfg, w, x, mod, pe, kpre=None, vpre=None, alias=False
     return out, kvs
 
 
+def run_modes(torch, qctx, cfg, w, x, mod, pe, kpre=None, vpre=None, alias=False, want_kv=False):
+    """The block in the candle and the bf16 activation mode: ((out, kv), (out, kv))."""
+    return tuple(run_block(torch, qctx, cfg, w, x, mod, pe, kpre, vpre, alias, want_kv, act)
+                 for act in (qimm.ACT_CANDLE, qimm.ACT_BF16))
+
+
+def check_modes(cfg, w, x, mod, pe, kpre, vpre, runs, want_kv=False):
+    """Both modes' outputs (and own k / v) against the oracle's matching modes."""
+    (got_c, kv_c), (got_b, kv_b) = runs
+    ref, kr, vr = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
+    ref_e, kre, vre = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
+    hid = cfg["hidden"]
+    check_block(*(a.reshape(-1, hid) for a in (got_c, got_b, ref, ref_e, x)))
+    if want_kv:
+        for (k, v), (kk, vv) in ((kv_c, (kr, vr)), (kv_b, (kre, vre))):
+            kv_close(k, kk)
+            kv_close(v, vv)
+
+
 def make_case(seed, cfg, b, s, p, attn_type, down_type, fused=True):
     rng = np.random.default_rng(seed)
     w = synth.block_weights(seed, cfg["hidden"], cfg["heads"], cfg["mlp"], attn_type, down_type, fused)
@@ -85,8 +107,7 @@ SMALL = dict(hidden=256, heads=2, head_dim=128, mlp=768)
 
 
 def check(got, ref, x, exact=False):
-    """exact=False: ref is candle mode, cosine on the output; exact=True: ref is
-    exact mode, cosine on the update."""
+    """exact=False: cosine on the output; exact=True: cosine on the update."""
     cs = cos_sim(got - x, ref - x) if exact else cos_sim(got, ref)
     mr = max_abs_rel(got, ref)
     assert cs >= 0.9999 and mr <= 2e-2, (cs, mr)
@@ -101,34 +122,24 @@ def check(got, ref, x, exact=False):
                                    (1, 520, 24), (2, 300, 16), (1, 514, 0)])
 def test_block_matches_oracle(torch_cuda, qctx, attn_type, down_type, b, s, p):
     w, x, mod, pe, kpre, vpre = make_case(b * 1000 + s + p, SMALL, b, s, p, attn_type, down_type)
-    got, (k, v) = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre, want_kv=True)
-    ref, kr, vr = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
-    check(got, ref, x)
-    ref_e, kre, vre = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
-    check(got, ref_e, x, exact=True)
-    for kk, vv in ((kr, vr), (kre, vre)):
-        assert cos_sim(k, kk) >= 0.9999 and max_abs_rel(k, kk) <= 2e-2
-        assert cos_sim(v, vv) >= 0.9999 and max_abs_rel(v, vv) <= 2e-2
+    runs = run_modes(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre, want_kv=True)
+    check_modes(SMALL, w, x, mod, pe, kpre, vpre, runs, want_kv=True)
 
 
 def test_block_in_place_and_separate_mlp_inputs(torch_cuda, qctx):
     w, x, mod, pe, kpre, vpre = make_case(7, SMALL, 1, 64, 16, synth.Q8_0, synth.Q8_0, fused=False)
-    got, _ = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre, alias=True)
-    ref, _, _ = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
-    check(got, ref, x)
-    ref_e, _, _ = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
-    check(got, ref_e, x, exact=True)
+    runs = run_modes(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre, alias=True)
+    check_modes(SMALL, w, x, mod, pe, kpre, vpre, runs)
 
 
 def test_block_mixed_qkv_types_unfused_path(torch_cuda, qctx):
+    """to_v in Q8_0 beside Q4_K to_q / to_k: unfused q/k/v GEMMs, and in candle
+    mode the norm1 output rounded per 256 values for q and k, per 32 for v."""
     w, x, mod, pe, kpre, vpre = make_case(8, SMALL, 1, 64, 32, synth.Q4_K, synth.Q6_K)
     rng = np.random.default_rng(80)
-    w["to_v"] = synth.weight(rng, synth.Q6_K, SMALL["hidden"], SMALL["hidden"])
-    got, _ = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre)
-    ref, _, _ = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
-    check(got, ref, x)
-    ref_e, _, _ = O.block_forward(SMALL, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
-    check(got, ref_e, x, exact=True)
+    w["to_v"] = synth.weight(rng, synth.Q8_0, SMALL["hidden"], SMALL["hidden"])
+    runs = run_modes(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre, want_kv=True)
+    check_modes(SMALL, w, x, mod, pe, kpre, vpre, runs, want_kv=True)
 
 
 def test_block_deterministic(torch_cuda, qctx):
@@ -143,11 +154,8 @@ def test_block_config1_shape(torch_cuda, qctx):
     prefix, Q8_0 weights: the reference CPU-path configuration."""
     cfg = dict(hidden=3072, heads=24, head_dim=128, mlp=9216)
     w, x, mod, pe, kpre, vpre = make_case(11, cfg, 1, 256, 64, synth.Q8_0, synth.Q8_0)
-    got, _ = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
-    ref, _, _ = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
-    check(got, ref, x)
-    ref_e, _, _ = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
-    check(got, ref_e, x, exact=True)
+    runs = run_modes(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
+    check_modes(cfg, w, x, mod, pe, kpre, vpre, runs)
 
 
 @pytest.mark.parametrize("b,s,p,mlp", [(1, 8, 16, 512), (2, 6, 0, 1024), (2, 8, 8, 1024), (1, 16, 0, 2048),
@@ -165,17 +173,8 @@ def test_block_hidden4096_short_m(torch_cuda, qctx, b, s, p, mlp):
     model's MLP 12288 runs at 40 and 24 tokens."""
     cfg = dict(hidden=4096, heads=32, head_dim=128, mlp=mlp)
     w, x, mod, pe, kpre, vpre = make_case(21 + b + s, cfg, b, s, p, synth.Q4_K, synth.Q6_K)
-    got, (k, v) = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)
-    ref, kr, vr = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
-    ref_e, kre, vre = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
-    if mlp == 12288:  # the candle path's own int8 SwiGLU hidden state: bars relative to it
-        check_block(*(a.reshape(b * s, -1) for a in (got, ref, ref_e, x)))
-    else:
-        check(got, ref, x)
-        check(got, ref_e, x, exact=True)
-    for kk, vv in ((kr, vr), (kre, vre)):
-        assert cos_sim(k, kk) >= 0.9999 and max_abs_rel(k, kk) <= 2e-2
-        assert cos_sim(v, vv) >= 0.9999 and max_abs_rel(v, vv) <= 2e-2
+    runs = run_modes(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)
+    check_modes(cfg, w, x, mod, pe, kpre, vpre, runs, want_kv=True)
 
 
 @pytest.mark.parametrize("b,s,p,mlp,attn_type,down_type", [
@@ -194,14 +193,8 @@ def test_block_hidden4096_large_m(torch_cuda, qctx, b, s, p, mlp, attn_type, dow
     both oracle modes. Short MLPs keep the oracle quick."""
     cfg = dict(hidden=4096, heads=32, head_dim=128, mlp=mlp)
     w, x, mod, pe, kpre, vpre = make_case(61 + b + s, cfg, b, s, p, attn_type, down_type)
-    got, (k, v) = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)
-    ref, kr, vr = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
-    check(got, ref, x)
-    ref_e, kre, vre = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
-    check(got, ref_e, x, exact=True)
-    for kk, vv in ((kr, vr), (kre, vre)):
-        assert cos_sim(k, kk) >= 0.9999 and max_abs_rel(k, kk) <= 2e-2
-        assert cos_sim(v, vv) >= 0.9999 and max_abs_rel(v, vv) <= 2e-2
+    runs = run_modes(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)
+    check_modes(cfg, w, x, mod, pe, kpre, vpre, runs, want_kv=True)
 
 
 def test_block_hidden4096_large_m_bf16_weights(torch_cuda, qctx):
@@ -230,16 +223,10 @@ def test_block_mid_m_split_k(torch_cuda, qctx, attn_type, down_type):
     SwiGLU and residual epilogues of the reduction kernel."""
     cfg = dict(hidden=1024, heads=8, head_dim=128, mlp=2048)
     w, x, mod, pe, kpre, vpre = make_case(31, cfg, 1, 128, 16, attn_type, down_type)
-    got, (k, v) = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)
-    ref, kr, vr = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
-    check(got, ref, x)
-    ref_e, kre, vre = O.block_forward(cfg, w, x, mod, pe, kpre, vpre, mode=O.EXACT)
-    check(got, ref_e, x, exact=True)
-    for kk, vv in ((kr, vr), (kre, vre)):
-        assert cos_sim(k, kk) >= 0.9999 and max_abs_rel(k, kk) <= 2e-2
-        assert cos_sim(v, vv) >= 0.9999 and max_abs_rel(v, vv) <= 2e-2
+    runs = run_modes(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre, want_kv=True)
+    check_modes(cfg, w, x, mod, pe, kpre, vpre, runs, want_kv=True)
     again, _ = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
-    assert np.array_equal(got, again)
+    assert np.array_equal(runs[0][0], again)
 
 
 def test_block_rejects_bad_config(torch_cuda, qctx):
@@ -266,6 +253,8 @@ def test_block_reserve_then_forward(torch_cuda, qctx):
     blk.reserve(2, 600)
     with pytest.raises(qimm.QimmError, match="QIMM_ERR_SHAPE"):
         blk.reserve(1, 64, 3)
+    with pytest.raises(qimm.QimmError, match="QIMM_ERR_ARG"):
+        blk.set_act_mode(2)
     blk.free()
     b, _ = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre)
     assert np.array_equal(a, b)

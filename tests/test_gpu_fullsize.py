@@ -15,27 +15,29 @@
   out 4096 x 4096, MLP up 16384 x 4096 and down 4096 x 16384
   (src/quantized_transformer.rs:19-33).
 
-Bars. Against the oracle's exact mode (f32 activations, f64 sums of the exact
-weights): cosine >= 0.9999 on the output and on the update x_out - x, and
-max|a-b|/max|b| <= 2e-2. Against its candle mode (the reference CPU path, whose
-activations are quantized to int8 per 256 values for K-quant weights and per 32
-for Q8_0): max|a-b|/max|b| <= 2e-2, and a cosine no lower than the candle
-path's own cosine to exact arithmetic (less 2e-5) on the same rows. At hidden
-4096 with MLP 12288 the int8 quantization of the SwiGLU hidden state alone puts
-the candle output at cosine ~0.99988 from exact arithmetic, below the 0.9999
-that a direct comparison would ask; the bf16 activations here are ~20x closer
-to exact arithmetic than that, and the test asserts that the GPU lies closer to
-the exact product than the candle path does. Where the oracle would take
-minutes, the query side runs for sampled token rows only
-(oracle.block_forward_rows: every row's K and V, bit-identical rows).
+Bars (gpu_util.check_block). The block in its default QIMM_ACT_CANDLE mode
+(every quantized-matmul input rounded to int8 as the reference CPU path does:
+Q8_K per 256 values for K-quant weights, Q8_0 per 32 for Q8_0) against the
+oracle's candle mode: cosine >= 0.9999 and max|a-b|/max|b| <= 2e-2 on the
+output (at 1024^2 over all rows, and on each row by itself), its update x_out - x closer to
+candle's than the bf16 mode's update. The block in QIMM_ACT_BF16 mode against
+the oracle's exact mode (f32 activations, f64 sums of the exact weights):
+cosine >= 0.9999 on the output and on the update, max|a-b|/max|b| <= 2e-2, and
+closer to exact arithmetic than the candle path. (At hidden 4096 with MLP
+12288 the candle path itself is only at cosine ~0.99988 from exact
+arithmetic: its int8 rounding of the SwiGLU hidden state alone accounts for
+most of that, so each mode is held to the reference whose rounding it follows.)
+Where the oracle would take minutes, the query side runs for sampled token rows
+only (oracle.block_forward_rows: every row's K and V, bit-identical rows).
 """
 import numpy as np
 import pytest
 
 import oracle as O
+import qimm
 import synth
-from gpu_util import bf16_dev, check_block, cos_sim, max_abs_rel, host, stream
-from test_gpu_block import make_case, run_block
+from gpu_util import bf16_dev, check_block, cos_sim, kv_close, max_abs_rel, host, stream
+from test_gpu_block import make_case, run_block, run_modes
 from test_gpu_kernels import _attention_case
 
 pytestmark = pytest.mark.gpu
@@ -51,28 +53,28 @@ def sampled_rows(rng, m, tile=256, extra=48):
     return np.unique(rows)
 
 
-def kv_close(got, want):
-    assert cos_sim(got, want) >= 0.9999 and max_abs_rel(got, want) <= 2e-2, (cos_sim(got, want),
-                                                                            max_abs_rel(got, want))
-
-
 def test_block_1024_q4km_full_size(torch_cuda, qctx):
     b, s, p = 1, 4096, 256
     print("case: block 1024^2 Q4_K_M, hidden 4096, 32 heads, MLP 12288, 4096 tokens over 256", flush=True)
     w, x, mod, pe, kpre, vpre = make_case(4, CFG4, b, s, p, synth.Q4_K, synth.Q6_K)
-    got, (k, v) = run_block(torch_cuda, qctx, CFG4, w, x, mod, pe, kpre, vpre, want_kv=True)
-    assert np.isfinite(got).all()
-    # every output row against the candle-mode oracle
+    (got, (k, v)), (got_b, (kb, vb)) = run_modes(torch_cuda, qctx, CFG4, w, x, mod, pe, kpre, vpre, want_kv=True)
+    assert np.isfinite(got).all() and np.isfinite(got_b).all()
+    # the candle mode against the candle-mode oracle on every output row
     ref, kr, vr = O.block_forward(CFG4, w, x, mod, pe, kpre, vpre, mode=O.CANDLE)
-    assert max_abs_rel(got, ref) <= 2e-2
+    g2, r2 = got.reshape(s, -1), ref.reshape(s, -1)
+    row_cos = np.sum(g2.astype(np.float64) * r2, 1) / np.sqrt(np.sum(np.square(g2, dtype=np.float64), 1) *
+                                                            np.sum(np.square(r2, dtype=np.float64), 1))
+    c, m = cos_sim(got, ref), max_abs_rel(got, ref)
+    print(f"all rows: cos {c:.7f} mar {m:.2e}; lowest row cosine {row_cos.min():.7f}", flush=True)
+    assert c >= 0.9999 and m <= 2e-2 and row_cos.min() >= 0.9999
     kv_close(k, kr)
     kv_close(v, vr)
-    # sampled rows against exact mode (and candle on the same rows), every K / V
+    # sampled rows of both modes against both oracle modes, every K / V of the bf16 mode
     rows = sampled_rows(np.random.default_rng(40), s)
     ref_e, kre, vre = O.block_forward_rows(CFG4, w, x, mod, pe, rows, kpre, vpre, mode=O.EXACT)
-    check_block(got.reshape(s, -1)[rows], ref.reshape(s, -1)[rows], ref_e, x.reshape(s, -1)[rows])
-    kv_close(k, kre)
-    kv_close(v, vre)
+    check_block(g2[rows], got_b.reshape(s, -1)[rows], r2[rows], ref_e, x.reshape(s, -1)[rows])
+    kv_close(kb, kre)
+    kv_close(vb, vre)
 
 
 def multi_ref_pe(text_len, cond, grid):
@@ -103,8 +105,8 @@ def test_multi_ref_attention_full_size(torch_cuda, qctx):
 def test_multi_ref_block_q8_0_full_size(torch_cuda, qctx):
     """One Q8_0 block of the multi-reference step, both CFG prompts batched: 2 x 4096
     target tokens, each prompt over its own 8448-token bf16 prefix cache. Every K / V
-    against the candle-mode oracle; the output on sampled rows of both prompts
-    against exact and candle mode."""
+    of each mode against the matching oracle mode; the output on sampled rows of both
+    prompts in both modes."""
     b, s, p = 2, 4096, 8448
     print("case: multi-reference block Q8_0, B2 x 4096 tokens over 8448-token prefixes", flush=True)
     rng = np.random.default_rng(55)
@@ -114,17 +116,18 @@ def test_multi_ref_block_q8_0_full_size(torch_cuda, qctx):
     pe = multi_ref_pe(256, [64, 64], 64)
     kpre = O.f32_to_bf16(rng.standard_normal((b, CFG4["heads"], p, 128), dtype=np.float32))
     vpre = O.f32_to_bf16(rng.standard_normal((b, CFG4["heads"], p, 128), dtype=np.float32))
-    got, (k, v) = run_block(torch_cuda, qctx, CFG4, w, x, mod, pe, kpre, vpre, want_kv=True)
-    assert np.isfinite(got).all()
+    (got, (k, v)), (got_b, (kb, vb)) = run_modes(torch_cuda, qctx, CFG4, w, x, mod, pe, kpre, vpre, want_kv=True)
+    assert np.isfinite(got).all() and np.isfinite(got_b).all()
     r0 = sampled_rows(np.random.default_rng(56), s, extra=24)
     rows = np.concatenate([r0, s + r0])
-    got_r = got.reshape(b * s, -1)[rows]
     xr = x.reshape(b * s, -1)[rows]
     ref, kr, vr = O.block_forward_rows(CFG4, w, x, mod, pe, rows, kpre, vpre, mode=O.CANDLE)
     kv_close(k, kr)
     kv_close(v, vr)
-    ref_e, _, _ = O.block_forward_rows(CFG4, w, x, mod, pe, rows, kpre, vpre, mode=O.EXACT)
-    check_block(got_r, ref, ref_e, xr)
+    ref_e, kre, vre = O.block_forward_rows(CFG4, w, x, mod, pe, rows, kpre, vpre, mode=O.EXACT)
+    kv_close(kb, kre)
+    kv_close(vb, vre)
+    check_block(got.reshape(b * s, -1)[rows], got_b.reshape(b * s, -1)[rows], ref, ref_e, xr)
 
 
 Q8_SETS = {"qkv": (12288, 4096), "out": (4096, 4096), "up": (16384, 4096), "down": (4096, 16384)}

@@ -1,0 +1,151 @@
+"""Pins the oracle's activation rounding (oq_quant_act_bf16): candle's CPU
+QMatMul::forward quantizes each f32 input row to the weight's vec-dot type
+(src/quantized_transformer.rs:19-29 -> candle-core 0.11 quantized/k_quants.rs,
+BlockQ8K::from_float for Q4_K / Q6_K weights, BlockQ8_0::from_float for Q8_0
+weights), and the GPU feeds the quantized values d * q to its MFMAs as bf16.
+
+Pinned by an independent numpy restatement written from candle's code (f32
+scale arithmetic, first-index maximum, half-away-from-zero rounding, the f16
+scale of Q8_0) with its own bf16 rounding of the exact product (integer
+rounding of the float64 bit pattern, not frexp/rint as in the C code), and by
+known-answer blocks derived by hand, each chosen so that a plausible mistake
+(the last instead of the first maximum, round-half-even, no clamp at 127, the
+f32 instead of the f16 scale, a double-rounded product) fails.
+"""
+import numpy as np
+
+import oracle as O
+
+
+def _round_away(v):
+    """Rust f32::round (half away from zero) of float32 values, exactly (in f64)."""
+    v = v.astype(np.float64)
+    return np.sign(v) * np.floor(np.abs(v) + 0.5)
+
+
+def _bf16_of_f64(v):
+    """bf16 bits of float64 values rounded once to nearest even, by integer
+    rounding of the f64 bit pattern (45 dropped mantissa bits); normal range."""
+    v = np.asarray(v, dtype=np.float64)
+    bits = v.view(np.uint64)
+    keep = bits >> np.uint64(45)
+    rem = bits & np.uint64((1 << 45) - 1)
+    half = np.uint64(1 << 44)
+    up = (rem > half) | ((rem == half) & ((keep & np.uint64(1)) == 1))
+    keep = keep + up.astype(np.uint64)
+    r = (keep << np.uint64(45)).view(np.float64).astype(np.float32)
+    r[v == 0] = 0.0
+    return (r.view(np.uint32) >> 16).astype(np.uint16)
+
+
+def numpy_q8_k(x):
+    x = np.asarray(x, dtype=np.float32).reshape(-1, 256)
+    out = np.empty(x.shape, dtype=np.uint16)
+    for b, xs in enumerate(x):
+        i = int(np.argmax(np.abs(xs)))          # first index of the largest magnitude
+        if np.abs(xs[i]) == 0:
+            out[b] = 0
+            continue
+        iscale = np.float32(-128.0) / xs[i]
+        q = np.minimum(_round_away(iscale * xs), 127.0)
+        d = np.float32(1.0) / iscale
+        out[b] = _bf16_of_f64(np.float64(d) * q)
+    return out.reshape(-1)
+
+
+def numpy_q8_0(x):
+    x = np.asarray(x, dtype=np.float32).reshape(-1, 32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    for b, xs in enumerate(x):
+        amax = np.max(np.abs(xs))
+        d = amax / np.float32(127.0)
+        inv = np.float32(1.0) / d if d != 0 else np.float32(0.0)
+        q = _round_away(xs * inv)
+        d16 = np.float64(np.float16(d))
+        out[b] = _bf16_of_f64(d16 * q)
+    return out.reshape(-1)
+
+
+def _rows(seed, m, k):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((m, k)) * np.exp(rng.standard_normal((m, 1)))).astype(np.float32)
+    x[0, :256] = 0.0                              # an all-zero block
+    x[1, 5], x[1, 77] = -7.0, 7.0                 # equal magnitudes, opposite signs: the first wins
+    x[1, 100], x[1, 101] = 3.5, -3.5
+    return x
+
+
+def test_q8_k_rounding_matches_numpy_restatement():
+    x = _rows(1, 6, 1024)
+    for wt in (O.Q4_K, O.Q6_K):
+        got = O.quant_act_bf16(wt, x)
+        assert np.array_equal(got.reshape(-1), numpy_q8_k(x))
+
+
+def test_q8_0_rounding_matches_numpy_restatement():
+    x = _rows(2, 6, 1024)
+    got = O.quant_act_bf16(O.Q8_0, x)
+    assert np.array_equal(got.reshape(-1), numpy_q8_0(x))
+
+
+def _val(b):
+    """The f32 value of bf16 bits b."""
+    return float(np.array([int(b) << 16], dtype=np.uint32).view(np.float32)[0])
+
+
+def test_q8_k_known_answers():
+    x = np.zeros(256, dtype=np.float32)
+    x[3], x[10] = -2.0, 2.0        # first maximum -2: iscale 64, d 1/64; x[10] -> 128 -> clamped 127
+    x[20], x[21] = 0.5, -0.0078125  # 0.5 * 64 = 32; -0.5 -> -1 (half away from zero; even gives 0)
+    got = O.quant_act_bf16(O.Q4_K, x[None])[0]
+    assert _val(got[3]) == -2.0
+    assert _val(got[10]) == 127.0 / 64.0     # 1.984375, 8 significant bits: exact in bf16
+    assert _val(got[20]) == 0.5
+    assert _val(got[21]) == -1.0 / 64.0
+    assert got[0] == 0
+    # iscale = 1 (x_max = -128): 2.5 -> 3 and -2.5 -> -3 away from zero (2 and -2 to even)
+    y = np.zeros(256, dtype=np.float32)
+    y[0], y[1], y[2] = -128.0, 2.5, -2.5
+    g = O.quant_act_bf16(O.Q6_K, y[None])[0]
+    assert _val(g[0]) == -128.0 and _val(g[1]) == 3.0 and _val(g[2]) == -3.0
+    # the all-zero block gives zeros (candle: d = 0, codes 0)
+    assert np.all(O.quant_act_bf16(O.Q4_K, np.zeros((1, 256), np.float32)) == 0)
+
+
+def test_q8_0_known_answers():
+    # amax 127 * 2^-6: d = 2^-6 exactly in f16, q = x * 64
+    x = np.zeros(32, dtype=np.float32)
+    x[0], x[1], x[2] = 127.0 / 64.0, -1.0, 0.0234375   # 0.0234375 * 64 = 1.5 -> 2 (away from zero)
+    got = O.quant_act_bf16(O.Q8_0, x[None])[0]
+    assert _val(got[0]) == 127.0 / 64.0 and _val(got[1]) == -1.0 and _val(got[2]) == 2.0 / 64.0
+    # amax 1: d = 1/127 rounds to the f16 2^-7 * (1 + 8/1024); x = 1 -> q = 127 ->
+    # 127 * 0.00787353515625 = 0.99993896484375, whose nearest bf16 is 1.0;
+    # x = 1/3 -> q = round(42.33) = 42 -> 0.3306884765625 -> bf16 0.330078125
+    # (the f32 scale 1/127 would give 42/127 = 0.33070866 -> bf16 0.33203125)
+    y = np.zeros(32, dtype=np.float32)
+    y[0], y[1] = 1.0, np.float32(1.0 / 3.0)
+    g = O.quant_act_bf16(O.Q8_0, y[None])[0]
+    assert _val(g[0]) == 1.0
+    assert _val(g[1]) == 0.330078125
+
+
+def test_product_is_rounded_once():
+    """d * q needs up to 32 significant bits, so its f32 rounding can land
+    exactly halfway between two bf16 values and then round the wrong way. Over
+    many random blocks the oracle's bits equal the once-rounded exact product
+    (numpy restatement), and the twice-rounded variant (f32 product, then bf16)
+    differs from it somewhere, so the test can tell the two apart."""
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((400, 256)).astype(np.float32)
+    got = O.quant_act_bf16(O.Q4_K, x).reshape(-1)
+    want = numpy_q8_k(x)
+    assert np.array_equal(got, want)
+    # the twice-rounded variant (f32 product, then bf16) differs somewhere
+    twice = []
+    for xs in x:
+        i = int(np.argmax(np.abs(xs)))
+        iscale = np.float32(-128.0) / xs[i]
+        q = np.minimum(_round_away(iscale * xs), 127.0).astype(np.float32)
+        d = np.float32(1.0) / iscale
+        twice.append(O.f32_to_bf16((d * q).astype(np.float32)))
+    assert not np.array_equal(np.concatenate(twice), want)

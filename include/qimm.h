@@ -112,14 +112,25 @@ int qimm_qmatmul(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_
  * results as qimm_qmatmul; the split-K partial sums and arrival counters live
  * in a static device array of QIMM_NOALLOC_SCRATCH_BYTES (48 MiB) per device,
  * set up when the device's first context is created and held until the
- * process ends, instead of the context's growable scratch. Every shape the
- * library plans needs at most ~34 MB; a product that would need more returns
- * QIMM_ERR_SHAPE. All calls on one device share that array (it keeps the last
- * call's contents; the counters return to zero after every call), so calls
- * that overlap on one device, from any context or stream, race: order them. */
+ * process ends, instead of the context's growable scratch. A product needs
+ * qimm_qmatmul_scratch_bytes(w, m) of it; one that needs more than the array
+ * returns QIMM_ERR_SHAPE (use qimm_qmatmul there). Every projection of the
+ * reference's block (hidden 4096, mlp 12288: q/k/v, out, gate_up, down in
+ * Q8_0, Q4_K, Q6_K or BF16) fits at any m (32 MiB at most); larger products
+ * may not: up to 64 tokens the short-M kernels keep at least m * N * 4 bytes
+ * of split-K partial sums (more than 48 MiB for N above ~196,000 outputs at
+ * 64 tokens). All calls on one device share that array (it
+ * keeps the last call's contents; the counters return to zero after every
+ * call), so calls that overlap on one device, from any context or stream,
+ * race: order them. */
 #define QIMM_NOALLOC_SCRATCH_BYTES (48u << 20)
 int qimm_qmatmul_noalloc(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_t m,
                          int64_t lda, void *y, int out_type, void *stream);
+/* Bytes of device scratch the product of w with m rows takes (0 = none; -1 on
+ * a bad argument): what qimm_qmatmul grows the context scratch to, and what
+ * qimm_qmatmul_noalloc needs of its static array. It depends on the device's
+ * compute-unit count (the split plans). No counterpart in the reference. */
+int64_t qimm_qmatmul_scratch_bytes(const qimm_weight *w, int64_t m);
 
 /* ---------------- host-side layout and RoPE ---------------- */
 
@@ -296,6 +307,11 @@ int qimm_block_act_mode(const qimm_block *blk);
  * allocate nor synchronize. The reference allocates per call through candle
  * and has no counterpart; this is for serving loops that must not stall. */
 int qimm_block_reserve(qimm_block *blk, int64_t batch, int64_t seq, int64_t mod_rows);
+/* A forward captured into a HIP graph keeps the scratch addresses it was
+ * captured with: while such a graph may still be replayed, no call on the
+ * context may grow the scratch (a larger forward, a qimm_qmatmul of a larger
+ * product, qimm_attention_masked over more queries), since growing frees the
+ * old buffers. Reserve the largest sizes first. */
 
 /* An attention mask, the product of build_block_causal_mask
  * (src/attention_mask.rs:18-66) kept as its two inputs (device pointers):
@@ -328,7 +344,12 @@ int qimm_block_forward_masked(qimm_block *blk, const float *x, float *x_out, int
 
 /* qimm_attention with a mask: chunked_attention (src/transformer.rs:259-296)
  * called with Some(mask) (the masked branch adds -inf where the mask is 0).
- * With mask->image_ids, kv must be NULL and so == sq. */
+ * With mask->image_ids, kv must be NULL and so == sq, and the call keeps each
+ * query's last visible key (sq int32) in the context scratch, growing it
+ * first when it is smaller (a device-wide synchronize and an allocation);
+ * after qimm_block_reserve on this context, or any earlier call of that size,
+ * it neither allocates nor synchronizes. Like every call through one context,
+ * it must not overlap another on the device. */
 int qimm_attention_masked(qimm_ctx *ctx, const uint16_t *q, int64_t batch, int64_t heads,
                           int64_t sq, const qimm_kv *kv, int64_t layer, const uint16_t *k_own,
                           const uint16_t *vt_own, int64_t so, float scale,

@@ -110,6 +110,35 @@ def model_forward(cfg, g, blocks, latents, t_sin, pe, kcache=None, vcache=None, 
     return final_layer(g, h, temb)
 
 
+def model_forward_rows(cfg, g, blocks, latents, t_sin, pe, rows, kcache=None, vcache=None, mode=O.CANDLE):
+    """model_forward for the flat token rows `rows` of [B*S] only: every block
+    but the last over all tokens (the last block needs every token's K and V),
+    the last one through oracle.block_forward_rows, then the final layer on
+    those rows. Bit-identical to the same rows of model_forward. Returns
+    pred [len(rows), C]."""
+    temb = time_embed(g, t_sin)
+    mod = modulation(g, temb)
+    h = linear(g["img_in"], latents)
+    b, s, _ = h.shape
+    for i, w in enumerate(blocks[:-1]):
+        kp = None if kcache is None else kcache[i]
+        vp = None if vcache is None else vcache[i]
+        h, _, _ = O.block_forward(cfg, w, h, mod, pe, kp, vp, mode=mode)
+    rows = np.asarray(rows)
+    if blocks:
+        i = len(blocks) - 1
+        kp = None if kcache is None else kcache[i]
+        vp = None if vcache is None else vcache[i]
+        hr, _, _ = O.block_forward_rows(cfg, blocks[-1], h, mod, pe, rows, kp, vp, mode=mode)
+    else:
+        hr = h.reshape(b * s, -1)[rows]
+    out = np.empty((len(rows), h.shape[-1]), np.float32)
+    scale = linear(g["norm_out"], silu(temb))
+    for j, r in enumerate(rows):
+        out[j] = O.layernorm_mod(hr[j][None], scale[r // s])[0]
+    return linear(g["proj_out"], out)
+
+
 def assemble(txt_h, cond_h, pieces):
     """JointLayout::assemble narrowed to the prefix (src/joint_layout.rs:112-126)."""
     parts = [(txt_h if kind == 0 else cond_h)[:, st:st + n] for kind, st, n in pieces]

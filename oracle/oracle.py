@@ -20,8 +20,32 @@ CANDLE, EXACT = 0, 1
 _lib = None
 
 
+NATIVE_PATH = os.path.join(HERE, "_native", "liboracle_native.so")
+_isa = "x86-64-v3"
+
+
 def build():
     subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def use_native_build():
+    """Build the oracle for this host's own instruction set (-march=native,
+    always rebuilt here, never a copy made on another machine) and load it in
+    place of the portable x86-64-v3 build; for the timed CPU baseline. Must run
+    before the first lib() call. Returns the ISA label of the loaded build."""
+    global LIB_PATH, _isa
+    if _lib is not None:
+        return _isa
+    try:
+        subprocess.run(["make", "-s", "-B", "-C", HERE, "native"], check=True, capture_output=True, timeout=300)
+        LIB_PATH, _isa = NATIVE_PATH, "native"
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return _isa
+
+
+def isa():
+    return _isa
 
 
 def lib():

@@ -219,11 +219,11 @@ int qmatmul_check(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64
 int qimm_qmatmul(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_t m, int64_t lda, void *y,
                  int out_type, void *stream) {
     if (const int rc = qmatmul_check(ctx, w, x_bf16, m, lda, y, out_type)) return rc;
+    QIMM_HIP(ctx, hipSetDevice(ctx->device));
     qimm::EpiParams ep{};
     ep.out = y;
     ep.ldo = w->rows;
     if (const size_t need = qimm::qgemm_workspace(w->gw, m)) {
-        QIMM_HIP(ctx, hipSetDevice(ctx->device));
         const int rc = qimm_host::ensure_part_workspace(ctx, need);
         if (rc) return rc;
         ep.part_ws = (float *)ctx->ws_part;
@@ -238,6 +238,7 @@ int qimm_qmatmul(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_
 int qimm_qmatmul_noalloc(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16, int64_t m, int64_t lda, void *y,
                          int out_type, void *stream) {
     if (const int rc = qmatmul_check(ctx, w, x_bf16, m, lda, y, out_type)) return rc;
+    QIMM_HIP(ctx, hipSetDevice(ctx->device));
     qimm::EpiParams ep{};
     ep.out = y;
     ep.ldo = w->rows;
@@ -256,6 +257,12 @@ int qimm_qmatmul_noalloc(qimm_ctx *ctx, const qimm_weight *w, const void *x_bf16
                                      out_type == QIMM_TYPE_F32 ? qimm::EPI_F32 : qimm::EPI_BF16, ep,
                                      (hipStream_t)stream));
     return QIMM_OK;
+}
+
+int64_t qimm_qmatmul_scratch_bytes(const qimm_weight *w, int64_t m) {
+    if (!w || m < 0) return -1;
+    if (hipSetDevice(w->ctx->device) != hipSuccess) return -1;
+    return (int64_t)qimm::qgemm_workspace(w->gw, m);
 }
 
 }  // extern "C"

@@ -466,14 +466,14 @@ hipError_t launch_any(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t
 }  // namespace
 
 int device_cu_count() {
-    static int cus = -1;
-    if (cus < 0) {
+    // initialised once, by the first caller (a function-local static: thread-safe)
+    static const int cus = [] {
         int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-            cus = v;
-        else
-            cus = 0;
-    }
+        return (hipGetDevice(&dev) == hipSuccess &&
+                hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+                   ? v
+                   : 0;
+    }();
     return cus;
 }
 

@@ -47,6 +47,7 @@ SIGNATURES = [
     ("qimm_dequant", _i32, [_vp, _i32, _vp, _i64, _vp, _vp]),
     ("qimm_qmatmul", _i32, [_vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp]),
     ("qimm_qmatmul_noalloc", _i32, [_vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp]),
+    ("qimm_qmatmul_scratch_bytes", _i64, [_vp, _i64]),
     ("qimm_joint_layout", _i32, [_i64, _vp, _vp, _i64, _i64, _i64, _vp, _i64,
                                  C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i64)]),
     ("qimm_rope_table", _i32, [_vp, _i64, _vp, _i64, _vp, C.c_double, _vp]),
@@ -223,6 +224,10 @@ class Context:
         self.check(self.lib.qimm_quantize_act(self.h, weight_type, x_dev, m, k, ldx or k, out_dev, ldo or k, stream),
                    "qimm_quantize_act")
 
+    def qmatmul_scratch_bytes(self, w: "Weight", m: int) -> int:
+        """Device scratch bytes of the product of w with m rows (qimm_qmatmul_scratch_bytes)."""
+        return int(self.lib.qimm_qmatmul_scratch_bytes(w.h, m))
+
     # -- cache --
     def kv_create(self, layers: int, batch: int, heads: int, prefix_len: int, head_dim: int = 128) -> "KvCache":
         h = C.c_void_p()
@@ -396,7 +401,7 @@ def joint_layout(text_len: int, text_image_mask=None, cond_shapes=(), target=(1,
 
 
 def rope_table(shapes, image_mask, axes=(16, 56, 56), theta=10000.0):
-    """EmbedNd::forward restated host-side: returns a flat list pe[seq * sum(axes)]."""
+    """EmbedNd::forward restated host-side: returns pe [seq, sum(axes)] f32."""
     import numpy as np
     lib = load()
     seq = len(image_mask)

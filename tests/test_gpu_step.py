@@ -272,3 +272,74 @@ def test_model_rejects_bad_calls(torch_cuda, qctx):
     kv.free()
     m.free()
     blk.free()
+
+
+def test_model_full_size_prefix_fill_and_forward(torch_cuda, qctx):
+    """The step around the blocks at the reference's sizes (src/transformer.rs:63-79,
+    src/quantized_transformer.rs:36-81,213-228,288-310,359-392,471-551): hidden 4096,
+    32 heads, MLP 12288, joint dim 4096; the 256-token text prefix through txt_in
+    (RMSNorm + 1, GELU-tanh) and two Q4_K_M blocks under the t = 0 modulation into
+    the cache, then the cached forward of 4096 image tokens (img_in, the modulation
+    GEMV [16384 x 4096], the blocks, norm_out, proj_out). Sampled rows of the
+    prediction against oracle/model.py (blocks in candle mode, as the GPU blocks'
+    default): cosine >= 0.9999, max|a-b|/max|b| <= 2e-2; the cache layers against the
+    oracle's prefix pass."""
+    torch = torch_cuda
+    hid, heads, mlp, jd, ch, T, grid, layers = 4096, 32, 12288, 4096, 64, 256, 64, 2
+    cfg = dict(hidden=hid, heads=heads, head_dim=128, mlp=mlp)
+    s = grid * grid
+    print("case: model forward hidden 4096, joint dim 4096, 2 blocks, 4096 tokens over a 256-token prefix",
+          flush=True)
+    rng = np.random.default_rng(77)
+    g = {"img_in": synth.weight(rng, synth.F32, hid, ch, std=0.2),
+         "t_linear_1": synth.weight(rng, synth.Q8_0, hid, 256, std=0.05),
+         "t_linear_2": synth.weight(rng, synth.Q4_K, hid, hid, std=0.02),
+         "modulation": synth.weight(rng, synth.Q4_K, 4 * hid, hid, std=0.02),
+         "norm_out": synth.weight(rng, synth.BF16, hid, hid, std=0.02),
+         "proj_out": synth.weight(rng, synth.Q6_K, ch, hid, std=0.02),
+         "txt_norm": synth.weight(rng, synth.F32, 1, jd, std=0.1),
+         "txt_in": synth.weight(rng, synth.Q8_0, hid, jd, std=0.02),
+         "txt_out": synth.weight(rng, synth.Q8_0, hid, hid, std=0.02)}
+    blocks = [synth.block_weights(780 + i, hid, heads, mlp, synth.Q4_K, synth.Q6_K) for i in range(layers)]
+    keep = []
+    blk = [qctx.block_create(qimm.BlockConfig(hid, heads, 128, mlp), block_tensors(w, keep)) for w in blocks]
+    Tm = qimm.ModelTensors()
+    for name, (t, data, rows, cols) in g.items():
+        setattr(Tm, name, qimm.make_tensor(t, rows, cols, data.tobytes(), keep))
+    model = qctx.model_create(qimm.ModelConfig(ch, jd, hid, layers), Tm, blk)
+    txt = rng.standard_normal((1, T, jd)).astype(np.float32)
+    latents = rng.standard_normal((1, s, ch)).astype(np.float32)
+    ids, plen, _ = O.joint_layout(T, None, (), (grid, grid))
+    pe_full = O.rope_table([(1, grid, grid)], [i >= 0 for i in ids])
+    pieces = qimm.joint_layout_pieces(T)
+    kv = qctx.kv_create(layers, 1, heads, plen)
+    td, ped, idd = dev(torch, txt), dev(torch, pe_full[:plen]), dev(torch, np.array(ids[:plen], np.int32))
+    model.prefix_fill(td.data_ptr(), T, None, 0, 1, pieces, idd.data_ptr(), None, ped.data_ptr(), kv, stream(torch))
+    tsd = t_sin_dev(torch, qctx, [0.55])
+    lat, pe_t = dev(torch, latents), dev(torch, pe_full[plen:])
+    pred = torch.empty((1, s, ch), dtype=torch.float32, device="cuda")
+    model.forward(lat.data_ptr(), 1, s, tsd.data_ptr(), pe_t.data_ptr(), kv, pred.data_ptr(), None, stream(torch))
+    got = host(pred).reshape(s, ch)
+    kg = torch.empty((1, heads, plen, 128), dtype=torch.bfloat16, device="cuda")
+    vg = torch.empty_like(kg)
+    cache = []
+    for i in range(layers):
+        kv.load(i, kg.data_ptr(), vg.data_ptr(), stream(torch))
+        cache.append((host(kg.float()), host(vg.float())))
+    kv.free()
+    model.free()
+    for b_ in blk:
+        b_.free()
+    assert np.isfinite(got).all()
+    ref_cache = OM.prefix_fill(cfg, g, blocks, txt, None, pieces, ids[:plen], None, pe_full[:plen])
+    for (k, v), (kr, vr) in zip(cache, ref_cache):
+        for a, r in ((k, O.bf16_to_f32(kr)), (v, O.bf16_to_f32(vr))):
+            assert cos_sim(a, r) >= 0.9999 and max_abs_rel(a, r) <= 2e-2, (cos_sim(a, r), max_abs_rel(a, r))
+    rows = np.unique(np.concatenate([np.arange(4), np.random.default_rng(78).choice(s, 60, replace=False),
+                                     np.arange(s - 4, s)]))
+    ts = O.timestep_embedding(np.array([0.55], np.float32))
+    ref = OM.model_forward_rows(cfg, g, blocks, latents, ts, pe_full[plen:], rows, [k for k, _ in ref_cache],
+                                [v for _, v in ref_cache])
+    c, m = cos_sim(got[rows], ref), max_abs_rel(got[rows], ref)
+    print(f"prediction rows: cos {c:.7f} mar {m:.2e}", flush=True)
+    assert c >= 0.9999 and m <= 2e-2

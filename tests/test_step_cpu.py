@@ -227,3 +227,29 @@ def test_model_forward_without_blocks():
     assert np.abs(out - want).max() < 1e-5
     g["proj_out"] = _f32w(np.zeros((ch, hid)))
     assert not OM.model_forward(dict(hidden=hid), g, [], lat, t_sin, None).any()
+
+
+def test_model_forward_rows_equal_full_forward():
+    """The rows variant (every block but the last in full, the last through
+    block_forward_rows, the final layer per row) gives the listed rows of the
+    full forward bit for bit: two blocks, batch 2, a prefix cache, rows across
+    the batch boundary and unsorted."""
+    cfg = dict(hidden=256, heads=2, head_dim=128, mlp=512)
+    rng = np.random.default_rng(5)
+    h, ch, b, s, p = 256, 16, 2, 12, 8
+    g = {"img_in": synth.weight(rng, synth.F32, h, ch, std=0.2),
+         "t_linear_1": synth.weight(rng, synth.Q8_0, h, 256, std=0.05),
+         "t_linear_2": synth.weight(rng, synth.Q8_0, h, h, std=0.05),
+         "modulation": synth.weight(rng, synth.Q8_0, 4 * h, h, std=0.05),
+         "norm_out": synth.weight(rng, synth.F32, h, h, std=0.05),
+         "proj_out": synth.weight(rng, synth.F32, ch, h, std=0.05)}
+    blocks = [synth.block_weights(70 + i, h, 2, 512, synth.Q4_K, synth.Q6_K) for i in range(2)]
+    lat = rng.standard_normal((b, s, ch)).astype(np.float32)
+    ts = O.timestep_embedding(np.array([0.3, 0.8], np.float32))
+    pe = O.rope_table([(1, 3, 4)], [1] * s)
+    kc = [O.f32_to_bf16(rng.standard_normal((b, 2, p, 128))) for _ in range(2)]
+    vc = [O.f32_to_bf16(rng.standard_normal((b, 2, p, 128))) for _ in range(2)]
+    full = OM.model_forward(cfg, g, blocks, lat, ts, pe, kc, vc).reshape(b * s, ch)
+    rows = np.array([17, 0, 11, 12, 5, 23])
+    part = OM.model_forward_rows(cfg, g, blocks, lat, ts, pe, rows, kc, vc)
+    assert np.array_equal(part.view(np.uint32), full[rows].view(np.uint32))

@@ -131,24 +131,44 @@ __device__ __forceinline__ uint32_t bf16_of_product(float d, float q) {
 // Returns the four bf16 operands bf16(d * q) (bf16_of_product), packed in
 // pairs. Every lane of the block must take part (whole waves for 256, whole
 // 8-lane groups for 32); all-zero blocks give zeros, as candle's d = 0 does.
+// max over each aligned group of 8 lanes (a >= 0 or any floats): DPP moves
+// within quads (xor 1, xor 2), then the half-row mirror (lane i <-> 7 - i)
+template <int CTRL>
+__device__ __forceinline__ float dpp_fmax(float a) {
+    return fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), CTRL, 0xf, 0xf, false)));
+}
+__device__ __forceinline__ float max8_lanes(float a) {
+    a = dpp_fmax<0xb1>(a);      // quad_perm [1,0,3,2]
+    a = dpp_fmax<0x4e>(a);      // quad_perm [2,3,0,1]
+    return dpp_fmax<0x141>(a);  // row_half_mirror
+}
+// max over the wave, the same value in every lane: 8-lane groups, the row
+// mirror (16 lanes), then the four rows' values read as scalars
+__device__ __forceinline__ float max_wave(float a) {
+    a = dpp_fmax<0x140>(max8_lanes(a));  // row_mirror
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 template <int QBLK>
 __device__ __forceinline__ u32x2 quant_act4(f32x4 v) {
     static_assert(QBLK == 32 || QBLK == 256, "Q8_0 or Q8_K blocks");
     float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     float d, s;  // value = d * q, q from x * s
     if constexpr (QBLK == 256) {
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o));
+        a = max_wave(a);
         const int e = fabsf(v[0]) == a ? 0 : fabsf(v[1]) == a ? 1 : fabsf(v[2]) == a ? 2 : fabsf(v[3]) == a ? 3 : -1;
         const uint64_t hit = __ballot(e >= 0);
         const int first = hit ? (int)__builtin_ctzll(hit) : 0;
         const float mine = e == 0 ? v[0] : e == 1 ? v[1] : e == 2 ? v[2] : v[3];
-        const float xmax = __shfl(mine, first);
+        const float xmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), first));
         s = a == 0.f ? 0.f : -128.f / xmax;
         d = a == 0.f ? 0.f : 1.f / s;
     } else {
-#pragma unroll
-        for (int o = 4; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o));
+        a = max8_lanes(a);
         const float d32 = a / 127.f;
         s = d32 != 0.f ? 1.f / d32 : 0.f;
         d = (float)(_Float16)d32;

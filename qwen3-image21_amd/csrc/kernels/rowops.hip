@@ -2,6 +2,8 @@
 // adaLN modulation prep, LayerNorm*(1+scale) to bf16, per-head RmsNorm+RoPE
 // prep for standalone attention inputs, and the bf16 [S,D] <-> [D,S]
 // transpose used by the prefix cache.
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -91,7 +93,10 @@ __global__ void mod_prep_kernel(const float *__restrict__ mod, int64_t n, int64_
 // is a multiple of 256: whole waves are in or out of the row).
 constexpr int LN_MAXV = (int)(LN_MAX_HIDDEN / 4 / 256);  // float4 chunks per thread
 
-template <int QBLK>
+// NI > 0: hidden == 1024 NI, every thread holds NI chunks (no guards, so the
+// NI roundings of a thread are independent straight-line code the scheduler
+// interleaves); NI == 0: any hidden, guarded chunks.
+template <int QBLK, int NI>
 __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x, int64_t hidden,
                                                      const float *__restrict__ scale, int64_t stride,
                                                      int64_t rows_per, uint16_t *__restrict__ out) {
@@ -99,13 +104,13 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x
     const int64_t row = blockIdx.x;
     const int tid = threadIdx.x;
     const float *xr = x + row * hidden;
-    const int nv = (int)(hidden / 4);
+    const int nv = NI > 0 ? 256 * NI : (int)(hidden / 4);
     // the modulation row is loaded with x, so its latency overlaps the row's
     const float *sc = scale + (row / rows_per) * stride;
-    f32x4 v[LN_MAXV], sv[LN_MAXV];
+    f32x4 v[NI > 0 ? NI : LN_MAXV], sv[NI > 0 ? NI : LN_MAXV];
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < LN_MAXV; i++) {
+    for (int i = 0; i < (NI > 0 ? NI : LN_MAXV); i++) {
         const int c = tid + 256 * i;
         if (c < nv) {
             v[i] = *(const f32x4 *)(xr + 4 * c);
@@ -119,7 +124,7 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x
     const float mean = (red[0] + red[1] + red[2] + red[3]) / (float)hidden;
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < LN_MAXV; i++) {
+    for (int i = 0; i < (NI > 0 ? NI : LN_MAXV); i++) {
         const int c = tid + 256 * i;
         if (c < nv) {
 #pragma unroll
@@ -136,7 +141,7 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x
     const float rstd = 1.0f / sqrtf(var + 1e-6f);
     uint16_t *orow = out + row * hidden;
 #pragma unroll
-    for (int i = 0; i < LN_MAXV; i++) {
+    for (int i = 0; i < (NI > 0 ? NI : LN_MAXV); i++) {
         const int c = tid + 256 * i;
         if (c < nv) {
             const f32x4 s4 = sv[i];
@@ -153,20 +158,32 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x
 // ---- candle's activation quantization of f32 rows (QMatMul::forward's
 // quantize step, src/quantized_transformer.rs:19-29 -> candle-core 0.11
 // BlockQ8_0 / BlockQ8K::from_float) to the bf16 operands bf16(d * q) ----
-// One wave per 256 values of a row (four per lane): a Q8_K block, or eight
-// Q8_0 blocks. Rows of k values (k % 256 == 0 for Q8_K, k % 32 == 0 for
-// Q8_0; a row's last wave may be partial, whole 8-lane groups then idle).
+// One wave per QR_CH x 256 values of a row (four per lane and chunk, all
+// chunks' loads in flight before the first rounding): each chunk a Q8_K
+// block or eight Q8_0 blocks. Rows of k values (k % 256 == 0 for Q8_K,
+// k % 32 == 0 for Q8_0); chunks past the row end are zeros and not stored
+// (whole waves for Q8_K, whole 8-lane groups for Q8_0).
+constexpr int QR_CH = 4;
+
 template <int QBLK>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict__ x, int64_t ldx, int64_t m,
                                                          int64_t k, uint16_t *__restrict__ out, int64_t ldo) {
-    const int64_t wpr = (k + 255) / 256;
+    const int64_t wpr = (k + 256 * QR_CH - 1) / (256 * QR_CH);
     const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (gw >= m * wpr) return;  // whole waves
-    const int64_t row = gw / wpr, c = (gw % wpr) * 256 + 4 * (threadIdx.x & 63);
-    const bool ok = c < k;
-    const f32x4 v = ok ? *(const f32x4 *)(x + row * ldx + c) : f32x4{0.f, 0.f, 0.f, 0.f};
-    const u32x2 r = quant_act4<QBLK>(v);
-    if (ok) *(u32x2 *)(out + row * ldo + c) = r;
+    const int64_t row = gw / wpr, c0 = (gw % wpr) * (256 * QR_CH) + 4 * (threadIdx.x & 63);
+    f32x4 v[QR_CH];
+#pragma unroll
+    for (int j = 0; j < QR_CH; j++) {
+        const int64_t c = c0 + 256 * j;
+        v[j] = c < k ? *(const f32x4 *)(x + row * ldx + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < QR_CH; j++) {
+        const int64_t c = c0 + 256 * j;
+        const u32x2 r = quant_act4<QBLK>(v[j]);
+        if (c < k) *(u32x2 *)(out + row * ldo + c) = r;
+    }
 }
 
 // ---- per-head RmsNorm + RoPE prep (src/quantized_transformer.rs:137-142) ----
@@ -262,15 +279,25 @@ hipError_t launch_ln_mod(const float *x, int64_t m, int64_t hidden, const float 
     if (m <= 0) return hipSuccess;
     if (hidden > LN_MAX_HIDDEN || hidden % 4) return hipErrorInvalidValue;
     if (qblk && hidden % 256) return hipErrorInvalidValue;
+    if (qblk != 0 && qblk != 32 && qblk != 256) return hipErrorInvalidValue;
     const dim3 grid((unsigned)m), block(256);
-    if (qblk == 0)
-        ln_mod_kernel<0><<<grid, block, 0, stream>>>(x, hidden, scale, stride, rows_per, out);
-    else if (qblk == 32)
-        ln_mod_kernel<32><<<grid, block, 0, stream>>>(x, hidden, scale, stride, rows_per, out);
-    else if (qblk == 256)
-        ln_mod_kernel<256><<<grid, block, 0, stream>>>(x, hidden, scale, stride, rows_per, out);
-    else
-        return hipErrorInvalidValue;
+    auto go = [&](auto qb, auto ni) {
+        ln_mod_kernel<decltype(qb)::value, decltype(ni)::value>
+            <<<grid, block, 0, stream>>>(x, hidden, scale, stride, rows_per, out);
+    };
+    using Q0 = std::integral_constant<int, 0>;
+    using Q32 = std::integral_constant<int, 32>;
+    using Q256 = std::integral_constant<int, 256>;
+    auto by_q = [&](auto ni) {
+        if (qblk == 0) go(Q0{}, ni);
+        else if (qblk == 32) go(Q32{}, ni);
+        else go(Q256{}, ni);
+    };
+    switch (hidden % 1024 ? 0 : hidden / 1024) {
+    case 3: by_q(std::integral_constant<int, 3>{}); break;
+    case 4: by_q(std::integral_constant<int, 4>{}); break;
+    default: by_q(std::integral_constant<int, 0>{}); break;
+    }
     return hipGetLastError();
 }
 
@@ -279,7 +306,7 @@ hipError_t launch_quant_rows(const float *x, int64_t ldx, int64_t m, int64_t k, 
     if (m <= 0 || k <= 0) return hipSuccess;
     if ((qblk != 32 && qblk != 256) || k % qblk || k % 4 || ldx % 4 || ldo % 4 || ldx < k || ldo < k)
         return hipErrorInvalidValue;
-    const int64_t waves = m * ((k + 255) / 256);
+    const int64_t waves = m * ((k + 256 * QR_CH - 1) / (256 * QR_CH));
     const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
     if (qblk == 32)
         quant_rows_kernel<32><<<grid, block, 0, stream>>>(x, ldx, m, k, out, ldo);

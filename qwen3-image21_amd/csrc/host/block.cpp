@@ -140,6 +140,16 @@ int qimm_block_create(qimm_ctx *ctx, const qimm_block_config *cfg, const qimm_bl
         if (!rc) rc = tensor_to_f32(ctx, t->norm_q, D, nq);
         if (!rc) rc = tensor_to_f32(ctx, t->norm_k, D, nk);
         if (!rc) {
+            // ||RmsNorm(x) w|| <= sqrt(128) max|w|; q also carries 128^-1/2 log2 e
+            // (its epilogue scale); 2% covers RoPE's f32 rotation and bf16 rounding
+            float wq = 0.f, wk = 0.f;
+            for (float v : nq) wq = fmaxf(wq, fabsf(v));
+            for (float v : nk) wk = fmaxf(wk, fabsf(v));
+            b->q_norm_bound = wq * 1.4426950408889634f * 1.02f;
+            b->k_norm_bound = wk * sqrtf(128.0f) * 1.02f;
+            if (!(b->q_norm_bound < INFINITY) || !(b->k_norm_bound < INFINITY)) b->q_norm_bound = 0.f;
+        }
+        if (!rc) {
             hipError_t e = hipMalloc((void **)&b->norm_q, (size_t)D * 4);
             if (e == hipSuccess) e = hipMalloc((void **)&b->norm_k, (size_t)D * 4);
             if (e == hipSuccess) e = hipMemcpy(b->norm_q, nq.data(), (size_t)D * 4, hipMemcpyHostToDevice);
@@ -311,11 +321,15 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
     const int qb_out = act_qblk(blk, blk->out);
     float *stage_f32 = (float *)(ws + L.f32);
     float *att_f32 = qb_out ? stage_f32 : nullptr;
+    // score bound: q and own k from the RmsNorm weights, prefix k from the cache
+    const float *kpn = kv ? kv->knorm + layer : nullptr;
     if (img || kvalid)
         QIMM_HIP(ctx, qimm::launch_attention_masked(qb, pk, pvt, P, kb, vt, seq, batch, H, seq, 1.0f, img, kvalid,
-                                                    (int32_t *)(ws + L.lim), att, s, att_f32));
+                                                    (int32_t *)(ws + L.lim), att, s, att_f32, kpn,
+                                                    blk->q_norm_bound, blk->k_norm_bound));
     else
-        QIMM_HIP(ctx, qimm::launch_attention_log2(qb, pk, pvt, P, kb, vt, seq, batch, H, seq, att, s, att_f32));
+        QIMM_HIP(ctx, qimm::launch_attention_log2(qb, pk, pvt, P, kb, vt, seq, batch, H, seq, att, s, att_f32, kpn,
+                                                  blk->q_norm_bound, blk->k_norm_bound));
     if (kv) {
         const int rc = kv_release(kv, layer, s);
         if (rc) return rc;

@@ -5,6 +5,10 @@
 #include <algorithm>
 #include <new>
 
+#include <math.h>
+
+#include <vector>
+
 #include "internal.h"
 
 namespace qimm_host {
@@ -165,7 +169,20 @@ int kv_new(qimm_ctx *ctx, int64_t layers, int64_t batch, int64_t heads, int64_t 
     return QIMM_OK;
 }
 
+// The per-layer key-norm bounds, +inf (no bound) until a layer is stored.
+hipError_t kv_alloc_norms(qimm_kv *kv) {
+    hipError_t e = hipMalloc((void **)&kv->knorm, (size_t)kv->layers * 4);
+    if (e == hipSuccess) e = hipMalloc((void **)&kv->knorm_part, (size_t)kv->layers * qimm::QK_NORM_PARTS * 4);
+    if (e == hipSuccess) {
+        std::vector<float> inf((size_t)kv->layers, INFINITY);
+        e = hipMemcpy(kv->knorm, inf.data(), inf.size() * 4, hipMemcpyHostToDevice);
+    }
+    return e;
+}
+
 void kv_free(qimm_kv *kv) {
+    if (kv->knorm) (void)hipFree(kv->knorm);
+    if (kv->knorm_part) (void)hipFree(kv->knorm_part);
     if (kv->host) {
         if (kv->k) (void)hipHostFree(kv->k);
         if (kv->vt) (void)hipHostFree(kv->vt);
@@ -264,6 +281,7 @@ int qimm_kv_create(qimm_ctx *ctx, int64_t layers, int64_t batch, int64_t heads, 
         hipError_t e = hipSetDevice(ctx->device);
         if (e == hipSuccess) e = hipMalloc((void **)&kv->k, bytes);
         if (e == hipSuccess) e = hipMalloc((void **)&kv->vt, bytes);
+        if (e == hipSuccess) e = kv_alloc_norms(kv);
         if (e != hipSuccess) {
             kv_free(kv);
             return hip_err(ctx, e, "hipMalloc(kv cache)");
@@ -292,6 +310,7 @@ int qimm_kv_create_host(qimm_ctx *ctx, int64_t layers, int64_t batch, int64_t he
         if (e == hipSuccess) e = hipEventCreateWithFlags(&sl.released, hipEventDisableTiming);
     }
     if (e == hipSuccess) e = hipEventCreateWithFlags(&kv->written, hipEventDisableTiming);
+    if (e == hipSuccess) e = kv_alloc_norms(kv);
     if (e != hipSuccess) {
         kv_free(kv);
         return hip_err(ctx, e, "kv host cache allocation");
@@ -319,6 +338,9 @@ int qimm_kv_store_layer(qimm_kv *kv, int64_t layer, const uint16_t *k_bhpd, cons
     const int64_t n = kv->layer_elems();
     if (!n) return QIMM_OK;
     hipStream_t s = (hipStream_t)stream;
+    // the layer's largest key norm: the attention's score bound
+    QIMM_HIP(ctx, qimm::launch_row_norm_max(k_bhpd, n / 128, kv->knorm_part + layer * qimm::QK_NORM_PARTS,
+                                            kv->knorm + layer, s));
     if (!kv->host) {
         QIMM_HIP(ctx, hipMemcpyAsync(kv->k + layer * n, k_bhpd, (size_t)n * 2, hipMemcpyDeviceToDevice, s));
         QIMM_HIP(ctx, qimm::launch_transpose_sd(v_bhpd, kv->batch * kv->heads, kv->prefix, kv->vt + layer * n, 0, s));

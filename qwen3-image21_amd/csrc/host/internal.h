@@ -39,6 +39,11 @@ struct qimm_kv {
     uint16_t *k = nullptr;
     uint16_t *vt = nullptr;
     bool host = false;
+    // device [layers]: the largest key norm of each stored layer (+inf until
+    // stored), the attention's score bound; [layers][QK_NORM_PARTS] scratch of
+    // its reduction
+    float *knorm = nullptr;
+    float *knorm_part = nullptr;
     // Host cache: two device slots of one layer each. `ready` is recorded after
     // the copy into the slot, `released` after the last kernel reading it; a
     // copy into a slot waits for both, a reader waits for `ready`. `written` is
@@ -64,6 +69,10 @@ struct qimm_block {
     qimm_weight *gate_up = nullptr;      // rows interleaved per 64: gate | up
     qimm_weight *down = nullptr;
     float *norm_q = nullptr, *norm_k = nullptr;  // device [128]
+    // bounds of the q (softmax scale and log2 e folded in) and k norms after the
+    // q/k RmsNorm: sqrt(128) max|w| times those factors, with slack for RoPE
+    // and the bf16 rounding
+    float q_norm_bound = 0.f, k_norm_bound = 0.f;
     int act = QIMM_ACT_CANDLE;           // arithmetic at the quantized matmul inputs
     // stage timing (qimm_block_profile): events around the stages of a forward
     bool profiling = false;

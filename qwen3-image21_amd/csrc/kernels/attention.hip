@@ -31,6 +31,8 @@
 //    queries may see (key_limit_kernel).
 //  - attn_any_kernel (any lengths): 4 waves x 32 queries, K/V^T staged through
 //    registers with per-element bounds, the reference shape for ragged tails.
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -52,6 +54,20 @@ struct KeyMask {
     const uint8_t *kvalid;  // [B][kv_len]; null: every key valid
     int64_t kv_len;
 };
+
+// A bound on every score (log2 units): q_norm >= max ||q|| (as the kernel
+// sees q, scale folded in), k_own >= max ||k|| of the own keys, *k_prefix >= max
+// ||k|| of the prefix keys (null: no prefix). When q_norm * max(k_own,
+// *k_prefix) <= STATIC_MAX every |score| <= STATIC_MAX (Cauchy-Schwarz), and
+// the kernel takes p = exp2(score) against the fixed reference 0: no running
+// maximum, no rescaling. exp2 of at most 2^STATIC_MAX summed over any key count
+// stays far below f32 overflow, and floating-point sums keep their relative
+// precision at any scale, so the result is the softmax's. q_norm = 0 disables.
+struct ScoreBound {
+    const float *k_prefix;
+    float q_norm, k_own;
+};
+constexpr float STATIC_MAX = 64.0f;
 
 // v_permlane32_swap exchanges the upper 32 lanes of its first operand with
 // the lower 32 lanes of its second; with both operands holding x, each lane
@@ -162,7 +178,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
                                                                     int64_t H, int64_t Sq, int64_t nq, int64_t B,
                                                                     float sl2, uint16_t *__restrict__ out,
                                                                     float *__restrict__ outf, KeyMask km,
-                                                                    const int32_t *__restrict__ lim) {
+                                                                    const int32_t *__restrict__ lim,
+                                                                    ScoreBound sb) {
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int QB = 32 * NW;  // queries per workgroup
     constexpr int DI = 16 / NW;  // DMA instructions per wave per 16 KB tile
@@ -331,8 +348,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
     // id of window key kv, kb0: index of the window's first key, partial: test
     // each score (MASKED only)
     auto half_step = [&](const uint8_t *stg, int h, int lo, int hi, uint64_t kmask, int kid, int kb0,
-                         bool partial) __attribute__((always_inline)) {
-        f32x16 st = negm;
+                         bool partial, auto stat) __attribute__((always_inline)) {
+        constexpr bool STATIC = decltype(stat)::value;
+        f32x16 st;
+        if constexpr (STATIC) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) st[r] = 0.f;
+        } else {
+            st = negm;
+        }
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
             const bf16x8 a = *(const bf16x8 *)(stg + h * 32 * 256 + kaddr[kk]);
@@ -372,6 +396,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
                 }
             }
         }
+        if constexpr (!STATIC) {
         float m0 = st[0], m1 = st[1];
 #pragma unroll
         for (int r = 2; r < 16; r += 2) {
@@ -416,6 +441,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
                 negm[r] = -m_run;
             }
         }
+        }  // !STATIC
         uint32_t pk[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -448,7 +474,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
     };
 
     // block j computes from stage cur while block j+1 streams into the other
-    auto step = [&](int j, int cur) __attribute__((always_inline)) {
+    auto step = [&](int j, int cur, auto stat) __attribute__((always_inline)) {
         const Blk b = blk_of(j);
         int kid = 0, kb0 = 0;
         uint64_t kmask = 0;
@@ -475,8 +501,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
         if (j + 1 < nblk) dma(blk_of(j + 1), cur ^ 1);
         const uint8_t *stg = lds + cur * STAGE;
         if (!skip) {
-            half_step(stg, 0, b.lo, b.hi, kmask, kid, kb0, partial);
-            half_step(stg, 1, b.lo, b.hi, kmask, kid, kb0, partial);
+            half_step(stg, 0, b.lo, b.hi, kmask, kid, kb0, partial, stat);
+            half_step(stg, 1, b.lo, b.hi, kmask, kid, kb0, partial, stat);
         }
         __builtin_amdgcn_s_waitcnt(WAIT_VM0);  // vmcnt(0): block j+1 landed
         __syncthreads();
@@ -488,12 +514,24 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
     }
     __builtin_amdgcn_s_waitcnt(WAIT_VM0);
     __syncthreads();
-    int j = 0;
-    for (; j + 1 < nblk; j += 2) {
-        step(j, 0);
-        step(j + 1, 1);
+    // the fixed-reference form when the score bound allows it (wave-uniform)
+    bool stat_ok = false;
+    if (sb.q_norm > 0.f) {
+        const float kn = sb.k_prefix ? fmaxf(sb.k_own, *sb.k_prefix) : sb.k_own;
+        stat_ok = sb.q_norm * kn <= STATIC_MAX;
     }
-    if (j < nblk) step(j, 0);
+    auto run = [&](auto stat) __attribute__((always_inline)) {
+        int j = 0;
+        for (; j + 1 < nblk; j += 2) {
+            step(j, 0, stat);
+            step(j + 1, 1, stat);
+        }
+        if (j < nblk) step(j, 0, stat);
+    };
+    if (stat_ok)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
 
     // normalize and stage O [32 q x 128 d] per wave through LDS for row stores
     const float l_tot = xsum32(l_run);
@@ -756,10 +794,10 @@ __global__ __launch_bounds__(256, 2) void attn_any_kernel(const uint16_t *__rest
 
 template <int NW, bool PRE, bool MASKED>
 void launch_fast(const uint16_t *q, Seg s0, Seg s1, int64_t h, int64_t sq, int64_t b, float sl2, uint16_t *out,
-                 float *outf, const KeyMask &km, const int32_t *lim, hipStream_t stream) {
+                 float *outf, const KeyMask &km, const int32_t *lim, const ScoreBound &sb, hipStream_t stream) {
     const int64_t nq = (sq + 32 * NW - 1) / (32 * NW);
     fast::attn_fast_kernel<NW, PRE, MASKED><<<dim3((unsigned)(nq * h * b)), dim3(64 * NW), 0, stream>>>(
-        q, s0, s1, h, sq, nq, b, sl2, out, outf, km, lim);
+        q, s0, s1, h, sq, nq, b, sl2, out, outf, km, lim, sb);
 }
 
 // Waves per workgroup of the unmasked fast kernel, from the rounds each form
@@ -784,7 +822,7 @@ int fast_waves(int64_t bh, int64_t sq) {
 template <bool PRE>
 hipError_t launch(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p, const uint16_t *ko,
                   const uint16_t *vto, int64_t so, int64_t b, int64_t h, int64_t sq, float sl2, uint16_t *out,
-                  float *outf, hipStream_t stream) {
+                  float *outf, const ScoreBound &sb, hipStream_t stream) {
     if (sq <= 0 || b <= 0 || h <= 0) return hipSuccess;
     if (p < 0 || so < 0 || p + so <= 0) return hipErrorInvalidValue;
     Seg s0{kp, vtp, p}, s1{ko, vto, so};
@@ -795,9 +833,9 @@ hipError_t launch(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, in
     if ((p & 7) == 0 && (so & 7) == 0) {
         const KeyMask km{nullptr, nullptr, p + so};
         if (fast_waves(b * h, sq) == 4)
-            launch_fast<4, PRE, false>(q, s0, s1, h, sq, b, sl2, out, outf, km, nullptr, stream);
+            launch_fast<4, PRE, false>(q, s0, s1, h, sq, b, sl2, out, outf, km, nullptr, sb, stream);
         else
-            launch_fast<8, PRE, false>(q, s0, s1, h, sq, b, sl2, out, outf, km, nullptr, stream);
+            launch_fast<8, PRE, false>(q, s0, s1, h, sq, b, sl2, out, outf, km, nullptr, sb, stream);
     } else {
         const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;
         anylen::attn_any_kernel<false><<<dim3((unsigned)(nq * h * b)), dim3(256), 0, stream>>>(
@@ -811,13 +849,15 @@ hipError_t launch(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, in
 hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
                             const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
                             int64_t sq, float scale, uint16_t *out, hipStream_t stream, float *outf) {
-    return launch<false>(q, kp, vtp, p, ko, vto, so, b, h, sq, scale * 1.4426950408889634f, out, outf, stream);
+    return launch<false>(q, kp, vtp, p, ko, vto, so, b, h, sq, scale * 1.4426950408889634f, out, outf,
+                         ScoreBound{nullptr, 0.f, 0.f}, stream);
 }
 
 hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
                                    const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
                                    int64_t sq, float sl2, const int32_t *img, const uint8_t *kvalid,
-                                   int32_t *lim_scratch, uint16_t *out, hipStream_t stream, float *outf) {
+                                   int32_t *lim_scratch, uint16_t *out, hipStream_t stream, float *outf,
+                                   const float *k_prefix_norm, float q_norm, float k_own_norm) {
     if (sq <= 0 || b <= 0 || h <= 0) return hipSuccess;
     if (p < 0 || so < 0 || p + so <= 0) return hipErrorInvalidValue;
     if (img && (p != 0 || so != sq)) return hipErrorInvalidValue;  // block-causal: one shared sequence
@@ -833,7 +873,13 @@ hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const 
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
-        launch_fast<8, false, true>(q, s0, s1, h, sq, b, sl2, out, outf, km, img ? lim_scratch : nullptr, stream);
+        // the bound is on scores in log2 units: q's norm times sl2
+        const ScoreBound sb{p > 0 ? k_prefix_norm : nullptr, q_norm * sl2, k_own_norm};
+        // sl2 == 1: q already carries the scale (the block's q/k/v epilogue)
+        if (sl2 == 1.0f)
+            launch_fast<8, true, true>(q, s0, s1, h, sq, b, sl2, out, outf, km, img ? lim_scratch : nullptr, sb, stream);
+        else
+            launch_fast<8, false, true>(q, s0, s1, h, sq, b, sl2, out, outf, km, img ? lim_scratch : nullptr, sb, stream);
         return hipGetLastError();
     }
     const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;
@@ -844,8 +890,10 @@ hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const 
 
 hipError_t launch_attention_log2(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
                                  const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
-                                 int64_t sq, uint16_t *out, hipStream_t stream, float *outf) {
-    return launch<true>(q, kp, vtp, p, ko, vto, so, b, h, sq, 1.0f, out, outf, stream);
+                                 int64_t sq, uint16_t *out, hipStream_t stream, float *outf,
+                                 const float *k_prefix_norm, float q_norm, float k_own_norm) {
+    return launch<true>(q, kp, vtp, p, ko, vto, so, b, h, sq, 1.0f, out, outf,
+                        ScoreBound{p > 0 ? k_prefix_norm : nullptr, q_norm, k_own_norm}, stream);
 }
 
 }  // namespace qimm

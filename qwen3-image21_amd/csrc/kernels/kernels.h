@@ -150,13 +150,26 @@ hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const 
                                    const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
                                    int64_t sq, float sl2, const int32_t *img, const uint8_t *kvalid,
                                    int32_t *lim_scratch, uint16_t *out, hipStream_t stream,
-                                   float *outf = nullptr);
+                                   float *outf = nullptr, const float *k_prefix_norm = nullptr,
+                                   float q_norm = 0.f, float k_own_norm = 0.f);
 // The same with q already multiplied by scale * log2(e) (the QKV epilogue's
 // q_scale), so scores are in log2 units.
 hipError_t launch_attention_log2(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp,
                                  int64_t p, const uint16_t *ko, const uint16_t *vto, int64_t so,
                                  int64_t b, int64_t h, int64_t sq, uint16_t *out, hipStream_t stream,
-                                 float *outf = nullptr);
+                                 float *outf = nullptr, const float *k_prefix_norm = nullptr,
+                                 float q_norm = 0.f, float k_own_norm = 0.f);
+// Score bound of the fast kernels (both launches above): with q_norm >= every
+// query's norm (as passed, before sl2), k_own_norm >= every own key's norm and,
+// when there is a prefix, *k_prefix_norm (device) >= every prefix key's norm,
+// a bound q_norm * sl2 * max(k norms) <= 64 on the scores in log2 units lets
+// the kernel drop the running maximum (a fixed softmax reference). q_norm 0:
+// always the running-maximum form.
+
+// out_dev[0] = the largest Euclidean norm of the rows of k [rows][128] bf16
+// (f32 sums), through part (>= QK_NORM_PARTS floats of device scratch).
+constexpr int QK_NORM_PARTS = 1024;
+hipError_t launch_row_norm_max(const uint16_t *k, int64_t rows, float *part, float *out_dev, hipStream_t stream);
 
 // Per-head RmsNorm + RoPE of raw projections x [B,S,H,128] (f32) into the
 // attention layouts; mode 0: q/k -> [B,H,S,128]; mode 1: v -> vt [B,H,128,S].

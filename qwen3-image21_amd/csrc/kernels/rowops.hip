@@ -2,6 +2,7 @@
 // adaLN modulation prep, LayerNorm*(1+scale) to bf16, per-head RmsNorm+RoPE
 // prep for standalone attention inputs, and the bf16 [S,D] <-> [D,S]
 // transpose used by the prefix cache.
+#include <algorithm>
 #include <type_traits>
 
 #include "device_common.h"
@@ -186,6 +187,45 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
     }
 }
 
+// ---- the largest key norm of a cache layer (the attention's score bound) ----
+// Two passes, no atomics: workgroup g takes rows g, g + G, ... (16 lanes per
+// row of 128 bf16, 16 rows per workgroup step) and writes its maximum; one
+// workgroup then reduces the G partial maxima.
+__global__ __launch_bounds__(256) void row_norm_part_kernel(const uint16_t *__restrict__ k, int64_t rows,
+                                                            float *__restrict__ part) {
+    __shared__ float red[16];
+    const int tid = threadIdx.x, sub = tid & 15;
+    float best = 0.f;
+    for (int64_t r = (int64_t)blockIdx.x * 16 + (tid >> 4); r < rows; r += (int64_t)gridDim.x * 16) {
+        const u32x4 v = *(const u32x4 *)(k + r * 128 + sub * 8);
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float a = bf16_bits_to_f32(v[i] & 0xffffu), b = bf16_bits_to_f32(v[i] >> 16);
+            ss += a * a + b * b;
+        }
+        best = fmaxf(best, sqrtf(group_sum(ss, 16)));
+    }
+    if (sub == 0) red[tid >> 4] = best;  // the 16 lanes of a row group hold the same value
+    __syncthreads();
+    if (tid == 0) {
+        float m = red[0];
+        for (int i = 1; i < 16; i++) m = fmaxf(m, red[i]);
+        part[blockIdx.x] = m;
+    }
+}
+
+__global__ __launch_bounds__(256) void max_reduce_kernel(const float *__restrict__ part, int n,
+                                                         float *__restrict__ out) {
+    __shared__ float red[4];
+    float m = 0.f;
+    for (int i = threadIdx.x; i < n; i += 256) m = fmaxf(m, part[i]);
+    m = max_wave(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) out[0] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
 // ---- per-head RmsNorm + RoPE prep (src/quantized_transformer.rs:137-142) ----
 // x [B,S,H,128] f32. mode 0: out [B,H,S,128] bf16 after norm (w) and RoPE
 // (pe [S,128]); mode 1 (values): out = vt [B,H,128,S] bf16, no norm.
@@ -312,6 +352,13 @@ hipError_t launch_quant_rows(const float *x, int64_t ldx, int64_t m, int64_t k, 
         quant_rows_kernel<32><<<grid, block, 0, stream>>>(x, ldx, m, k, out, ldo);
     else
         quant_rows_kernel<256><<<grid, block, 0, stream>>>(x, ldx, m, k, out, ldo);
+    return hipGetLastError();
+}
+
+hipError_t launch_row_norm_max(const uint16_t *k, int64_t rows, float *part, float *out_dev, hipStream_t stream) {
+    const int64_t g = std::min<int64_t>(QK_NORM_PARTS, std::max<int64_t>(1, (rows + 15) / 16));
+    row_norm_part_kernel<<<dim3((unsigned)g), dim3(256), 0, stream>>>(k, rows, part);
+    max_reduce_kernel<<<dim3(1), dim3(256), 0, stream>>>(part, (int)g, out_dev);
     return hipGetLastError();
 }
 

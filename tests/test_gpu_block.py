@@ -142,6 +142,20 @@ def test_block_mixed_qkv_types_unfused_path(torch_cuda, qctx):
     check_modes(SMALL, w, x, mod, pe, kpre, vpre, runs, want_kv=True)
 
 
+def test_block_large_norm_weights_running_max_path(torch_cuda, qctx):
+    """q/k RmsNorm weights of magnitude ~3 (a score bound of ~150 in log2 units,
+    above the attention's fixed-reference limit of 64): the attention keeps the
+    running maximum; the small-weight cases elsewhere take the fixed reference.
+    Both modes against the oracle, with a prefix cache and without."""
+    for p in (32, 0):
+        w, x, mod, pe, kpre, vpre = make_case(13 + p, SMALL, 1, 96, p, synth.Q4_K, synth.Q6_K)
+        rng = np.random.default_rng(131 + p)
+        w["norm_q"] = (3.0 + 0.3 * rng.standard_normal(128)).astype(np.float32)
+        w["norm_k"] = (3.0 + 0.3 * rng.standard_normal(128)).astype(np.float32)
+        runs = run_modes(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre, want_kv=True)
+        check_modes(SMALL, w, x, mod, pe, kpre, vpre, runs, want_kv=True)
+
+
 def test_block_deterministic(torch_cuda, qctx):
     w, x, mod, pe, kpre, vpre = make_case(9, SMALL, 1, 96, 32, synth.Q4_K, synth.Q6_K)
     a, _ = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre)

@@ -160,13 +160,6 @@ def main():
     assert torch.isfinite(x_out).all().item(), "non-finite block output"
     log(f"bench: block step {ms_step:.3f} ms (wall {wall * 1e3 / args.steps:.3f} ms)")
 
-    # ---- the same step with bf16 activations (no int8 rounding, no f32 staging) ----
-    for blk in blocks:
-        blk.set_act_mode(qimm.ACT_BF16)
-    ms_bf16 = timed(torch, stream, lambda it=iter(range(1 << 30)): step(next(it)), max(8, args.steps // 2), warmup=2)
-    for blk in blocks:
-        blk.set_act_mode(qimm.ACT_CANDLE)
-    log(f"bench: block step with bf16 activations {ms_bf16:.3f} ms")
 
     # ---- per-stage device times inside the step (HIP events on the launch stream) ----
     stage_sum, nprof = {}, 0
@@ -188,6 +181,14 @@ def main():
         kernels, roofline = stage_report(stages, att_flop, synth)
 
     block_flop = att_flop + 2.0 * S_IMG * HID * (3 * HID + HID + 2 * MLP) + 2.0 * S_IMG * MLP * HID
+
+    # ---- the same step with bf16 activations (no int8 rounding, no f32 staging) ----
+    for blk in blocks:
+        blk.set_act_mode(qimm.ACT_BF16)
+    ms_bf16 = timed(torch, stream, lambda it=iter(range(1 << 30)): step(next(it)), max(8, args.steps // 2), warmup=2)
+    for blk in blocks:
+        blk.set_act_mode(qimm.ACT_CANDLE)
+    log(f"bench: block step with bf16 activations {ms_bf16:.3f} ms")
 
     # ---- weight streaming at short token counts (the HBM-bound regime) ----
     streaming = None if args.no_weight_streaming else weight_streaming(ctx, torch, np, qimm, synth, stream, host_w0)

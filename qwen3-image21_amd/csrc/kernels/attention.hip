@@ -461,6 +461,48 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
         }
     };
 
+    // The fixed-reference form without a mask, split so that both halves'
+    // scores come first: the exponentials of half 0 then issue while half 1's
+    // QK MFMAs are still in the matrix pipe, and those of half 1 while half 0's
+    // PV MFMAs run.
+    auto qk_static = [&](const uint8_t *stg, int h) __attribute__((always_inline)) {
+        f32x16 st;
+#pragma unroll
+        for (int r = 0; r < 16; r++) st[r] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+            const bf16x8 a = *(const bf16x8 *)(stg + h * 32 * 256 + kaddr[kk]);
+            st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], st, 0, 0, 0);
+        }
+        return st;
+    };
+    auto pv_static = [&](const uint8_t *stg, int h, f32x16 st, int lo, int hi) __attribute__((always_inline)) {
+        if (lo > h * 32 || hi < h * 32 + 32) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int kv = h * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
+                if (kv < lo || kv >= hi) st[r] = -INFINITY;
+            }
+        }
+        uint32_t pk[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float a = PRE ? st[2 * i] : st[2 * i] * sl2;
+            const float b = PRE ? st[2 * i + 1] : st[2 * i + 1] * sl2;
+            pk[i] = pack_bf16x2(__builtin_amdgcn_exp2f(a), __builtin_amdgcn_exp2f(b));
+            l_run = dot2_ones(pk[i], l_run);
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+            const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pk[4 * kk], pk[4 * kk + 1], pk[4 * kk + 2], pk[4 * kk + 3]});
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                const bf16x8 a = *(const bf16x8 *)(stg + dt * 32 * 128 + vaddr[h][kk]);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf, o[dt], 0, 0, 0);
+            }
+        }
+    };
+
     // MASKED: lane kv loads the image id of window key kv (0 without ids), or
     // KEY_OFF for a padded key, one block ahead; waited for with the tiles.
     constexpr int KEY_OFF = -0x7fffffff - 1;
@@ -500,7 +542,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
         }
         if (j + 1 < nblk) dma(blk_of(j + 1), cur ^ 1);
         const uint8_t *stg = lds + cur * STAGE;
-        if (!skip) {
+        if constexpr (decltype(stat)::value && !MASKED) {
+            const f32x16 s0 = qk_static(stg, 0), s1 = qk_static(stg, 1);
+            pv_static(stg, 0, s0, b.lo, b.hi);
+            pv_static(stg, 1, s1, b.lo, b.hi);
+        } else if (!skip) {
             half_step(stg, 0, b.lo, b.hi, kmask, kid, kb0, partial, stat);
             half_step(stg, 1, b.lo, b.hi, kmask, kid, kb0, partial, stat);
         }

@@ -84,6 +84,13 @@ hipError_t launch_qgemm_stream(const GemmWeight &w, const uint16_t *a, int64_t m
                                const EpiParams &ep, float *work, hipStream_t stream);
 hipError_t launch_qgemm_large(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda,
                               int epi, const EpiParams &ep, hipStream_t stream);
+// The large-M kernel for quantized weights (Q4_K, Q6_K, Q8_0 with K % 256 == 0
+// and N % 256 == 0): eight waves per 256x256 tile, each decoding its own 32
+// weight rows into registers. launch_qgemm_large takes it where it fits (the
+// q/k/v epilogue also needs hidden % 256 == 0).
+bool qgemm_wide_fits(const GemmWeight &w);
+hipError_t launch_qgemm_wide(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
+                             const EpiParams &ep, hipStream_t stream);
 // Sum of split-K partials part[splits][m][N] (f32) in split order, with the
 // epilogue epi applied (the second kernel of the split paths).
 hipError_t launch_split_epilogue(const float *part, int splits, int64_t m, int64_t N, int epi, const EpiParams &ep,

@@ -1,5 +1,7 @@
 // Large-M dequant-GEMM for gfx950 (M >= 512 token rows): C = A (bf16) x W^T
-// (GGUF blocks), same epilogues as the 128x128 kernel.
+// (GGUF blocks), same epilogues as the 128x128 kernel. Quantized weights with
+// K % 256 == 0 take the eight-wave kernel of qgemm_wide.hip instead; this one
+// serves bf16-stored weights and the remaining quantized shapes.
 //
 // Replaces candle's QMatMul::forward (src/quantized_transformer.rs:19-33) on
 // the block's token-parallel projections (call sites 133-135, 151, 196, 202).
@@ -679,6 +681,8 @@ bool qgemm_large_fits(const GemmWeight &w, int64_t m) {
 
 hipError_t launch_qgemm_large(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
                               const EpiParams &ep, hipStream_t stream) {
+    if (qgemm_wide_fits(w) && (epi != EPI_QKV || ep.hidden % BN == 0))
+        return launch_qgemm_wide(w, a, m, lda, epi, ep, stream);
     switch (w.fmt) {
     case WF_Q8_0: return launch_fmt<WF_Q8_0>(w, a, m, lda, epi, ep, stream);
     case WF_Q4_K: return launch_fmt<WF_Q4_K>(w, a, m, lda, epi, ep, stream);

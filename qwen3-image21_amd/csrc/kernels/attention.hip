@@ -173,7 +173,11 @@ constexpr float RESCALE_TH = 8.0f;    // log2 units
 // holds 8-key chunk c at slot c ^ ((d / 2) % 8). A 16-lane phase of b128 reads
 // (16 rows, one chunk) then covers all 64 banks once.
 // Two waves per SIMD either way: one 8-wave or two 4-wave workgroups per CU.
-template <int NW, bool PRE, bool MASKED>
+// SMODE: 0 = the softmax reference is chosen in the kernel from the score
+// bound (the prefix keys' norm is a device value); 1 = fixed reference, 2 =
+// running maximum, both decided on the host. A kernel with one form has only
+// that loop's registers to allocate.
+template <int NW, bool PRE, bool MASKED, int SMODE>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16_t *__restrict__ q, Seg s0, Seg s1,
                                                                     int64_t H, int64_t Sq, int64_t nq, int64_t B,
                                                                     float sl2, uint16_t *__restrict__ out,
@@ -191,13 +195,22 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
     // XCD-aware order: workgroups are dealt round-robin over 8 XCDs; each XCD
     // gets a contiguous range of (batch, head, query tile) so the query tiles
     // of one head share that XCD's L2 copy of its K/V.
+    // Under a key limit later query tiles see more keys: they are dispatched
+    // first (query tile major in block order, from the last), so that the short
+    // tiles fill the tail; workgroup b takes (batch, head) b % (B H), which
+    // keeps a head on one XCD when B H is a multiple of 8.
     const int64_t total = nq * H * B;
     int64_t L = blockIdx.x;
-    if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
-    // under a key limit later query tiles see more keys: they start first, so
-    // that the short tiles fill the tail
-    const int64_t qt = (MASKED && lim) ? nq - 1 - L % nq : L % nq, hh = (L / nq) % H, bb = L / (nq * H);
-    const int64_t bh = bb * H + hh;
+    int64_t qt, bh;
+    if (MASKED && lim) {
+        qt = nq - 1 - L / (H * B);
+        bh = L % (H * B);
+    } else {
+        if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
+        qt = L % nq;
+        bh = L / nq;
+    }
+    const int64_t hh = bh % H, bb = bh / H;
     const int64_t q0 = qt * QB + wave * 32;
 
     // Q^T fragments (B operand): lane holds query q0+l32, d = 16kk + 8g .. +8
@@ -574,10 +587,16 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
         }
         if (j < nblk) step(j, 0, stat);
     };
-    if (stat_ok)
+    if constexpr (SMODE == 1) {
         run(std::true_type{});
-    else
+    } else if constexpr (SMODE == 2) {
         run(std::false_type{});
+    } else {
+        if (stat_ok)
+            run(std::true_type{});
+        else
+            run(std::false_type{});
+    }
 
     // normalize and stage O [32 q x 128 d] per wave through LDS for row stores
     const float l_tot = xsum32(l_run);
@@ -838,12 +857,27 @@ __global__ __launch_bounds__(256, 2) void attn_any_kernel(const uint16_t *__rest
 
 }  // namespace anylen
 
-template <int NW, bool PRE, bool MASKED>
+template <int NW, bool PRE, bool MASKED, int SMODE = 0>
 void launch_fast(const uint16_t *q, Seg s0, Seg s1, int64_t h, int64_t sq, int64_t b, float sl2, uint16_t *out,
                  float *outf, const KeyMask &km, const int32_t *lim, const ScoreBound &sb, hipStream_t stream) {
     const int64_t nq = (sq + 32 * NW - 1) / (32 * NW);
-    fast::attn_fast_kernel<NW, PRE, MASKED><<<dim3((unsigned)(nq * h * b)), dim3(64 * NW), 0, stream>>>(
+    fast::attn_fast_kernel<NW, PRE, MASKED, SMODE><<<dim3((unsigned)(nq * h * b)), dim3(64 * NW), 0, stream>>>(
         q, s0, s1, h, sq, nq, b, sl2, out, outf, km, lim, sb);
+}
+
+// The masked kernel with the softmax form decided on the host where the score
+// bound needs no device value (no prefix keys).
+template <bool PRE>
+void launch_masked(const uint16_t *q, Seg s0, Seg s1, int64_t h, int64_t sq, int64_t b, float sl2, uint16_t *out,
+                   float *outf, const KeyMask &km, const int32_t *lim, const ScoreBound &sb, hipStream_t stream) {
+    if (sb.q_norm <= 0.f)
+        launch_fast<8, PRE, true, 2>(q, s0, s1, h, sq, b, sl2, out, outf, km, lim, sb, stream);
+    else if (sb.k_prefix)
+        launch_fast<8, PRE, true, 0>(q, s0, s1, h, sq, b, sl2, out, outf, km, lim, sb, stream);
+    else if (sb.q_norm * sb.k_own <= STATIC_MAX)
+        launch_fast<8, PRE, true, 1>(q, s0, s1, h, sq, b, sl2, out, outf, km, lim, sb, stream);
+    else
+        launch_fast<8, PRE, true, 2>(q, s0, s1, h, sq, b, sl2, out, outf, km, lim, sb, stream);
 }
 
 // Waves per workgroup of the unmasked fast kernel, from the rounds each form
@@ -923,9 +957,9 @@ hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const 
         const ScoreBound sb{p > 0 ? k_prefix_norm : nullptr, q_norm * sl2, k_own_norm};
         // sl2 == 1: q already carries the scale (the block's q/k/v epilogue)
         if (sl2 == 1.0f)
-            launch_fast<8, true, true>(q, s0, s1, h, sq, b, sl2, out, outf, km, img ? lim_scratch : nullptr, sb, stream);
+            launch_masked<true>(q, s0, s1, h, sq, b, sl2, out, outf, km, img ? lim_scratch : nullptr, sb, stream);
         else
-            launch_fast<8, false, true>(q, s0, s1, h, sq, b, sl2, out, outf, km, img ? lim_scratch : nullptr, sb, stream);
+            launch_masked<false>(q, s0, s1, h, sq, b, sl2, out, outf, km, img ? lim_scratch : nullptr, sb, stream);
         return hipGetLastError();
     }
     const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;

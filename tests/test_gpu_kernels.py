@@ -76,9 +76,11 @@ def _gemm_case(torch, qctx, t, m, n, k, seed, out_type=synth.F32, std=0.02):
                                    (16, 384, 4096), (33, 256, 1024), (64, 128, 8192),
                                    (130, 384, 1024), (300, 128, 4096),
                                    (600, 512, 1024), (1024, 256, 768),
-                                   # 256x256 kernel (more 128x128 tiles than two per CU); bf16
-                                   # weights there take the direct global->LDS operand path
-                                   (2304, 4096, 256)])
+                                   # 256x256 kernels (more 128x128 tiles than two per CU): the
+                                   # eight-wave kernel for the quantized formats, one super-block and
+                                   # four (every Q6_K scale-pair and half position, negative scales);
+                                   # bf16 weights take the four-wave kernel's direct global->LDS path
+                                   (2304, 4096, 256), (2304, 4096, 1024)])
 def test_qmatmul_matches_bf16_weight_products(torch_cuda, qctx, t, m, n, k):
     """Products of the bf16 activations and the weights each path multiplies:
     bf16-rounded dequantized weights on the MFMA dequant paths, the exact Q4_K

@@ -334,23 +334,32 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
             __builtin_amdgcn_sched_barrier(0);
         };
         rd(0, 0, 0);
+        ws.template scales<0>();
+        bf16x8 wf0 = ws.template frag<0>(0);  // slice 0 of the coming step
         auto step = [&](int kt, auto c_) __attribute__((always_inline)) {
-            constexpr int C = decltype(c_)::value, s = C & 1;
-            ws.template scales<C>();
+            constexpr int C = decltype(c_)::value, s = C & 1, CN = (C + 1) & 3;
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
-                const bf16x8 wf = ws.template frag<C>(kk);
+                const bf16x8 wf = kk == 0 ? wf0 : ws.template frag<C>(kk);
                 const int buf = kk & 1;
-                if (kk < 3) rd(buf ^ 1, s, kk + 1);
+                if (kk < 3) {
+                    rd(buf ^ 1, s, kk + 1);
+                } else {
+                    // slice 3's operands are in registers: the barrier comes
+                    // before its MFMAs, so the next step's first reads and its
+                    // slice-0 decode overlap them
+                    __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);
+                    __syncthreads();
+                    dma(s, (int64_t)min(kt + 2, KT - 1) * BK);
+                    ws.template issue<C>(kt, KT);
+                    rd(0, s ^ 1, 0);
+                    ws.template scales<CN>();
+                    wf0 = ws.template frag<CN>(0);
+                }
 #pragma unroll
                 for (int i = 0; i < 8; i++)
                     acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, fa[buf][i], acc[i], 0, 0, 0);
             }
-            __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);
-            __syncthreads();
-            dma(s, (int64_t)min(kt + 2, KT - 1) * BK);
-            ws.template issue<C>(kt, KT);
-            rd(0, s ^ 1, 0);
         };
         for (int kt = 0; kt < KT; kt += 4) {
             step(kt, std::integral_constant<int, 0>{});
@@ -379,16 +388,21 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, fh[0][i], acc[i], 0, 0, 0);
-                if (kk < 3) rdh(0, s, kk + 1, 0);
+                if (kk < 3) {
+                    rdh(0, s, kk + 1, 0);
+                } else {
+                    // the last four fragments are in registers: the barrier
+                    // comes before their MFMAs
+                    __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);
+                    __syncthreads();
+                    dma(s, (int64_t)min(kt + 2, KT - 1) * BK);
+                    ws.template issue<C>(kt, KT);
+                    rdh(0, s ^ 1, 0, 0);
+                }
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     acc[4 + i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, fh[1][i], acc[4 + i], 0, 0, 0);
             }
-            __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);
-            __syncthreads();
-            dma(s, (int64_t)min(kt + 2, KT - 1) * BK);
-            ws.template issue<C>(kt, KT);
-            rdh(0, s ^ 1, 0, 0);
         };
         for (int kt = 0; kt < KT; kt += 4) {
             step(kt, std::integral_constant<int, 0>{});

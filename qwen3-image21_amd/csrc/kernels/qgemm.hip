@@ -30,6 +30,7 @@ constexpr int TILEB = 128 * 128;        // bytes of one 128-row operand tile
 constexpr int STAGE = 2 * TILEB;        // A tile then W tile
 constexpr int RING = 2;                 // k steps in flight in registers
 constexpr int CP = 132;                 // f32 pitch of the epilogue tile row
+constexpr int MAX_MID_SPLITS = 16;      // K shares; the split-K reduction kernel sums at most 16
 constexpr int LDS_BYTES = BM * CP * 4;  // 67.6 KB (the two 64 KB operand stages fit): two workgroups per CU
 static_assert(2 * STAGE <= LDS_BYTES, "operand stages fit the epilogue tile");
 static_assert(RING == 2, "the step loop is unrolled by the ring size");
@@ -477,25 +478,40 @@ int device_cu_count() {
     return cus;
 }
 
-// K split of the 128x128 kernel when its tiles alone would leave CUs idle:
-// doubled (up to 8) while the grid stays within one workgroup per CU and each
-// share a whole number of 512-value groups. The partial sums cost 8 s m N
-// bytes of traffic (written once, read once) and a second launch that sums
-// them, which an unsplit product does not pay. One more doubling fills the
-// second resident workgroup slot of each CU (it hides the first one's load
-// waits) where the product is split already, the doubled grid fills nearly
-// both slots and each share keeps at least 1024 k. Measured on the Q8_0 sets
-// at 256 tokens: out 31 -> 27 us (8 -> 4 shares), qkv 57 -> 55 and up 65 -> 58
-// (2 -> 1), while down at K = 12288 and 16384 keeps its 8 shares.
+// K split of the 128x128 kernel, chosen by a cost estimate in microseconds:
+// each workgroup's k steps at 0.64 us per 64-k step when it has its CU to
+// itself, 0.58 us per step and workgroup when two or more share a CU (two are
+// resident at once; the second hides little of the first's issue-bound loop);
+// then, for a split product, the reduction launch (8.4 us) and the partial sums
+// written and read once (8 s m N bytes at ~6.5 TB/s), and for an unsplit one
+// the fused epilogue (9.6 us). Shares are whole 256-value super-blocks of at
+// least 512 k, and a split grid stays within two workgroups per CU, which also
+// bounds the partial sums by 2 x CUs f32 128x128 tiles. Fitted to the Q8_0,
+// Q4_K and Q6_K projections of hidden 3072 and 4096 at 256 and 384 tokens, it
+// picks the measured best share count or one within 3% of it on each, e.g.
+// Q8_0 3072x9216 at 256 tokens: 4 shares, 36.7 us (2 shares: 59.7), and
+// 9216x3072: 3 shares, 37.5 us (unsplit: 40.3).
 int qgemm_mid_splits(const GemmWeight &w, int64_t m) {
     if (m <= 0 || qgemm_large_fits(w, m) || qgemm_stream_fits(w, m)) return 1;
-    const int64_t tiles = (w.n / BN) * ((m + BM - 1) / BM), cus = device_cus();
-    int s = 1;
-    while (s < 8 && tiles * 2 * s <= cus && w.k % (512 * 2 * s) == 0) s *= 2;
-    if (s > 1 && s < 8 && tiles * 2 * s <= 2 * cus && 10 * tiles * 2 * s >= 18 * cus && w.k / (2 * s) >= 1024 &&
-        w.k % (512 * 2 * s) == 0)
-        s *= 2;
-    return s;
+    const int64_t tiles = (w.n / BN) * ((m + BM - 1) / BM), cus = device_cus(), steps = w.k / BK;
+    if (cus <= 0) return 1;
+    auto cost = [&](int s) {
+        const int64_t per_cu = (tiles * s + cus - 1) / cus;
+        const double st = (double)(steps / s);
+        const double loop = per_cu <= 1 ? 0.64 * st : 0.58 * (double)per_cu * st;
+        return loop + (s == 1 ? 9.6 : 8.4 + 8.0 * s * (double)m * (double)w.n / 6.5e6);
+    };
+    int best = 1;
+    double best_cost = cost(1);
+    for (int s = 2; s <= MAX_MID_SPLITS; s++) {
+        if (w.k % (256 * s) || w.k / s < 512 || tiles * s > 2 * cus) continue;
+        const double c = cost(s);
+        if (c < best_cost) {
+            best_cost = c;
+            best = s;
+        }
+    }
+    return best;
 }
 
 namespace {

@@ -153,6 +153,17 @@ __device__ __forceinline__ float max_wave(float a) {
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// Q8_K block rounding from the block's largest magnitude a and the signed value
+// xmax at its first occurrence: iscale s = -128 / xmax and d = 1 / s (both 0
+// for an all-zero block); one value's operand is bf16(d * min(127, round(v s))).
+__device__ __forceinline__ void q8k_scales(float a, float xmax, float &s, float &d) {
+    s = a == 0.f ? 0.f : -128.f / xmax;
+    d = a == 0.f ? 0.f : 1.f / s;
+}
+__device__ __forceinline__ uint32_t q8k_operand(float v, float s, float d) {
+    return bf16_of_product(d, fminf(roundf(v * s), 127.f));
+}
+
 template <int QBLK>
 __device__ __forceinline__ u32x2 quant_act4(f32x4 v) {
     static_assert(QBLK == 32 || QBLK == 256, "Q8_0 or Q8_K blocks");
@@ -165,8 +176,7 @@ __device__ __forceinline__ u32x2 quant_act4(f32x4 v) {
         const int first = hit ? (int)__builtin_ctzll(hit) : 0;
         const float mine = e == 0 ? v[0] : e == 1 ? v[1] : e == 2 ? v[2] : v[3];
         const float xmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), first));
-        s = a == 0.f ? 0.f : -128.f / xmax;
-        d = a == 0.f ? 0.f : 1.f / s;
+        q8k_scales(a, xmax, s, d);
     } else {
         a = max8_lanes(a);
         const float d32 = a / 127.f;

@@ -48,6 +48,12 @@ struct EpiParams {
     uint16_t *hmid;
     int64_t ldh;
     float *hmid_f32 = nullptr;
+    // EPI_SWIGLU with hmid_q8k set: hmid receives the hidden state rounded as
+    // candle's Q8_K (quant_act4<256> over each 256 columns of a row, ldh and the
+    // hidden width multiples of 256), and hmid_f32 is f32 scratch of the same
+    // shape for it (the large-M paired kernel, else the f32 state and then the
+    // rows quantizer)
+    int hmid_q8k = 0;
     // f32 scratch of part_ws_bytes for the short-M split-K path (optional;
     // without it short M takes the 128x128 kernel)
     float *part_ws = nullptr;
@@ -89,6 +95,8 @@ hipError_t launch_qgemm_large(const GemmWeight &w, const uint16_t *a, int64_t m,
 // weight rows into registers. launch_qgemm_large takes it where it fits (the
 // q/k/v epilogue also needs hidden % 256 == 0).
 bool qgemm_wide_fits(const GemmWeight &w);
+// the paired SwiGLU form with the Q8_K rounding of the hidden state (EpiParams::hmid_q8k)
+bool qgemm_wide_pairs_fit(const GemmWeight &w);
 hipError_t launch_qgemm_wide(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
                              const EpiParams &ep, hipStream_t stream);
 // Sum of split-K partials part[splits][m][N] (f32) in split order, with the

@@ -575,6 +575,17 @@ size_t qgemm_workspace(const GemmWeight &w, int64_t m) {
 hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
                         const EpiParams &ep, hipStream_t stream) {
     if (m <= 0) return hipSuccess;
+    if (epi == EPI_SWIGLU && ep.hmid_q8k) {
+        // the Q8_K rounding of the hidden state: inside the paired large-M
+        // kernel where it runs, else the f32 state and then the rows quantizer
+        if (!ep.hmid || !ep.hmid_f32 || ep.ldh % 256 || (w.n / 2) % 256) return hipErrorInvalidValue;
+        if (qgemm_large_fits(w, m) && qgemm_wide_pairs_fit(w)) return launch_qgemm_large(w, a, m, lda, epi, ep, stream);
+        EpiParams e = ep;
+        e.hmid_q8k = 0;
+        const hipError_t err = launch_qgemm(w, a, m, lda, EPI_SWIGLU, e, stream);
+        if (err != hipSuccess) return err;
+        return launch_quant_rows(ep.hmid_f32, ep.ldh, m, w.n / 2, 256, ep.hmid, ep.ldh, stream);
+    }
     if (qgemm_large_fits(w, m)) {
         const int64_t tail = (epi == EPI_F32 || epi == EPI_BF16) ? large_tail_rows(w, m) : 0;
         if (tail && ep.part_ws && ep.part_ws_bytes >= small_workspace(w, tail)) {

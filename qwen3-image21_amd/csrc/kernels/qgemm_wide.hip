@@ -38,6 +38,10 @@ constexpr int BM = 256, BN = 256, NW = 8, BK = 64;
 constexpr int ROWB = 128;         // bytes per LDS row of an activation stage: 64 bf16
 constexpr int STAGE = BM * ROWB;  // 32 KB
 constexpr int GROUP_M = 4;
+// Epilogue code of the paired SwiGLU form (EpiParams::hmid_q8k): a workgroup
+// takes the n tiles 2u and 2u + 1 of one token tile in turn, whose 128 + 128
+// hidden columns are one Q8_K block of every token row.
+constexpr int EPI_SWIGLU_Q8K = 16;
 
 __device__ __forceinline__ uint32_t byte_of(const u32x4 &x, int i) {
     return (x[i >> 2] >> (8 * (i & 3))) & 0xffu;
@@ -252,316 +256,457 @@ struct WStream<WF_Q6_K> {
 template <int FMT, int EPI>
 __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *__restrict__ A, int64_t M, int64_t lda,
                                                                GemmWeight w, EpiParams ep, int mt, int nt) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int l32 = lane & 31, g = lane >> 5;
+    constexpr bool PAIR = EPI == EPI_SWIGLU_Q8K;
+    // the two activation stages; in the paired form then the first tile's
+    // per-token largest magnitude, and the block column of its first
+    // occurrence times 2 plus its sign bit (one LDS object, so the compiler
+    // tells the direct loads into one stage from the reads of the other)
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE + (PAIR ? 2 * BM * 4 : 0)];
+    float *pair_amax = (float *)(lds + 2 * STAGE);
+    int *pair_first = (int *)(lds + 2 * STAGE + BM * 4);
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    // XCD-aware, M-grouped tile order
-    const int total = mt * nt;
+    // XCD-aware, M-grouped order of the (token tile, n unit) pairs; an n unit
+    // is one tile, or two in the paired form
+    const int nu = PAIR ? nt / 2 : nt;
+    const int total = mt * nu;
     int L = blockIdx.x;
     if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
-    const int per_group = GROUP_M * nt;
+    const int per_group = GROUP_M * nu;
     const int grp = L / per_group;
     const int first_m = grp * GROUP_M;
     const int gm = min(mt - first_m, GROUP_M);
     const int mtile = first_m + (L % per_group) % gm;
-    const int ntile = (L % per_group) / gm;
-    const int64_t m0 = (int64_t)mtile * BM, n0 = (int64_t)ntile * BN;
+    const int nunit = (L % per_group) / gm;
+    const int64_t m0 = (int64_t)mtile * BM;
     const int KT = (int)(w.k / BK);
 
-    // activation stage by direct global->LDS loads (16 B per lane, lane l at
-    // base + 16 l): instruction i of wave v fills rows 8 (4 v + i) .. +8, lane l
-    // row 8 (4 v + i) + l / 8 at slot l % 8, which holds chunk (l % 8) ^ key(row).
-    // Rows past M repeat row M - 1; their outputs are never written.
-    const uint16_t *asrc[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int row = 8 * (4 * wave + i) + (lane >> 3);
-        const int c = (lane & 7) ^ swz_key(row);
-        asrc[i] = A + min(m0 + row, M - 1) * lda + 8 * c;
-    }
-    auto dma = [&](int stage, int64_t k0) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            __builtin_amdgcn_global_load_lds((const void *)(asrc[i] + k0),
-                                             (lds_ptr_t)(lds + stage * STAGE + (4 * wave + i) * 8 * ROWB), 16, 0, 0);
-    };
+    // one tile (t: its index in the workgroup's n unit)
+    auto tile = [&](auto t_) __attribute__((always_inline)) {
+        constexpr int t = decltype(t_)::value;
+        const int64_t n0 = (int64_t)(PAIR ? 2 * nunit + t : nunit) * BN;
+        // every lane-dependent value of a tile derives from this copy of the
+        // thread index, which the compiler cannot see through: in the paired
+        // form nothing of the second tile's addressing is computed early and
+        // kept live across the first tile's loop. The mask after it keeps the
+        // lane's range known (the fragment reads of one stage provably miss
+        // the other stage's direct loads, so they wait for no load).
+        int lane = tid;
+        if constexpr (PAIR) asm volatile("" : "+v"(lane));
+        lane &= 63;
+        const int l32 = lane & 31, g = lane >> 5;
 
-    // this lane's weight row (the A-operand row l32 of the wave's fragment)
-    int64_t wrow;
-    if constexpr (EPI == EPI_SWIGLU) {
-        // rows interleaved per 64 (gate | up): the wave takes 16 gate rows and
-        // the 16 up rows of the same hidden columns
-        const int G = wave >> 2, sub = wave & 3;
-        wrow = n0 + 128 * G + (l32 < 16 ? 16 * sub + l32 : 64 + 16 * sub + l32 - 16);
-    } else {
-        wrow = n0 + 32 * wave + l32;
-    }
-    WStream<FMT> ws;
-    ws.init(w, wrow, g, KT);
-
-    // LDS offsets of the token fragments: row l32 (+ 32 i), chunk(kk, g)
-    const int key = swz_key(l32);
-    int aoff[4];
+        // activation stage by direct global->LDS loads (16 B per lane, lane l at
+        // base + 16 l): instruction i of wave v fills rows 8 (4 v + i) .. +8, lane l
+        // row 8 (4 v + i) + l / 8 at slot l % 8, which holds chunk (l % 8) ^ key(row).
+        // Rows past M repeat row M - 1; their outputs are never written.
+        const uint16_t *asrc[4];
 #pragma unroll
-    for (int kk = 0; kk < 4; kk++) aoff[kk] = l32 * ROWB + ((WStream<FMT>::chunk(kk, g) ^ key) << 4);
-
-    f32x16 acc[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[i][r] = 0.f;
-
-    dma(0, 0);
-    dma(1, (int64_t)min(1, KT - 1) * BK);
-    __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);  // vmcnt(0) lgkmcnt(0)
-    __syncthreads();
-
-    // Step kt (kt % 4 == C), stage s = C & 1: slice kk decodes its weight
-    // fragment and runs 8 MFMAs against the slice's token fragments, which
-    // were read ahead. After slice 3: the wait for the next step's activation
-    // stage (issued a step ago) and ONE barrier, after which stage s receives
-    // the activations of step kt + 2, the weight stream loads for step kt + 2,
-    // and the first token fragments of step kt + 1 are read. Every read is
-    // pinned ahead of the MFMAs it overlaps by a scheduling barrier.
-    if constexpr (FMT != WF_Q6_K) {
-        // the 8 fragments of slice kk + 1 are read while slice kk's MFMAs run
-        bf16x8 fa[2][8];
-        auto rd = [&](int buf, int stage, int kk) __attribute__((always_inline)) {
-            const uint8_t *st = lds + stage * STAGE + aoff[kk];
-#pragma unroll
-            for (int i = 0; i < 8; i++) fa[buf][i] = *(const bf16x8 *)(st + i * 32 * ROWB);
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        rd(0, 0, 0);
-        ws.template scales<0>();
-        bf16x8 wf0 = ws.template frag<0>(0);  // slice 0 of the coming step
-        auto step = [&](int kt, auto c_) __attribute__((always_inline)) {
-            constexpr int C = decltype(c_)::value, s = C & 1, CN = (C + 1) & 3;
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const bf16x8 wf = kk == 0 ? wf0 : ws.template frag<C>(kk);
-                const int buf = kk & 1;
-                if (kk < 3) {
-                    rd(buf ^ 1, s, kk + 1);
-                } else {
-                    // slice 3's operands are in registers: the barrier comes
-                    // before its MFMAs, so the next step's first reads and its
-                    // slice-0 decode overlap them
-                    __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);
-                    __syncthreads();
-                    dma(s, (int64_t)min(kt + 2, KT - 1) * BK);
-                    ws.template issue<C>(kt, KT);
-                    rd(0, s ^ 1, 0);
-                    ws.template scales<CN>();
-                    wf0 = ws.template frag<CN>(0);
-                }
-#pragma unroll
-                for (int i = 0; i < 8; i++)
-                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, fa[buf][i], acc[i], 0, 0, 0);
-            }
-        };
-        for (int kt = 0; kt < KT; kt += 4) {
-            step(kt, std::integral_constant<int, 0>{});
-            step(kt + 1, std::integral_constant<int, 1>{});
-            step(kt + 2, std::integral_constant<int, 2>{});
-            step(kt + 3, std::integral_constant<int, 3>{});
+        for (int i = 0; i < 4; i++) {
+            const int row = 8 * (4 * wave + i) + (lane >> 3);
+            const int c = (lane & 7) ^ swz_key(row);
+            asrc[i] = A + min(m0 + row, M - 1) * lda + 8 * c;
         }
-    } else {
-        // Q6_K holds twice the raw bytes of Q4_K in registers, so its token
-        // fragments are read half a slice ahead (four at a time)
-        bf16x8 fh[2][4];
-        auto rdh = [&](int buf, int stage, int kk, int h) __attribute__((always_inline)) {
-            const uint8_t *st = lds + stage * STAGE + aoff[kk] + h * 4 * 32 * ROWB;
+        auto dma = [&](int stage, int64_t k0) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) fh[buf][i] = *(const bf16x8 *)(st + i * 32 * ROWB);
-            __builtin_amdgcn_sched_barrier(0);
+            for (int i = 0; i < 4; i++)
+                __builtin_amdgcn_global_load_lds((const void *)(asrc[i] + k0),
+                                                 (lds_ptr_t)(lds + stage * STAGE + (4 * wave + i) * 8 * ROWB), 16, 0, 0);
         };
-        rdh(0, 0, 0, 0);
-        auto step = [&](int kt, auto c_) __attribute__((always_inline)) {
-            constexpr int C = decltype(c_)::value, s = C & 1;
-            ws.template scales<C>();
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const bf16x8 wf = ws.template frag<C>(kk);
-                rdh(1, s, kk, 1);
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, fh[0][i], acc[i], 0, 0, 0);
-                if (kk < 3) {
-                    rdh(0, s, kk + 1, 0);
-                } else {
-                    // the last four fragments are in registers: the barrier
-                    // comes before their MFMAs
-                    __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);
-                    __syncthreads();
-                    dma(s, (int64_t)min(kt + 2, KT - 1) * BK);
-                    ws.template issue<C>(kt, KT);
-                    rdh(0, s ^ 1, 0, 0);
-                }
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    acc[4 + i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, fh[1][i], acc[4 + i], 0, 0, 0);
-            }
-        };
-        for (int kt = 0; kt < KT; kt += 4) {
-            step(kt, std::integral_constant<int, 0>{});
-            step(kt + 1, std::integral_constant<int, 1>{});
-            step(kt + 2, std::integral_constant<int, 2>{});
-            step(kt + 3, std::integral_constant<int, 3>{});
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);  // no load into LDS still in flight
 
-    // ---- epilogue: lane (g, l32) of token tile i holds token m0 + 32 i + l32,
-    // register r the wave's weight row p(r) = 8 (r / 4) + 4 g + r % 4 ----
-    if constexpr (EPI == EPI_F32 || EPI == EPI_BF16 || EPI == EPI_RESID) {
-        const int64_t nw = n0 + 32 * wave + 4 * g;  // + 8 j: the lane's run j of four rows
-        const int64_t N = w.n;
+        // LDS offsets of the token fragments: row l32 (+ 32 i), chunk(kk, g)
+        const int key = swz_key(l32);
+        int aoff[4];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int64_t m = m0 + 32 * i + l32;
-            if (m >= M) continue;
-            if constexpr (EPI == EPI_F32) {
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    *(f32x4 *)((float *)ep.out + m * ep.ldo + nw + 8 * j) =
-                        f32x4{acc[i][4 * j], acc[i][4 * j + 1], acc[i][4 * j + 2], acc[i][4 * j + 3]};
-            } else if constexpr (EPI == EPI_BF16) {
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    *(u32x2 *)((uint16_t *)ep.out + m * ep.ldo + nw + 8 * j) =
-                        u32x2{pack_bf16x2(acc[i][4 * j], acc[i][4 * j + 1]),
-                              pack_bf16x2(acc[i][4 * j + 2], acc[i][4 * j + 3])};
-            } else {
-                // x_out may alias x_in: each element is read and written by
-                // the same lane, every load of the row before its stores
-                const float *grow = ep.gvec + (int64_t)((int)m / (int)ep.g_rows_per) * ep.g_stride;
-                f32x4 xv[4], gv[4];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    xv[j] = *(const f32x4 *)(ep.x_in + m * N + nw + 8 * j);
-                    gv[j] = *(const f32x4 *)(grow + nw + 8 * j);
-                }
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    f32x4 o;
-#pragma unroll
-                    for (int e = 0; e < 4; e++) o[e] = xv[j][e] + gv[j][e] * acc[i][4 * j + e];
-                    *(f32x4 *)(ep.x_out + m * N + nw + 8 * j) = o;
-                }
-            }
+        for (int kk = 0; kk < 4; kk++) aoff[kk] = l32 * ROWB + ((WStream<FMT>::chunk(kk, g) ^ key) << 4);
+
+        // this lane's weight row (the A-operand row l32 of the wave's fragment)
+        int64_t wrow;
+        if constexpr (EPI == EPI_SWIGLU || PAIR) {
+            // rows interleaved per 64 (gate | up): the wave takes 16 gate rows and
+            // the 16 up rows of the same hidden columns
+            const int G = wave >> 2, sub = wave & 3;
+            wrow = n0 + 128 * G + (l32 < 16 ? 16 * sub + l32 : 64 + 16 * sub + l32 - 16);
+        } else {
+            wrow = n0 + 32 * wave + l32;
         }
-    } else if constexpr (EPI == EPI_SWIGLU) {
-        // registers r < 8 are gate rows 16 sub + p(r), r + 8 the up rows of the
-        // same hidden columns
-        const int G = wave >> 2, sub = wave & 3;
-        const int64_t hc = (n0 + 128 * G) / 2 + 16 * sub + 4 * g;  // + 8 j
+        WStream<FMT> ws;
+        ws.init(w, wrow, g, KT);
+
+        f32x16 acc[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int64_t m = m0 + 32 * i + l32;
-            if (m >= M) continue;
+        for (int i = 0; i < 8; i++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                float h[4];
+            for (int r = 0; r < 16; r++) acc[i][r] = 0.f;
+
+        dma(0, 0);
+        dma(1, (int64_t)min(1, KT - 1) * BK);
+        __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);  // vmcnt(0) lgkmcnt(0)
+        __syncthreads();
+
+        // Step kt (kt % 4 == C), stage s = C & 1: slice kk decodes its weight
+        // fragment and runs 8 MFMAs against the slice's token fragments, which
+        // were read ahead. After slice 3: the wait for the next step's activation
+        // stage (issued a step ago) and ONE barrier, after which stage s receives
+        // the activations of step kt + 2, the weight stream loads for step kt + 2,
+        // and the first token fragments of step kt + 1 are read. Every read is
+        // pinned ahead of the MFMAs it overlaps by a scheduling barrier.
+        if constexpr (FMT != WF_Q6_K) {
+            // the 8 fragments of slice kk + 1 are read while slice kk's MFMAs run
+            bf16x8 fa[2][8];
+            auto rd = [&](int buf, int stage, int kk) __attribute__((always_inline)) {
+                const uint8_t *st = lds + stage * STAGE + aoff[kk];
 #pragma unroll
-                for (int e = 0; e < 4; e++) h[e] = silu(acc[i][4 * j + e]) * acc[i][8 + 4 * j + e];
-                const int64_t o = m * ep.ldh + hc + 8 * j;
-                if (ep.hmid_f32)
-                    *(f32x4 *)(ep.hmid_f32 + o) = f32x4{h[0], h[1], h[2], h[3]};
-                else
-                    *(u32x2 *)(ep.hmid + o) = u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
-            }
-        }
-    } else if constexpr (EPI == EPI_QKV) {
-        // waves 4 G .. 4 G + 3 hold one head (128 fused columns), wave sub its
-        // dims 32 sub + p(r)
-        const int G = wave >> 2, sub = wave & 3;
-        const int64_t nb = n0 + 128 * G + ep.n_offset;
-        const int sec = (int)(nb / ep.hidden);
-        const int64_t head = (nb % ep.hidden) / 128;
-        const uint32_t Su = (uint32_t)ep.seq;
-        const int64_t H = ep.heads, S = ep.seq;
-        if (sec < 2) {
-            // RmsNorm over the head: each lane's 16 squares, the partner half
-            // (lane ^ 32), then the head's four waves through LDS
-            float *red = (float *)lds;  // [8 waves][256 tokens]
-            __syncthreads();            // every wave is done with the operand stages
+                for (int i = 0; i < 8; i++) fa[buf][i] = *(const bf16x8 *)(st + i * 32 * ROWB);
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            rd(0, 0, 0);
+            ws.template scales<0>();
+            bf16x8 wf0 = ws.template frag<0>(0);  // slice 0 of the coming step
+            auto step = [&](int kt, auto c_) __attribute__((always_inline)) {
+                constexpr int C = decltype(c_)::value, s = C & 1, CN = (C + 1) & 3;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                float ss = 0.f;
-#pragma unroll
-                for (int r = 0; r < 16; r++) ss += acc[i][r] * acc[i][r];
-                float lo = ss, hi = ss;
-                asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lo), "+v"(hi));
-                if (g == 0) red[wave * 256 + 32 * i + l32] = lo + hi;
-            }
-            __syncthreads();
-            typedef __attribute__((address_space(4))) const f32x4 cf32x4;
-            const __attribute__((address_space(4))) float *nwt =
-                (const __attribute__((address_space(4))) float *)(sec == 0 ? ep.norm_q : ep.norm_k);
-            const float osc = sec == 0 ? ep.q_scale : 1.0f;
-            uint16_t *dst = sec == 0 ? ep.q : ep.k;
-            const int dbase = 32 * sub + 4 * g;  // + 8 j
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int t = 32 * i + l32;
-                const int64_t m = m0 + t;
-                if (m >= M) continue;
-                const float *rr = red + 4 * G * 256 + t;
-                const float tot = (rr[0] + rr[256]) + (rr[512] + rr[768]);
-                const float rs = 1.0f / sqrtf(tot * (1.0f / 128.0f) + 1e-6f);
-                const uint32_t s = (uint32_t)m % Su, b = (uint32_t)m / Su;
-                const float *pr = ep.pe + (int64_t)s * 128;  // (cos, sin) of pair i at 2i, 2i + 1
-                uint16_t *drow = dst + (((int64_t)b * H + head) * S + s) * 128;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int d = dbase + 8 * j;
-                    const f32x4 cs = *(const f32x4 *)(pr + d);
-                    const f32x4 wv = *(const cf32x4 *)(nwt + d);
-                    uint32_t o[2];
-#pragma unroll
-                    for (int e = 0; e < 2; e++) {
-                        const float x0 = acc[i][4 * j + 2 * e] * rs * wv[2 * e];
-                        const float x1 = acc[i][4 * j + 2 * e + 1] * rs * wv[2 * e + 1];
-                        const float co = cs[2 * e], sn = cs[2 * e + 1];
-                        o[e] = pack_bf16x2((x0 * co - x1 * sn) * osc, (x0 * sn + x1 * co) * osc);
+                for (int kk = 0; kk < 4; kk++) {
+                    const bf16x8 wf = kk == 0 ? wf0 : ws.template frag<C>(kk);
+                    const int buf = kk & 1;
+                    if (kk < 3) {
+                        rd(buf ^ 1, s, kk + 1);
+                    } else {
+                        // slice 3's operands are in registers: the barrier comes
+                        // before its MFMAs, so the next step's first reads and its
+                        // slice-0 decode overlap them
+                        __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);
+                        __syncthreads();
+                        dma(s, (int64_t)min(kt + 2, KT - 1) * BK);
+                        ws.template issue<C>(kt, KT);
+                        rd(0, s ^ 1, 0);
+                        ws.template scales<CN>();
+                        wf0 = ws.template frag<CN>(0);
                     }
-                    *(u32x2 *)(drow + d) = u32x2{o[0], o[1]};
+#pragma unroll
+                    for (int i = 0; i < 8; i++)
+                        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, fa[buf][i], acc[i], 0, 0, 0);
                 }
+            };
+            for (int kt = 0; kt < KT; kt += 4) {
+                step(kt, std::integral_constant<int, 0>{});
+                step(kt + 1, std::integral_constant<int, 1>{});
+                step(kt + 2, std::integral_constant<int, 2>{});
+                step(kt + 3, std::integral_constant<int, 3>{});
             }
         } else {
-            // v: transposed to vt [B,H,128,S] (consecutive lanes hold
-            // consecutive tokens of a d row), and [B,H,S,128] when v_bhsd is set
-            const int dbase = 32 * sub + 4 * g;
+            // Q6_K holds twice the raw bytes of Q4_K in registers, so its token
+            // fragments are read half a slice ahead (four at a time)
+            bf16x8 fh[2][4];
+            auto rdh = [&](int buf, int stage, int kk, int h) __attribute__((always_inline)) {
+                const uint8_t *st = lds + stage * STAGE + aoff[kk] + h * 4 * 32 * ROWB;
+#pragma unroll
+                for (int i = 0; i < 4; i++) fh[buf][i] = *(const bf16x8 *)(st + i * 32 * ROWB);
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            rdh(0, 0, 0, 0);
+            auto step = [&](int kt, auto c_) __attribute__((always_inline)) {
+                constexpr int C = decltype(c_)::value, s = C & 1;
+                ws.template scales<C>();
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) {
+                    const bf16x8 wf = ws.template frag<C>(kk);
+                    rdh(1, s, kk, 1);
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, fh[0][i], acc[i], 0, 0, 0);
+                    if (kk < 3) {
+                        rdh(0, s, kk + 1, 0);
+                    } else {
+                        // the last four fragments are in registers: the barrier
+                        // comes before their MFMAs
+                        __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);
+                        __syncthreads();
+                        dma(s, (int64_t)min(kt + 2, KT - 1) * BK);
+                        ws.template issue<C>(kt, KT);
+                        rdh(0, s ^ 1, 0, 0);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        acc[4 + i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, fh[1][i], acc[4 + i], 0, 0, 0);
+                }
+            };
+            for (int kt = 0; kt < KT; kt += 4) {
+                step(kt, std::integral_constant<int, 0>{});
+                step(kt + 1, std::integral_constant<int, 1>{});
+                step(kt + 2, std::integral_constant<int, 2>{});
+                step(kt + 3, std::integral_constant<int, 3>{});
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(WAIT_VM0_LGKM0);  // no load into LDS still in flight
+
+        // ---- epilogue: lane (g, l32) of token tile i holds token m0 + 32 i + l32,
+        // register r the wave's weight row p(r) = 8 (r / 4) + 4 g + r % 4 ----
+        if constexpr (EPI == EPI_F32 || EPI == EPI_BF16 || EPI == EPI_RESID) {
+            const int64_t nw = n0 + 32 * wave + 4 * g;  // + 8 j: the lane's run j of four rows
+            const int64_t N = w.n;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const int64_t m = m0 + 32 * i + l32;
                 if (m >= M) continue;
-                const uint32_t s = (uint32_t)m % Su, b = (uint32_t)m / Su;
-                uint16_t *vrow = ep.vt + ((int64_t)b * H + head) * 128 * S + s;
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int d = dbase + 8 * (r >> 2) + (r & 3);
-                    vrow[(int64_t)d * S] = (uint16_t)(pack_bf16x2(acc[i][r], 0.f) & 0xffffu);
-                }
-                if (ep.v_bhsd) {
-                    uint16_t *brow = ep.v_bhsd + (((int64_t)b * H + head) * S + s) * 128;
+                if constexpr (EPI == EPI_F32) {
 #pragma unroll
                     for (int j = 0; j < 4; j++)
-                        *(u32x2 *)(brow + dbase + 8 * j) = u32x2{pack_bf16x2(acc[i][4 * j], acc[i][4 * j + 1]),
-                                                                 pack_bf16x2(acc[i][4 * j + 2], acc[i][4 * j + 3])};
+                        *(f32x4 *)((float *)ep.out + m * ep.ldo + nw + 8 * j) =
+                            f32x4{acc[i][4 * j], acc[i][4 * j + 1], acc[i][4 * j + 2], acc[i][4 * j + 3]};
+                } else if constexpr (EPI == EPI_BF16) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        *(u32x2 *)((uint16_t *)ep.out + m * ep.ldo + nw + 8 * j) =
+                            u32x2{pack_bf16x2(acc[i][4 * j], acc[i][4 * j + 1]),
+                                  pack_bf16x2(acc[i][4 * j + 2], acc[i][4 * j + 3])};
+                } else {
+                    // x_out may alias x_in: each element is read and written by
+                    // the same lane, every load of the row before its stores
+                    const float *grow = ep.gvec + (int64_t)((int)m / (int)ep.g_rows_per) * ep.g_stride;
+                    f32x4 xv[4], gv[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        xv[j] = *(const f32x4 *)(ep.x_in + m * N + nw + 8 * j);
+                        gv[j] = *(const f32x4 *)(grow + nw + 8 * j);
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        f32x4 o;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) o[e] = xv[j][e] + gv[j][e] * acc[i][4 * j + e];
+                        *(f32x4 *)(ep.x_out + m * N + nw + 8 * j) = o;
+                    }
+                }
+            }
+        } else if constexpr (EPI == EPI_SWIGLU) {
+            // registers r < 8 are gate rows 16 sub + p(r), r + 8 the up rows of the
+            // same hidden columns
+            const int G = wave >> 2, sub = wave & 3;
+            const int64_t hc = (n0 + 128 * G) / 2 + 16 * sub + 4 * g;  // + 8 j
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int64_t m = m0 + 32 * i + l32;
+                if (m >= M) continue;
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    float h[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) h[e] = silu(acc[i][4 * j + e]) * acc[i][8 + 4 * j + e];
+                    const int64_t o = m * ep.ldh + hc + 8 * j;
+                    if (ep.hmid_f32)
+                        *(f32x4 *)(ep.hmid_f32 + o) = f32x4{h[0], h[1], h[2], h[3]};
+                    else
+                        *(u32x2 *)(ep.hmid + o) = u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+                }
+            }
+        } else if constexpr (PAIR) {
+            // candle's Q8_K rounding of the hidden state (the down projection's
+            // input), in the arithmetic of quant_act4<256>: the first tile's f32
+            // values go to hmid_f32 (scratch) and its per-token largest magnitude
+            // and first column to LDS; after the second tile the block's x_max is
+            // the first of largest magnitude over both, and both halves are
+            // written to hmid as bf16(d q). Register r < 8 of token tile i is gate
+            // row 16 sub + p(r), r + 8 its up row: hidden column hc + 8 (r / 4) + r % 4.
+            const int G = wave >> 2, sub = wave & 3;
+            const int64_t hc = n0 / 2 + 64 * G + 16 * sub + 4 * g;
+            const int cb = (int)(hc & 255);  // its column in the Q8_K block
+            float h[8][8];
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+#pragma unroll
+                for (int r = 0; r < 8; r++) h[i][r] = silu(acc[i][r]) * acc[i][8 + r];
+            if constexpr (t == 0) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int64_t m = m0 + 32 * i + l32;
+                    if (m >= M) continue;
+                    float *frow = ep.hmid_f32 + m * ep.ldh + hc;
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        *(f32x4 *)(frow + 8 * j) = f32x4{h[i][4 * j], h[i][4 * j + 1], h[i][4 * j + 2], h[i][4 * j + 3]};
+                }
+            }
+            float *red = (float *)lds;                    // [8 waves][256 tokens]
+            int *redi = (int *)(lds + NW * BM * 4);       // [8 waves][256 tokens]
+            float *tmax = (float *)(lds + 2 * NW * BM * 4);  // [256] per token
+            float *tsc = tmax + BM, *tdq = tmax + 2 * BM;    // [256] s and d per token
+            __syncthreads();  // every wave is done with the operand stages
+            // largest magnitude per token: the lane's 8, its partner half (lane ^ 32), the 8 waves
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float a = 0.f;
+#pragma unroll
+                for (int r = 0; r < 8; r++) a = fmaxf(a, fabsf(h[i][r]));
+                float lo = a, hi = a;
+                asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lo), "+v"(hi));
+                if (g == 0) red[wave * BM + 32 * i + l32] = fmaxf(lo, hi);
+            }
+            __syncthreads();
+            if (tid < BM) {
+                float a = red[tid];
+#pragma unroll
+                for (int v = 1; v < NW; v++) a = fmaxf(a, red[v * BM + tid]);
+                tmax[tid] = a;
+            }
+            __syncthreads();
+            // its first occurrence: the smallest (column << 1 | sign) holding it
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float a = tmax[32 * i + l32];
+                int f = 0x7fffffff;
+#pragma unroll
+                for (int r = 7; r >= 0; r--) {
+                    const int code = ((cb + 8 * (r >> 2) + (r & 3)) << 1) | (h[i][r] < 0.f ? 1 : 0);
+                    f = fabsf(h[i][r]) == a ? code : f;
+                }
+                int lo = f, hi = f;
+                asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lo), "+v"(hi));
+                if (g == 0) redi[wave * BM + 32 * i + l32] = min(lo, hi);
+            }
+            __syncthreads();
+            if (tid < BM) {
+                int f = redi[tid];
+#pragma unroll
+                for (int v = 1; v < NW; v++) f = min(f, redi[v * BM + tid]);
+                float a = tmax[tid];
+                if constexpr (t == 0) {
+                    pair_amax[tid] = a;
+                    pair_first[tid] = f;
+                } else {
+                    // the first tile's columns come first: it wins ties
+                    if (!(a > pair_amax[tid])) {
+                        a = pair_amax[tid];
+                        f = pair_first[tid];
+                    }
+                    float sc, dq;
+                    q8k_scales(a, (f & 1) ? -a : a, sc, dq);
+                    tsc[tid] = sc;
+                    tdq[tid] = dq;
+                }
+            }
+            __syncthreads();  // (first tile) the next tile's stages overwrite these tables
+            if constexpr (t == 1) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int64_t m = m0 + 32 * i + l32;
+                    if (m >= M) continue;
+                    const float sc = tsc[32 * i + l32], dq = tdq[32 * i + l32];
+                    uint16_t *hrow = ep.hmid + m * ep.ldh + hc;
+                    // this lane's own f32 stores of the first tile, 128 columns back
+                    const float *frow = ep.hmid_f32 + m * ep.ldh + hc - 128;
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        const float *v = &h[i][4 * j];
+                        const f32x4 u = *(const f32x4 *)(frow + 8 * j);
+                        *(u32x2 *)(hrow + 8 * j) =
+                            u32x2{q8k_operand(v[0], sc, dq) | (q8k_operand(v[1], sc, dq) << 16),
+                                  q8k_operand(v[2], sc, dq) | (q8k_operand(v[3], sc, dq) << 16)};
+                        *(u32x2 *)(hrow - 128 + 8 * j) =
+                            u32x2{q8k_operand(u[0], sc, dq) | (q8k_operand(u[1], sc, dq) << 16),
+                                  q8k_operand(u[2], sc, dq) | (q8k_operand(u[3], sc, dq) << 16)};
+                    }
+                }
+            }
+        } else if constexpr (EPI == EPI_QKV) {
+            // waves 4 G .. 4 G + 3 hold one head (128 fused columns), wave sub its
+            // dims 32 sub + p(r)
+            const int G = wave >> 2, sub = wave & 3;
+            const int64_t nb = n0 + 128 * G + ep.n_offset;
+            const int sec = (int)(nb / ep.hidden);
+            const int64_t head = (nb % ep.hidden) / 128;
+            const uint32_t Su = (uint32_t)ep.seq;
+            const int64_t H = ep.heads, S = ep.seq;
+            if (sec < 2) {
+                // RmsNorm over the head: each lane's 16 squares, the partner half
+                // (lane ^ 32), then the head's four waves through LDS
+                float *red = (float *)lds;  // [8 waves][256 tokens]
+                __syncthreads();            // every wave is done with the operand stages
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    float ss = 0.f;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) ss += acc[i][r] * acc[i][r];
+                    float lo = ss, hi = ss;
+                    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lo), "+v"(hi));
+                    if (g == 0) red[wave * 256 + 32 * i + l32] = lo + hi;
+                }
+                __syncthreads();
+                typedef __attribute__((address_space(4))) const f32x4 cf32x4;
+                const __attribute__((address_space(4))) float *nwt =
+                    (const __attribute__((address_space(4))) float *)(sec == 0 ? ep.norm_q : ep.norm_k);
+                const float osc = sec == 0 ? ep.q_scale : 1.0f;
+                uint16_t *dst = sec == 0 ? ep.q : ep.k;
+                const int dbase = 32 * sub + 4 * g;  // + 8 j
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int t = 32 * i + l32;
+                    const int64_t m = m0 + t;
+                    if (m >= M) continue;
+                    const float *rr = red + 4 * G * 256 + t;
+                    const float tot = (rr[0] + rr[256]) + (rr[512] + rr[768]);
+                    const float rs = 1.0f / sqrtf(tot * (1.0f / 128.0f) + 1e-6f);
+                    const uint32_t s = (uint32_t)m % Su, b = (uint32_t)m / Su;
+                    const float *pr = ep.pe + (int64_t)s * 128;  // (cos, sin) of pair i at 2i, 2i + 1
+                    uint16_t *drow = dst + (((int64_t)b * H + head) * S + s) * 128;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int d = dbase + 8 * j;
+                        const f32x4 cs = *(const f32x4 *)(pr + d);
+                        const f32x4 wv = *(const cf32x4 *)(nwt + d);
+                        uint32_t o[2];
+#pragma unroll
+                        for (int e = 0; e < 2; e++) {
+                            const float x0 = acc[i][4 * j + 2 * e] * rs * wv[2 * e];
+                            const float x1 = acc[i][4 * j + 2 * e + 1] * rs * wv[2 * e + 1];
+                            const float co = cs[2 * e], sn = cs[2 * e + 1];
+                            o[e] = pack_bf16x2((x0 * co - x1 * sn) * osc, (x0 * sn + x1 * co) * osc);
+                        }
+                        *(u32x2 *)(drow + d) = u32x2{o[0], o[1]};
+                    }
+                }
+            } else {
+                // v: transposed to vt [B,H,128,S] (consecutive lanes hold
+                // consecutive tokens of a d row), and [B,H,S,128] when v_bhsd is set
+                const int dbase = 32 * sub + 4 * g;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int64_t m = m0 + 32 * i + l32;
+                    if (m >= M) continue;
+                    const uint32_t s = (uint32_t)m % Su, b = (uint32_t)m / Su;
+                    uint16_t *vrow = ep.vt + ((int64_t)b * H + head) * 128 * S + s;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int d = dbase + 8 * (r >> 2) + (r & 3);
+                        vrow[(int64_t)d * S] = (uint16_t)(pack_bf16x2(acc[i][r], 0.f) & 0xffffu);
+                    }
+                    if (ep.v_bhsd) {
+                        uint16_t *brow = ep.v_bhsd + (((int64_t)b * H + head) * S + s) * 128;
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            *(u32x2 *)(brow + dbase + 8 * j) = u32x2{pack_bf16x2(acc[i][4 * j], acc[i][4 * j + 1]),
+                                                                     pack_bf16x2(acc[i][4 * j + 2], acc[i][4 * j + 3])};
+                    }
                 }
             }
         }
-    }
+    };
+    tile(std::integral_constant<int, 0>{});
+    if constexpr (PAIR) tile(std::integral_constant<int, 1>{});
 }
 
 template <int FMT>
 hipError_t launch_fmt(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi, const EpiParams &ep,
                       hipStream_t stream) {
     const int mt = (int)((m + BM - 1) / BM), nt = (int)(w.n / BN);
-    const dim3 grid((unsigned)(mt * nt)), block(64 * NW);
+    const dim3 block(64 * NW);
+    if (epi == EPI_SWIGLU && ep.hmid_q8k) {
+        if (nt % 2 || !ep.hmid || !ep.hmid_f32) return hipErrorInvalidValue;
+        qgemm_wide_kernel<FMT, EPI_SWIGLU_Q8K>
+            <<<dim3((unsigned)(mt * nt / 2)), block, 0, stream>>>(a, m, lda, w, ep, mt, nt);
+        return hipGetLastError();
+    }
+    const dim3 grid((unsigned)(mt * nt));
     switch (epi) {
     case EPI_F32: qgemm_wide_kernel<FMT, EPI_F32><<<grid, block, 0, stream>>>(a, m, lda, w, ep, mt, nt); break;
     case EPI_BF16: qgemm_wide_kernel<FMT, EPI_BF16><<<grid, block, 0, stream>>>(a, m, lda, w, ep, mt, nt); break;
@@ -578,6 +723,8 @@ hipError_t launch_fmt(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t
 bool qgemm_wide_fits(const GemmWeight &w) {
     return (w.fmt == WF_Q4_K || w.fmt == WF_Q6_K || w.fmt == WF_Q8_0) && w.n % BN == 0 && w.k % 256 == 0 && w.k > 0;
 }
+
+bool qgemm_wide_pairs_fit(const GemmWeight &w) { return qgemm_wide_fits(w) && w.n % (2 * BN) == 0; }
 
 hipError_t launch_qgemm_wide(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
                              const EpiParams &ep, hipStream_t stream) {

@@ -77,6 +77,59 @@ def test_block_1024_q4km_full_size(torch_cuda, qctx):
     kv_close(vb, vre)
 
 
+def _q4k_negated(rows):
+    """Q4_K rows [n, bytes] holding the exact negation of the given ones: the f16
+    d and dmin of every 144-byte block change sign (value = d sc q - dmin m)."""
+    out = rows.copy().reshape(rows.shape[0], -1, 144)
+    out[:, :, 1] ^= 0x80
+    out[:, :, 3] ^= 0x80
+    return out.reshape(rows.shape)
+
+
+def _tied_gate_up(w, mlp):
+    """gate_up whose hidden state repeats each block's first 64 columns with
+    signs -, -, + at offsets 64, 128, 192: every 256-value block of every row
+    holds its largest magnitude four times, in both 128-column halves and in
+    both 64-column groups of each, the first occurrence at the lowest column
+    (gate rows copied, up rows copied or negated; silu(g) (-u) = -(silu(g) u))."""
+    t, data, rows, cols = w["gate_up"]
+    d = np.asarray(data).reshape(rows, -1).copy()
+    for b in range(mlp // 256):
+        c = 256 * b
+        for off, neg in ((64, True), (128, True), (192, False)):
+            d[c + off:c + off + 64] = d[c:c + 64]
+            up = d[mlp + c:mlp + c + 64]
+            d[mlp + c + off:mlp + c + off + 64] = _q4k_negated(up) if neg else up
+    w["gate_up"] = (t, d.reshape(-1), rows, cols)
+
+
+@pytest.mark.parametrize("case", ["1024x1024", "ragged_ties"])
+def test_hidden_rounding_in_gate_up_epilogue_bit_identical(torch_cuda, qctx, monkeypatch, case):
+    """The candle-mode Q8_K rounding of the SwiGLU hidden state, done by the
+    large-M gate_up kernel's epilogue (one workgroup per pair of 256-row tiles,
+    the 256 hidden columns of a Q8_K block), against the same rounding as its
+    own pass after the GEMM (QIMM_SEPARATE_ROUNDING=1): bit-identical block
+    outputs. Cases: the 1024^2 Q4_K_M block (4096 tokens, MLP 12288: 16 token
+    tiles x 48 tile pairs), and hidden 1024 / MLP 4096 at 1100 tokens (a last
+    token tile of 76 rows) with every block's largest magnitude tied four times
+    across both tiles and both wave groups, opposite signs included."""
+    if case == "1024x1024":
+        cfg, b, s, p = CFG4, 1, 4096, 256
+    else:
+        cfg, b, s, p = dict(hidden=1024, heads=8, head_dim=128, mlp=4096), 1, 1100, 64
+    print(f"case: {case}, hidden {cfg['hidden']}, MLP {cfg['mlp']}, {s} tokens", flush=True)
+    w, x, mod, pe, kpre, vpre = make_case(21, cfg, b, s, p, synth.Q4_K, synth.Q6_K)
+    if case == "ragged_ties":
+        _tied_gate_up(w, cfg["mlp"])
+    fused, _ = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
+    monkeypatch.setenv("QIMM_SEPARATE_ROUNDING", "1")
+    separate, _ = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
+    assert np.isfinite(fused).all()
+    diff = np.count_nonzero(fused.view(np.uint32) != separate.view(np.uint32))
+    print(f"outputs differing in any bit: {diff} of {fused.size}", flush=True)
+    assert diff == 0
+
+
 def multi_ref_pe(text_len, cond, grid):
     """RoPE rows of the target over a joint layout of text, condition images and
     the target (EmbedNd::forward, src/rope.rs:104-211): positions run on past the

@@ -106,17 +106,31 @@ __device__ __forceinline__ float group_sum(float v, int width) {
     return v;
 }
 
-// bf16 bits of the exact product d * q, rounded once to nearest even. p = d*q
-// is the f32 rounding and e = d*q - p its exact error (one fma); the bf16
-// rounding of p equals that of the exact product except when p sits exactly
-// halfway between two bf16 values, where the sign of e decides.
-__device__ __forceinline__ uint32_t bf16_of_product(float d, float q) {
-    const float p = d * q;
-    const float e = __builtin_fmaf(d, q, -p);
+// An f32 whose rounding to bf16 (nearest even, as pack_bf16x2 rounds) is that
+// of the exact product d * q, for an integer code q (|q| <= 128: the product
+// has at most 32 significant bits). p = fma(d, q, +0) is the product rounded
+// once to f32, and +0 for q = 0 whatever the signs. The bf16 rounding of p is
+// the exact product's unless p lies exactly halfway between two bf16 values
+// (low half 0x8000) while the product is not p: then p moves one f32 ulp
+// toward the product (its error e = dq - p by one fma gives the side), off the
+// halfway point. That case is rare and sits behind a branch.
+__device__ __forceinline__ float product_for_bf16(float d, float q) {
+    const float p = __builtin_fmaf(d, q, 0.f);
     const uint32_t b = __float_as_uint(p);
-    uint32_t r = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
-    if ((b & 0xffffu) == 0x8000u && e != 0.f) r = ((e > 0.f) == (p > 0.f)) ? (b >> 16) + 1u : (b >> 16);
-    return q == 0.f ? 0u : r;  // a zero code gives +0 whatever the signs (the codes are integers)
+    if (__builtin_expect((b & 0xffffu) == 0x8000u, 0)) {
+        const float e = __builtin_fmaf(d, q, -p);
+        // same signs: the product is larger in magnitude, so is the next pattern
+        if (e != 0.f) return __uint_as_float(((__float_as_uint(e) ^ b) >> 31) ? b - 1u : b + 1u);
+    }
+    return p;
+}
+
+// Rounding half away from zero for |x| < 2^22: x plus the largest float below
+// 1/2 with x's sign, truncated. The sum reaches the next integer exactly when
+// x's fraction is at least 1/2: below that it stays short of the integer by
+// more than half an ulp of the sum, so its own rounding does not reach it.
+__device__ __forceinline__ float round_half_away(float x) {
+    return __builtin_truncf(x + __builtin_copysignf(0.49999997f, x));
 }
 
 // The activation rounding of candle's CPU QMatMul (candle-core 0.11
@@ -128,7 +142,7 @@ __device__ __forceinline__ uint32_t bf16_of_product(float d, float q) {
 //  QBLK 32, BlockQ8_0::from_float: each aligned group of 8 lanes is one block;
 //    d = amax/127, q = round(x / d) computed as x * (1/d), and the block keeps d
 //    as f16 (round to nearest even).
-// Returns the four bf16 operands bf16(d * q) (bf16_of_product), packed in
+// Returns the four bf16 operands bf16(d * q) (product_for_bf16), packed in
 // pairs. Every lane of the block must take part (whole waves for 256, whole
 // 8-lane groups for 32); all-zero blocks give zeros, as candle's d = 0 does.
 // max over each aligned group of 8 lanes (a >= 0 or any floats): DPP moves
@@ -155,13 +169,14 @@ __device__ __forceinline__ float max_wave(float a) {
 
 // Q8_K block rounding from the block's largest magnitude a and the signed value
 // xmax at its first occurrence: iscale s = -128 / xmax and d = 1 / s (both 0
-// for an all-zero block); one value's operand is bf16(d * min(127, round(v s))).
+// for an all-zero block); one value's operand is bf16(d * min(127, round(v s))),
+// q8k_value giving the f32 to round to bf16.
 __device__ __forceinline__ void q8k_scales(float a, float xmax, float &s, float &d) {
     s = a == 0.f ? 0.f : -128.f / xmax;
     d = a == 0.f ? 0.f : 1.f / s;
 }
-__device__ __forceinline__ uint32_t q8k_operand(float v, float s, float d) {
-    return bf16_of_product(d, fminf(roundf(v * s), 127.f));
+__device__ __forceinline__ float q8k_value(float v, float s, float d) {
+    return product_for_bf16(d, fminf(round_half_away(v * s), 127.f));
 }
 
 template <int QBLK>
@@ -183,14 +198,14 @@ __device__ __forceinline__ u32x2 quant_act4(f32x4 v) {
         s = d32 != 0.f ? 1.f / d32 : 0.f;
         d = (float)(_Float16)d32;
     }
-    float q[4];
+    float p[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        q[i] = roundf(v[i] * s);
-        if constexpr (QBLK == 256) q[i] = fminf(q[i], 127.f);
+        float q = round_half_away(v[i] * s);
+        if constexpr (QBLK == 256) q = fminf(q, 127.f);
+        p[i] = product_for_bf16(d, q);
     }
-    return u32x2{bf16_of_product(d, q[0]) | (bf16_of_product(d, q[1]) << 16),
-                 bf16_of_product(d, q[2]) | (bf16_of_product(d, q[3]) << 16)};
+    return u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
 }
 
 }  // namespace qimm

@@ -511,6 +511,18 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
             const int G = wave >> 2, sub = wave & 3;
             const int64_t hc = n0 / 2 + 64 * G + 16 * sub + 4 * g;
             const int cb = (int)(hc & 255);  // its column in the Q8_K block
+            // second tile: this lane's own f32 stores of the first tile, 128
+            // columns back, loaded first so they arrive during the work below
+            f32x4 ha[8][2];
+            if constexpr (t == 1) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int64_t m = min(m0 + 32 * i + l32, M - 1);
+                    const float *frow = ep.hmid_f32 + m * ep.ldh + hc - 128;
+#pragma unroll
+                    for (int j = 0; j < 2; j++) ha[i][j] = *(const f32x4 *)(frow + 8 * j);
+                }
+            }
             float h[8][8];
 #pragma unroll
             for (int i = 0; i < 8; i++)
@@ -593,18 +605,14 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
                     if (m >= M) continue;
                     const float sc = tsc[32 * i + l32], dq = tdq[32 * i + l32];
                     uint16_t *hrow = ep.hmid + m * ep.ldh + hc;
-                    // this lane's own f32 stores of the first tile, 128 columns back
-                    const float *frow = ep.hmid_f32 + m * ep.ldh + hc - 128;
 #pragma unroll
                     for (int j = 0; j < 2; j++) {
                         const float *v = &h[i][4 * j];
-                        const f32x4 u = *(const f32x4 *)(frow + 8 * j);
-                        *(u32x2 *)(hrow + 8 * j) =
-                            u32x2{q8k_operand(v[0], sc, dq) | (q8k_operand(v[1], sc, dq) << 16),
-                                  q8k_operand(v[2], sc, dq) | (q8k_operand(v[3], sc, dq) << 16)};
-                        *(u32x2 *)(hrow - 128 + 8 * j) =
-                            u32x2{q8k_operand(u[0], sc, dq) | (q8k_operand(u[1], sc, dq) << 16),
-                                  q8k_operand(u[2], sc, dq) | (q8k_operand(u[3], sc, dq) << 16)};
+                        const f32x4 u = ha[i][j];
+                        *(u32x2 *)(hrow + 8 * j) = u32x2{pack_bf16x2(q8k_value(v[0], sc, dq), q8k_value(v[1], sc, dq)),
+                                                         pack_bf16x2(q8k_value(v[2], sc, dq), q8k_value(v[3], sc, dq))};
+                        *(u32x2 *)(hrow - 128 + 8 * j) = u32x2{pack_bf16x2(q8k_value(u[0], sc, dq), q8k_value(u[1], sc, dq)),
+                                                               pack_bf16x2(q8k_value(u[2], sc, dq), q8k_value(u[3], sc, dq))};
                     }
                 }
             }

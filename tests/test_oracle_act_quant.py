@@ -149,3 +149,67 @@ def test_product_is_rounded_once():
         d = np.float32(1.0) / iscale
         twice.append(O.f32_to_bf16((d * q).astype(np.float32)))
     assert not np.array_equal(np.concatenate(twice), want)
+
+
+def _trunc_plus_below_half(x):
+    """The kernels' round-half-away form (round_half_away in device_common.h):
+    trunc(x + copysign(0.49999997f, x)), the sum rounded once in float32."""
+    c = np.copysign(np.float32(0.49999997), x).astype(np.float32)
+    return np.trunc((x + c).astype(np.float32))
+
+
+def test_round_half_away_three_instruction_form_exhaustive():
+    """trunc(x + copysign(largest float below 1/2, x)) equals half-away-from-zero
+    rounding on every float32 with 2^-3 <= |x| < 2^8 (the |v s| <= 128 range of
+    the activation codes; below 2^-3 both give 0), both signs: including the
+    exact halves, the float just below each half, and 0.49999997 itself, where
+    x + 0.5 would round up to 1."""
+    lo = np.float32(2.0 ** -3).view(np.uint32)
+    hi = np.float32(2.0 ** 8).view(np.uint32)
+    step = 1 << 24
+    for start in range(int(lo), int(hi), step):
+        x = np.arange(start, min(start + step, int(hi)), dtype=np.uint32).view(np.float32)
+        for v in (x, -x):
+            got = _trunc_plus_below_half(v)
+            want = _round_away(v)
+            assert np.array_equal(got, want), v[np.nonzero(got != want)[0][:4]]
+    small = np.array([0.0, 2.0 ** -30, 0.1249999, 0.25, 0.49999997], dtype=np.float32)
+    assert np.array_equal(_trunc_plus_below_half(small), _round_away(small))
+    assert np.array_equal(_trunc_plus_below_half(-small), _round_away(-small))
+
+
+def test_product_for_bf16_form():
+    """The kernels' bf16 operand of d * q (product_for_bf16 then round to
+    nearest even): p = fma(d, q, +0) in float32, moved one ulp toward the exact
+    product when p sits exactly halfway between two bf16 values with a nonzero
+    error. Against the exact product's rounding (_bf16_of_f64) for random scales
+    d and every code q in [-128, 127], plus scales chosen so that d * q lands
+    exactly on a bf16 halfway point after its f32 rounding (the nudge in both
+    directions) and q = 0 (+0 whatever d's sign)."""
+    rng = np.random.default_rng(77)
+    d = (rng.standard_normal(4096) * 10.0 ** rng.uniform(-6, 1, 4096)).astype(np.float32)
+    # scales whose products with small codes round to bf16 halfway points:
+    # an 8-bit significand plus the halfway bit, then one f32 ulp either way
+    mid = ((rng.integers(128, 256, 2048) * 2 + 1) * 2.0 ** rng.integers(-20, 0, 2048)).astype(np.float32)
+    for k in (3, 5, 7, 9, 11):
+        t = (mid.astype(np.float64) / k).astype(np.float32)
+        d = np.concatenate([d, t, np.nextafter(t, np.float32(0)), np.nextafter(t, np.float32(1e9)), -t])
+    q = np.arange(-128, 128, dtype=np.float32)
+    D, Q = np.meshgrid(d, q, indexing="ij")
+    D, Q = D.ravel(), Q.ravel()
+    exact = D.astype(np.float64) * Q.astype(np.float64)
+    p = (exact + 0.0).astype(np.float32)  # f32 rounding of the exact product
+    p[Q == 0] = np.float32(0.0)
+    b = p.view(np.uint32).copy()
+    e = exact - p.astype(np.float64)
+    tie = ((b & 0xFFFF) == 0x8000) & (e != 0)
+    same = (np.sign(e) == np.sign(p.astype(np.float64)))
+    b[tie & same] += 1
+    b[tie & ~same] -= 1
+    pn = b.view(np.float32)
+    r = pn.view(np.uint32)
+    got = ((r + 0x7FFF + ((r >> 16) & 1)) >> 16).astype(np.uint16)
+    want = _bf16_of_f64(exact)
+    assert tie.sum() > 1000  # the halfway case is exercised
+    assert np.array_equal(got, want)
+    assert np.all(got[Q == 0] == 0)

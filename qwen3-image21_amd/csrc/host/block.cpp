@@ -276,15 +276,15 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
 #define STAGE_MARK(i) \
     if (blk->profiling) QIMM_HIP(ctx, hipEventRecord(blk->ev[i], s))
     STAGE_MARK(0);
-    // modulation.chunk(4) -> (1 + scale1, tanh gate1, 1 + scale2, tanh gate2)
     const int64_t rows_per = seq / mod_rows;  // tokens sharing one modulation row
-    QIMM_HIP(ctx, qimm::launch_mod_prep(mod, batch * mod_rows, hid, modp, s));
     // norm1(x) * (1 + scale1)                                  (:267-269)
     // In candle mode the output is already the q/k/v matmuls' quantized input
     // (Linear::forward -> QMatMul::forward rounds its f32 input rows, :19-29).
+    // The same launch prepares modulation.chunk(4) -> (1 + scale1, tanh gate1,
+    // 1 + scale2, tanh gate2) into modp for the later stages.
     const qimm_weight *qkv0 = blk->qkv_fused ? blk->qkv : blk->q;
     int qb_norm1 = act_qblk(blk, qkv0);
-    QIMM_HIP(ctx, qimm::launch_ln_mod(x, M, hid, modp, 4 * hid, rows_per, xn, s, qb_norm1));
+    QIMM_HIP(ctx, qimm::launch_ln_mod(x, M, hid, mod, 4 * hid, rows_per, xn, s, qb_norm1, modp, batch * mod_rows));
     STAGE_MARK(1);
     // to_q/to_k/to_v + per-head RmsNorm + RoPE                 (:133-142)
     qimm::EpiParams ep{};

@@ -126,20 +126,20 @@ void *noalloc_scratch(int device);
 hipError_t launch_dequant(int ggml_type, const uint8_t *src, int64_t n, float *out,
                           hipStream_t stream);
 
-// modp[r][0:h] = 1 + scale1, [h:2h] = tanh(gate1), [2h:3h] = 1 + scale2,
-// [3h:4h] = tanh(gate2), for each of rows modulation rows [rows][4h].
-hipError_t launch_mod_prep(const float *mod, int64_t rows, int64_t hidden, float *modp,
-                           hipStream_t stream);
-
 // out[m][:] = bf16(LayerNorm(x[m][:]) * modp_scale[(m / rows_per) * stride + :]);
 // one workgroup keeps a row in registers, so hidden <= LN_MAX_HIDDEN
 // (hipErrorInvalidValue beyond).
 // qblk 32 / 256: the output is candle's activation rounding of the f32 values
 // instead (Q8_0 / Q8_K blocks along the row, quant_act4 of device_common.h;
 // hidden % 256 == 0); 0: plain bf16.
+// prep non-null: scale points at the raw modulation rows [prep_rows][4h] (1 is
+// added to their scale1 part here), and the launch also writes their prepared
+// form to prep: prep[r][0:h] = 1 + scale1, [h:2h] = tanh(gate1), [2h:3h] =
+// 1 + scale2, [3h:4h] = tanh(gate2).
 constexpr int64_t LN_MAX_HIDDEN = 8192;
 hipError_t launch_ln_mod(const float *x, int64_t m, int64_t hidden, const float *scale,
-                         int64_t stride, int64_t rows_per, uint16_t *out, hipStream_t stream, int qblk = 0);
+                         int64_t stride, int64_t rows_per, uint16_t *out, hipStream_t stream, int qblk = 0,
+                         float *prep = nullptr, int64_t prep_rows = 0);
 // out[m][:] (bf16, row stride ldo) = candle's activation rounding of the f32
 // rows x[m][:k] (row stride ldx) in blocks of qblk = 32 (Q8_0) or 256 (Q8_K).
 hipError_t launch_quant_rows(const float *x, int64_t ldx, int64_t m, int64_t k, int qblk, uint16_t *out,

@@ -76,13 +76,11 @@ __global__ void dequant_kernel(int type, const uint8_t *__restrict__ src, int64_
 }
 
 // ---- adaLN modulation rows (src/quantized_transformer.rs:259-282) ----
-__global__ void mod_prep_kernel(const float *__restrict__ mod, int64_t n, int64_t hidden,
-                                float *__restrict__ modp) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
+// prepared element i of rows [r][4h]: 1 + scale1 | tanh(gate1) | 1 + scale2 | tanh(gate2)
+__device__ __forceinline__ float mod_prep_value(const float *__restrict__ mod, int64_t i, int64_t hidden) {
     const int64_t part = (i % (4 * hidden)) / hidden;
     const float v = mod[i];
-    modp[i] = (part & 1) ? tanhf(v) : v + 1.0f;
+    return (part & 1) ? tanhf(v) : v + 1.0f;
 }
 
 // ---- LayerNorm (weight 1, bias 0, eps 1e-6) * (1 + scale) -> bf16 ----
@@ -97,13 +95,22 @@ constexpr int LN_MAXV = (int)(LN_MAX_HIDDEN / 4 / 256);  // float4 chunks per th
 // NI > 0: hidden == 1024 NI, every thread holds NI chunks (no guards, so the
 // NI roundings of a thread are independent straight-line code the scheduler
 // interleaves); NI == 0: any hidden, guarded chunks.
+// With `prep` set, scale points at the raw modulation rows (the scale part, 1
+// added here) and the workgroups also write the prepared rows of all of them
+// to prep (grid-strided), which the block's later
+// stages read.
 template <int QBLK, int NI>
 __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x, int64_t hidden,
                                                      const float *__restrict__ scale, int64_t stride,
-                                                     int64_t rows_per, uint16_t *__restrict__ out) {
+                                                     int64_t rows_per, uint16_t *__restrict__ out,
+                                                     const float *__restrict__ mod, float *__restrict__ prep,
+                                                     int64_t prep_n) {
     __shared__ float red[8];
     const int64_t row = blockIdx.x;
     const int tid = threadIdx.x;
+    if (prep)
+        for (int64_t i = row * 256 + tid; i < prep_n; i += (int64_t)gridDim.x * 256)
+            prep[i] = mod_prep_value(mod, i, hidden);
     const float *xr = x + row * hidden;
     const int nv = NI > 0 ? 256 * NI : (int)(hidden / 4);
     // the modulation row is loaded with x, so its latency overlaps the row's
@@ -118,6 +125,13 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x
             sv[i] = *(const f32x4 *)(sc + 4 * c);
             s += v[i][0] + v[i][1] + v[i][2] + v[i][3];
         }
+    }
+    if (prep) {
+        // 1 + scale, the same rounding as the prepared rows
+#pragma unroll
+        for (int i = 0; i < (NI > 0 ? NI : LN_MAXV); i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) sv[i][e] = sv[i][e] + 1.0f;
     }
     s = wave_sum(s);
     if ((tid & 63) == 0) red[tid >> 6] = s;
@@ -307,15 +321,9 @@ hipError_t launch_dequant(int ggml_type, const uint8_t *src, int64_t n, float *o
     return hipGetLastError();
 }
 
-hipError_t launch_mod_prep(const float *mod, int64_t rows, int64_t hidden, float *modp, hipStream_t stream) {
-    const int64_t n = rows * 4 * hidden;
-    if (n <= 0) return hipSuccess;
-    mod_prep_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream>>>(mod, n, hidden, modp);
-    return hipGetLastError();
-}
-
 hipError_t launch_ln_mod(const float *x, int64_t m, int64_t hidden, const float *scale, int64_t stride,
-                         int64_t rows_per, uint16_t *out, hipStream_t stream, int qblk) {
+                         int64_t rows_per, uint16_t *out, hipStream_t stream, int qblk, float *prep,
+                         int64_t prep_rows) {
     if (m <= 0) return hipSuccess;
     if (hidden > LN_MAX_HIDDEN || hidden % 4) return hipErrorInvalidValue;
     if (qblk && hidden % 256) return hipErrorInvalidValue;
@@ -323,7 +331,8 @@ hipError_t launch_ln_mod(const float *x, int64_t m, int64_t hidden, const float 
     const dim3 grid((unsigned)m), block(256);
     auto go = [&](auto qb, auto ni) {
         ln_mod_kernel<decltype(qb)::value, decltype(ni)::value>
-            <<<grid, block, 0, stream>>>(x, hidden, scale, stride, rows_per, out);
+            <<<grid, block, 0, stream>>>(x, hidden, scale, stride, rows_per, out, scale, prep,
+                                         prep ? prep_rows * 4 * hidden : 0);
     };
     using Q0 = std::integral_constant<int, 0>;
     using Q32 = std::integral_constant<int, 32>;

@@ -1579,13 +1579,6 @@ hipError_t launch(const GemmWeight &w, const uint16_t *a, int m, int64_t lda, in
 
 }  // namespace wk
 
-// Sum of the split-K partials of C[m][n], in split order.
-__device__ __forceinline__ float csum(const float *part, int splits, int64_t MN, int64_t idx) {
-    float v = 0.f;
-    for (int s = 0; s < splits; s++) v += part[s * MN + idx];
-    return v;
-}
-
 // Sum of the split-K partials of 4 consecutive outputs at idx (16 B aligned),
 // in split order; every share's 16 B load is issued before the adds.
 constexpr int MAX_SPLITS = 16;  // qgemm_stream_splits and qgemm_mid_splits stay within it
@@ -1637,40 +1630,100 @@ __global__ __launch_bounds__(256) void stream_epi_kernel(const float *__restrict
     }
 }
 
-// QKV epilogue: one wave per (token, head); lane j holds the RoPE pair
-// (2j, 2j+1) of the head's 128 columns.
+// QKV epilogue in one launch. Workgroups [0, nqk): one wave per (token, HG
+// consecutive q or k heads), lane j holding the RoPE pair (2j, 2j+1) of each
+// head's 128 columns (every load of the wave issued before the sums, the HG
+// row reductions independent).
+// The rest: one workgroup per (batch, 32 tokens, v head), which sums the
+// shares of 32 tokens x 128 columns (16 B per thread and share, rows read
+// whole), writes the [B,H,S,D] copy directly and goes through an LDS tile
+// [d][token] for vt [B,H,D,S], whose rows then take 32 consecutive tokens per
+// store run instead of one 2-byte store per value.
+constexpr int VT_T = 32;  // tokens per v workgroup
+constexpr int VT_P = 33;  // bf16 pitch of the transpose tile rows: the 32 rows 4 c of one write go to distinct banks
+template <int HG>
 __global__ __launch_bounds__(256) void stream_qkv_kernel(const float *__restrict__ part, int splits, int64_t M,
-                                                         int64_t N, EpiParams ep) {
+                                                         int64_t N, EpiParams ep, int64_t nqk, int64_t c_first,
+                                                         int64_t heads_v) {
+    __shared__ uint16_t tile[128 * VT_P];
     const int64_t MN = M * N;
-    const int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (token, head slot)
-    const int lane = threadIdx.x & 63;
-    const int64_t heads_here = N / 128;
-    if (g >= M * heads_here) return;
-    const int64_t m = g / heads_here, hs = g % heads_here;
-    const int64_t nb = hs * 128 + ep.n_offset;  // fused column of the head start
-    const int sec = (int)(nb / ep.hidden);
-    const int64_t head = (nb % ep.hidden) / 128;
     const int64_t S = ep.seq, H = ep.heads;
+    if ((int64_t)blockIdx.x >= nqk) {
+        const int64_t sblocks = (S + VT_T - 1) / VT_T;
+        int64_t L = (int64_t)blockIdx.x - nqk;
+        const int64_t hv = L % heads_v;
+        L /= heads_v;
+        const int64_t s0 = (L % sblocks) * VT_T, b = L / sblocks;
+        const int64_t col = c_first + hv * 128;                          // the head's first column in this product
+        const int64_t head = (col + ep.n_offset - 2 * ep.hidden) / 128;  // its index among the v heads
+        const int tid = threadIdx.x, c = tid & 31;
+#pragma unroll
+        for (int r = 0; r < VT_T / 8; r++) {
+            const int i = (tid >> 5) + 8 * r;  // token s0 + i, columns 4 c .. 4 c + 3
+            const int64_t s = min(s0 + i, S - 1);
+            const int64_t m = b * S + s;
+            const f32x4 v = csum4(part, splits, MN, m * N + col + 4 * c);
+            const u32x2 pk{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            if (ep.v_bhsd && s0 + i < S) *(u32x2 *)(ep.v_bhsd + ((b * H + head) * S + s) * 128 + 4 * c) = pk;
+            tile[(4 * c) * VT_P + i] = (uint16_t)(pk[0] & 0xffffu);
+            tile[(4 * c + 1) * VT_P + i] = (uint16_t)(pk[0] >> 16);
+            tile[(4 * c + 2) * VT_P + i] = (uint16_t)(pk[1] & 0xffffu);
+            tile[(4 * c + 3) * VT_P + i] = (uint16_t)(pk[1] >> 16);
+        }
+        __syncthreads();
+        // row d = tid / 2, tokens 16 (tid % 2) .. + 16 of the block
+        const int d = tid >> 1, t0 = (VT_T / 2) * (tid & 1);
+        const int nt = (int)min((int64_t)(VT_T / 2), S - s0 - t0);
+        if (nt <= 0) return;
+        uint16_t *dst = ep.vt + ((b * H + head) * 128 + d) * S + s0 + t0;
+        const uint16_t *src = tile + d * VT_P + t0;
+        if (nt == VT_T / 2 && (S & 7) == 0) {
+            // 16 B aligned: S and s0 + t0 are multiples of 8
+#pragma unroll
+            for (int j = 0; j < VT_T / 16; j++) {
+                u32x4 w;
+#pragma unroll
+                for (int e = 0; e < 4; e++) w[e] = (uint32_t)src[8 * j + 2 * e] | ((uint32_t)src[8 * j + 2 * e + 1] << 16);
+                *(u32x4 *)(dst + 8 * j) = w;
+            }
+        } else {
+            for (int j = 0; j < nt; j++) dst[j] = src[j];
+        }
+        return;
+    }
+    const int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (token, head group)
+    const int lane = threadIdx.x & 63;
+    const int64_t groups = N / (128 * HG);
+    if (g >= M * groups) return;
+    const int64_t m = g / groups, hs = (g % groups) * HG;
+    const int64_t nb = hs * 128 + ep.n_offset;  // fused column of the group's first head
+    const int sec = (int)(nb / ep.hidden);      // a group stays in one section (heads per section % HG == 0)
+    if (sec >= 2) return;                       // v heads: the workgroups after nqk
+    const int64_t head = (nb % ep.hidden) / 128;
     const int64_t b = m / S, s = m % S;
-    const int64_t c0 = hs * 128 + 2 * lane;
-    float x0 = csum(part, splits, MN, m * N + c0), x1 = csum(part, splits, MN, m * N + c0 + 1);
-    if (sec < 2) {
-        const float *nw = sec == 0 ? ep.norm_q : ep.norm_k;
-        const float ss = wave_sum(x0 * x0 + x1 * x1);
+    const float *nw = sec == 0 ? ep.norm_q : ep.norm_k;
+    const float2 w2 = *(const float2 *)(nw + 2 * lane);
+    const float2 cs2 = *(const float2 *)(ep.pe + s * 128 + 2 * lane);  // (cos, sin) of pair lane
+    float2 x[HG];
+#pragma unroll
+    for (int h = 0; h < HG; h++) {
+        const int64_t c0 = m * N + (hs + h) * 128 + 2 * lane;
+        x[h] = make_float2(0.f, 0.f);
+        for (int sp = 0; sp < splits; sp++) {
+            const float2 v = *(const float2 *)(part + sp * MN + c0);
+            x[h].x += v.x;
+            x[h].y += v.y;
+        }
+    }
+    const float osc = sec == 0 ? ep.q_scale : 1.0f;
+    uint16_t *dst = sec == 0 ? ep.q : ep.k;
+#pragma unroll
+    for (int h = 0; h < HG; h++) {
+        const float ss = wave_sum(x[h].x * x[h].x + x[h].y * x[h].y);
         const float rs = 1.0f / sqrtf(ss * (1.0f / 128.0f) + 1e-6f);
-        x0 = x0 * rs * nw[2 * lane];
-        x1 = x1 * rs * nw[2 * lane + 1];
-        const float *pr = ep.pe + s * 128 + 2 * lane;
-        const float cs = pr[0], sn = pr[1];
-        const float osc = sec == 0 ? ep.q_scale : 1.0f;
-        const float y0 = (x0 * cs - x1 * sn) * osc, y1 = (x0 * sn + x1 * cs) * osc;
-        uint16_t *dst = sec == 0 ? ep.q : ep.k;
-        *(uint32_t *)(dst + ((b * H + head) * S + s) * 128 + 2 * lane) = pack_bf16x2(y0, y1);
-    } else {
-        const uint32_t pk = pack_bf16x2(x0, x1);
-        ep.vt[((b * H + head) * 128 + 2 * lane) * S + s] = (uint16_t)(pk & 0xffffu);
-        ep.vt[((b * H + head) * 128 + 2 * lane + 1) * S + s] = (uint16_t)(pk >> 16);
-        if (ep.v_bhsd) *(uint32_t *)(ep.v_bhsd + ((b * H + head) * S + s) * 128 + 2 * lane) = pk;
+        const float x0 = x[h].x * rs * w2.x, x1 = x[h].y * rs * w2.y;
+        const float y0 = (x0 * cs2.x - x1 * cs2.y) * osc, y1 = (x0 * cs2.y + x1 * cs2.x) * osc;
+        *(uint32_t *)(dst + ((b * H + head + h) * S + s) * 128 + 2 * lane) = pack_bf16x2(y0, y1);
     }
 }
 
@@ -1771,8 +1824,22 @@ hipError_t launch_split_epilogue(const float *part, int splits, int64_t m, int64
     case EPI_RESID: stream_epi_kernel<EPI_RESID><<<grid, block, 0, stream>>>(part, splits, m, N, ep); break;
     case EPI_SWIGLU: stream_epi_kernel<EPI_SWIGLU><<<grid, block, 0, stream>>>(part, splits, m, N, ep); break;
     case EPI_QKV: {
-        const int64_t waves = m * (N / 128);
-        stream_qkv_kernel<<<dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream>>>(part, splits, m, N, ep);
+        // q / k heads one wave each, then the v heads (fused columns [2 hidden,
+        // 3 hidden)) by (batch, 32 tokens, head)
+        if (ep.seq <= 0 || m % ep.seq) return hipErrorInvalidValue;
+        // heads per q / k wave: groups never straddle a section boundary
+        const int64_t hps = ep.hidden / 128, off = ep.n_offset / 128, nh = N / 128;
+        const int hg = (hps % 4 == 0 && off % 4 == 0 && nh % 4 == 0) ? 4 : (hps % 2 == 0 && off % 2 == 0 && nh % 2 == 0) ? 2 : 1;
+        const int64_t nqk = (m * (nh / hg) + 3) / 4;
+        const int64_t v0 = std::max<int64_t>(0, 2 * ep.hidden - ep.n_offset);
+        const int64_t v1 = std::min<int64_t>(N, 3 * ep.hidden - ep.n_offset);
+        const int64_t heads_v = v1 > v0 ? (v1 - v0) / 128 : 0;
+        const int64_t nv = heads_v * (m / ep.seq) * ((ep.seq + VT_T - 1) / VT_T);
+        const dim3 grid((unsigned)(nqk + nv));
+        const int64_t hv = std::max<int64_t>(heads_v, 1);
+        if (hg == 4) stream_qkv_kernel<4><<<grid, dim3(256), 0, stream>>>(part, splits, m, N, ep, nqk, v0, hv);
+        else if (hg == 2) stream_qkv_kernel<2><<<grid, dim3(256), 0, stream>>>(part, splits, m, N, ep, nqk, v0, hv);
+        else stream_qkv_kernel<1><<<grid, dim3(256), 0, stream>>>(part, splits, m, N, ep, nqk, v0, hv);
         break;
     }
     default: return hipErrorInvalidValue;

@@ -156,6 +156,35 @@ __device__ __forceinline__ void store_out_f32(float *osf, const f32x16 (&o)[4], 
     }
 }
 
+// bf16 output of a wave's 32 queries x 128 d (the same accumulator layout)
+// into its staging rows (pitch PITCH bf16). With q8 every 32-d slice dt of a
+// query, 16 values in this lane and 16 in its partner half (lane ^ 32), is
+// first rounded as candle's Q8_0 activation block (quant_act4<32>'s
+// arithmetic): the to_out projection's input when its weight is Q8_0.
+template <int PITCH>
+__device__ __forceinline__ void stage_out_bf16(uint16_t *os, const f32x16 (&o)[4], float inv, int lane, bool q8) {
+    const int g = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) {
+        float v[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) v[r] = o[dt][r] * inv;
+        if (q8) {
+            float a = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) a = fmaxf(a, fabsf(v[r]));
+            float sc, dq;
+            q8_0_scales(xmax32(a), sc, dq);
+#pragma unroll
+            for (int r = 0; r < 16; r++) v[r] = q8_0_value(v[r], sc, dq);
+        }
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++)
+            *(u32x2 *)(os + l32 * PITCH + dt * 32 + 8 * rq + 4 * g) =
+                u32x2{pack_bf16x2(v[4 * rq], v[4 * rq + 1]), pack_bf16x2(v[4 * rq + 2], v[4 * rq + 3])};
+    }
+}
+
 namespace fast {
 
 // A workgroup of NW waves (8, or 4 where 8-wave workgroups leave CUs idle)
@@ -183,7 +212,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
                                                                     float sl2, uint16_t *__restrict__ out,
                                                                     float *__restrict__ outf, KeyMask km,
                                                                     const int32_t *__restrict__ lim,
-                                                                    ScoreBound sb) {
+                                                                    ScoreBound sb, int q8) {
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int QB = 32 * NW;  // queries per workgroup
     constexpr int DI = 16 / NW;  // DMA instructions per wave per 16 KB tile
@@ -606,15 +635,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
         return;
     }
     uint16_t *os = (uint16_t *)lds + wave * 32 * OP;
-#pragma unroll
-    for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-        for (int rq = 0; rq < 4; rq++) {
-            const int d = dt * 32 + 8 * rq + 4 * g;
-            u32x2 w{pack_bf16x2(o[dt][4 * rq] * inv, o[dt][4 * rq + 1] * inv),
-                    pack_bf16x2(o[dt][4 * rq + 2] * inv, o[dt][4 * rq + 3] * inv)};
-            *(u32x2 *)(os + l32 * OP + d) = w;
-        }
+    stage_out_bf16<OP>(os, o, inv, lane, q8 != 0);
     __syncthreads();
     const int64_t HDt = H * HD;
 #pragma unroll
@@ -648,7 +669,7 @@ template <bool MASKED>
 __global__ __launch_bounds__(256, 2) void attn_any_kernel(const uint16_t *__restrict__ q, Seg s0, Seg s1,
                                                       int64_t H, int64_t Sq, int64_t nq, int64_t B,
                                                       float sl2, uint16_t *__restrict__ out,
-                                                      float *__restrict__ outf, KeyMask km) {
+                                                      float *__restrict__ outf, KeyMask km, int q8) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
 
@@ -834,15 +855,7 @@ __global__ __launch_bounds__(256, 2) void attn_any_kernel(const uint16_t *__rest
         return;
     }
     uint16_t *os = lds + wave * 32 * OP;
-#pragma unroll
-    for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-        for (int rq = 0; rq < 4; rq++) {
-            const int d = dt * 32 + 8 * rq + 4 * g;
-            u32x2 w{pack_bf16x2(o[dt][4 * rq] * inv, o[dt][4 * rq + 1] * inv),
-                    pack_bf16x2(o[dt][4 * rq + 2] * inv, o[dt][4 * rq + 3] * inv)};
-            *(u32x2 *)(os + l32 * OP + d) = w;
-        }
+    stage_out_bf16<OP>(os, o, inv, lane, q8 != 0);
     __syncthreads();
     const int64_t HDt = H * HD;
 #pragma unroll
@@ -859,25 +872,27 @@ __global__ __launch_bounds__(256, 2) void attn_any_kernel(const uint16_t *__rest
 
 template <int NW, bool PRE, bool MASKED, int SMODE = 0>
 void launch_fast(const uint16_t *q, Seg s0, Seg s1, int64_t h, int64_t sq, int64_t b, float sl2, uint16_t *out,
-                 float *outf, const KeyMask &km, const int32_t *lim, const ScoreBound &sb, hipStream_t stream) {
+                 float *outf, const KeyMask &km, const int32_t *lim, const ScoreBound &sb, int q8,
+                 hipStream_t stream) {
     const int64_t nq = (sq + 32 * NW - 1) / (32 * NW);
     fast::attn_fast_kernel<NW, PRE, MASKED, SMODE><<<dim3((unsigned)(nq * h * b)), dim3(64 * NW), 0, stream>>>(
-        q, s0, s1, h, sq, nq, b, sl2, out, outf, km, lim, sb);
+        q, s0, s1, h, sq, nq, b, sl2, out, outf, km, lim, sb, q8);
 }
 
 // The masked kernel with the softmax form decided on the host where the score
 // bound needs no device value (no prefix keys).
 template <bool PRE>
 void launch_masked(const uint16_t *q, Seg s0, Seg s1, int64_t h, int64_t sq, int64_t b, float sl2, uint16_t *out,
-                   float *outf, const KeyMask &km, const int32_t *lim, const ScoreBound &sb, hipStream_t stream) {
+                   float *outf, const KeyMask &km, const int32_t *lim, const ScoreBound &sb, int q8,
+                   hipStream_t stream) {
     if (sb.q_norm <= 0.f)
-        launch_fast<8, PRE, true, 2>(q, s0, s1, h, sq, b, sl2, out, outf, km, lim, sb, stream);
+        launch_fast<8, PRE, true, 2>(q, s0, s1, h, sq, b, sl2, out, outf, km, lim, sb, q8, stream);
     else if (sb.k_prefix)
-        launch_fast<8, PRE, true, 0>(q, s0, s1, h, sq, b, sl2, out, outf, km, lim, sb, stream);
+        launch_fast<8, PRE, true, 0>(q, s0, s1, h, sq, b, sl2, out, outf, km, lim, sb, q8, stream);
     else if (sb.q_norm * sb.k_own <= STATIC_MAX)
-        launch_fast<8, PRE, true, 1>(q, s0, s1, h, sq, b, sl2, out, outf, km, lim, sb, stream);
+        launch_fast<8, PRE, true, 1>(q, s0, s1, h, sq, b, sl2, out, outf, km, lim, sb, q8, stream);
     else
-        launch_fast<8, PRE, true, 2>(q, s0, s1, h, sq, b, sl2, out, outf, km, lim, sb, stream);
+        launch_fast<8, PRE, true, 2>(q, s0, s1, h, sq, b, sl2, out, outf, km, lim, sb, q8, stream);
 }
 
 // Waves per workgroup of the unmasked fast kernel, from the rounds each form
@@ -902,7 +917,7 @@ int fast_waves(int64_t bh, int64_t sq) {
 template <bool PRE>
 hipError_t launch(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p, const uint16_t *ko,
                   const uint16_t *vto, int64_t so, int64_t b, int64_t h, int64_t sq, float sl2, uint16_t *out,
-                  float *outf, const ScoreBound &sb, hipStream_t stream) {
+                  float *outf, const ScoreBound &sb, int q8, hipStream_t stream) {
     if (sq <= 0 || b <= 0 || h <= 0) return hipSuccess;
     if (p < 0 || so < 0 || p + so <= 0) return hipErrorInvalidValue;
     Seg s0{kp, vtp, p}, s1{ko, vto, so};
@@ -913,13 +928,13 @@ hipError_t launch(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, in
     if ((p & 7) == 0 && (so & 7) == 0) {
         const KeyMask km{nullptr, nullptr, p + so};
         if (fast_waves(b * h, sq) == 4)
-            launch_fast<4, PRE, false>(q, s0, s1, h, sq, b, sl2, out, outf, km, nullptr, sb, stream);
+            launch_fast<4, PRE, false>(q, s0, s1, h, sq, b, sl2, out, outf, km, nullptr, sb, q8, stream);
         else
-            launch_fast<8, PRE, false>(q, s0, s1, h, sq, b, sl2, out, outf, km, nullptr, sb, stream);
+            launch_fast<8, PRE, false>(q, s0, s1, h, sq, b, sl2, out, outf, km, nullptr, sb, q8, stream);
     } else {
         const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;
         anylen::attn_any_kernel<false><<<dim3((unsigned)(nq * h * b)), dim3(256), 0, stream>>>(
-            q, s0, s1, h, sq, nq, b, sl2, out, outf, KeyMask{nullptr, nullptr, p + so});
+            q, s0, s1, h, sq, nq, b, sl2, out, outf, KeyMask{nullptr, nullptr, p + so}, q8);
     }
     return hipGetLastError();
 }
@@ -930,14 +945,14 @@ hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_
                             const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
                             int64_t sq, float scale, uint16_t *out, hipStream_t stream, float *outf) {
     return launch<false>(q, kp, vtp, p, ko, vto, so, b, h, sq, scale * 1.4426950408889634f, out, outf,
-                         ScoreBound{nullptr, 0.f, 0.f}, stream);
+                         ScoreBound{nullptr, 0.f, 0.f}, 0, stream);
 }
 
 hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
                                    const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
                                    int64_t sq, float sl2, const int32_t *img, const uint8_t *kvalid,
                                    int32_t *lim_scratch, uint16_t *out, hipStream_t stream, float *outf,
-                                   const float *k_prefix_norm, float q_norm, float k_own_norm) {
+                                   const float *k_prefix_norm, float q_norm, float k_own_norm, int out_q8) {
     if (sq <= 0 || b <= 0 || h <= 0) return hipSuccess;
     if (p < 0 || so < 0 || p + so <= 0) return hipErrorInvalidValue;
     if (img && (p != 0 || so != sq)) return hipErrorInvalidValue;  // block-causal: one shared sequence
@@ -957,23 +972,25 @@ hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const 
         const ScoreBound sb{p > 0 ? k_prefix_norm : nullptr, q_norm * sl2, k_own_norm};
         // sl2 == 1: q already carries the scale (the block's q/k/v epilogue)
         if (sl2 == 1.0f)
-            launch_masked<true>(q, s0, s1, h, sq, b, sl2, out, outf, km, img ? lim_scratch : nullptr, sb, stream);
+            launch_masked<true>(q, s0, s1, h, sq, b, sl2, out, outf, km, img ? lim_scratch : nullptr, sb, out_q8,
+                                stream);
         else
-            launch_masked<false>(q, s0, s1, h, sq, b, sl2, out, outf, km, img ? lim_scratch : nullptr, sb, stream);
+            launch_masked<false>(q, s0, s1, h, sq, b, sl2, out, outf, km, img ? lim_scratch : nullptr, sb, out_q8,
+                                 stream);
         return hipGetLastError();
     }
     const int64_t nq = (sq + anylen::QB - 1) / anylen::QB;
     anylen::attn_any_kernel<true><<<dim3((unsigned)(nq * h * b)), dim3(256), 0, stream>>>(
-        q, s0, s1, h, sq, nq, b, sl2, out, outf, km);
+        q, s0, s1, h, sq, nq, b, sl2, out, outf, km, out_q8);
     return hipGetLastError();
 }
 
 hipError_t launch_attention_log2(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp, int64_t p,
                                  const uint16_t *ko, const uint16_t *vto, int64_t so, int64_t b, int64_t h,
                                  int64_t sq, uint16_t *out, hipStream_t stream, float *outf,
-                                 const float *k_prefix_norm, float q_norm, float k_own_norm) {
+                                 const float *k_prefix_norm, float q_norm, float k_own_norm, int out_q8) {
     return launch<true>(q, kp, vtp, p, ko, vto, so, b, h, sq, 1.0f, out, outf,
-                        ScoreBound{p > 0 ? k_prefix_norm : nullptr, q_norm, k_own_norm}, stream);
+                        ScoreBound{p > 0 ? k_prefix_norm : nullptr, q_norm, k_own_norm}, out_q8, stream);
 }
 
 }  // namespace qimm

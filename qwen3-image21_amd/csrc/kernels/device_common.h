@@ -178,6 +178,15 @@ __device__ __forceinline__ void q8k_scales(float a, float xmax, float &s, float 
 __device__ __forceinline__ float q8k_value(float v, float s, float d) {
     return product_for_bf16(d, fminf(round_half_away(v * s), 127.f));
 }
+// Q8_0 block rounding from the block's largest magnitude a: q = round(v s) with
+// s = 1 / (a / 127) (0 for an all-zero block), the value d q with d = a / 127
+// kept as f16; q8_0_value gives the f32 to round to bf16.
+__device__ __forceinline__ void q8_0_scales(float a, float &s, float &d) {
+    const float d32 = a / 127.f;
+    s = d32 != 0.f ? 1.f / d32 : 0.f;
+    d = (float)(_Float16)d32;
+}
+__device__ __forceinline__ float q8_0_value(float v, float s, float d) { return product_for_bf16(d, round_half_away(v * s)); }
 
 template <int QBLK>
 __device__ __forceinline__ u32x2 quant_act4(f32x4 v) {
@@ -193,10 +202,7 @@ __device__ __forceinline__ u32x2 quant_act4(f32x4 v) {
         const float xmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), first));
         q8k_scales(a, xmax, s, d);
     } else {
-        a = max8_lanes(a);
-        const float d32 = a / 127.f;
-        s = d32 != 0.f ? 1.f / d32 : 0.f;
-        d = (float)(_Float16)d32;
+        q8_0_scales(max8_lanes(a), s, d);
     }
     float p[4];
 #pragma unroll

@@ -272,3 +272,26 @@ def test_block_reserve_then_forward(torch_cuda, qctx):
     blk.free()
     b, _ = run_block(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre)
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("case", ["config1_fast_4wave", "ragged_any_length"])
+def test_attention_q8_0_rounding_in_epilogue_bit_identical(torch_cuda, qctx, monkeypatch, case):
+    """Q8_0 weights in candle mode: the attention output's Q8_0 rounding (to_out's
+    input, 32 values of one head per block) done by the attention kernel's
+    epilogue against the same rounding as the rows-quantizer pass
+    (QIMM_SEPARATE_ROUNDING=1): bit-identical block outputs. Cases: config 1
+    (hidden 3072, 24 heads, MLP 9216, 256 tokens over 64: the 4-wave fast
+    kernel) and a prefix and token count that are not multiples of 8 (the
+    any-length kernel)."""
+    if case == "config1_fast_4wave":
+        cfg, b, s, p = dict(hidden=3072, heads=24, head_dim=128, mlp=9216), 1, 256, 64
+    else:
+        cfg, b, s, p = SMALL, 2, 100, 61
+    w, x, mod, pe, kpre, vpre = make_case(41, cfg, b, s, p, synth.Q8_0, synth.Q8_0)
+    fused, _ = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
+    monkeypatch.setenv("QIMM_SEPARATE_ROUNDING", "1")
+    separate, _ = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
+    assert np.isfinite(fused).all()
+    diff = np.count_nonzero(fused.view(np.uint32) != separate.view(np.uint32))
+    print(f"{case}: outputs differing in any bit: {diff} of {fused.size}", flush=True)
+    assert diff == 0

@@ -340,3 +340,23 @@ def test_cached_step_equals_uncached_target_rows(torch_cuda, qctx, layout, b, pa
                                 kq, vq, mask=np.broadcast_to(kvalid[:, None, :], (b, tlen, plen + tlen)),
                                 mode=O.CANDLE)
     _check(cached, ref)
+
+
+@pytest.mark.parametrize("layout,b,pads", [(LAYOUT_SMALL, 2, (0, 3)), (LAYOUT_MID, 1, (0,))])
+def test_attention_q8_0_rounding_in_epilogue_bit_identical(torch_cuda, qctx, monkeypatch, layout, b, pads):
+    """The masked prefix pass with Q8_0 weights: the attention output's Q8_0
+    rounding (to_out's input) done by the masked attention kernels' epilogue
+    against the same rounding as the rows-quantizer pass
+    (QIMM_SEPARATE_ROUNDING=1): bit-identical block outputs and k / v."""
+    torch = torch_cuda
+    w, ids, plen, _, pe, x, mod0, _ = _case(31 + b, b, layout, synth.Q8_0, synth.Q8_0)
+    xp, idp, pep = np.ascontiguousarray(x[:, :plen]), ids[:plen], pe[:plen]
+    kvalid = _key_valid(b, idp, pads)
+    blk = _block(torch, qctx, w)
+    got, k, v = _forward_masked(torch, qctx, blk, xp, mod0, pep, idp, kvalid, want_kv=True)
+    monkeypatch.setenv("QIMM_SEPARATE_ROUNDING", "1")
+    ref, kr, vr = _forward_masked(torch, qctx, blk, xp, mod0, pep, idp, kvalid, want_kv=True)
+    blk.free()
+    assert np.isfinite(got).all()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert torch.equal(k, kr) and torch.equal(v, vr)

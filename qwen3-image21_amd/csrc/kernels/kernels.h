@@ -112,9 +112,12 @@ int qgemm_mid_splits(const GemmWeight &w, int64_t m);
 size_t qgemm_workspace(const GemmWeight &w, int64_t m);
 
 // Static scratch of the allocation-free product (noalloc.hip): one file-scope
-// device array per device. The split planners keep qgemm_workspace below
-// ~34 MB for every shape (short-M partials <= 32 MiB, split 128x128 partials
-// <= 16 MiB, plus the counters), so 48 MiB covers them all.
+// device array per device. The split 128x128 partials stay within 32 MiB for
+// every shape (at most two workgroups per CU of f32 128x128 tiles), and the
+// short-M partials within 32 MiB for every projection of the reference's
+// block; with the counters 48 MiB covers them. A product that needs more (one
+// share of m x N x 4 bytes of partials for a very wide bf16 weight at 64
+// tokens) is rejected by the allocation-free entry point.
 constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)48 << 20;  // QIMM_NOALLOC_SCRATCH_BYTES of qimm.h
 // Looks up the array's device address on `device` (which must be current)
 // once, zeroes its counter area and waits; later calls return at once.

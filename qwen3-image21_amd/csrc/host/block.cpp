@@ -196,8 +196,8 @@ int act_qblk(const qimm_block *blk, const qimm_weight *w) {
 // QIMM_SEPARATE_ROUNDING=1 in the environment (read at every forward) rounds
 // the hidden state and the attention output in their own passes even where
 // their producers would round them in their epilogues (the large-M gate_up
-// for Q8_K blocks, the attention kernels for Q8_0): the reference form the
-// fused ones are checked against bit for bit.
+// for Q8_K blocks, the attention kernels for Q8_0 and, paired over two heads,
+// for Q8_K): the reference form the fused ones are checked against bit for bit.
 bool separate_rounding() {
     const char *e = getenv("QIMM_SEPARATE_ROUNDING");
     return e && e[0] == '1';
@@ -328,28 +328,28 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
         const int rc = kv_layer(kv, layer, s, &pk, &pvt);
         if (rc) return rc;
     }
-    // candle mode: to_out's activation rounding. Q8_0 blocks (32 values, within a
-    // head) are rounded by the attention kernel itself; Q8_K blocks span two
-    // heads, so the output leaves in f32 for the rows quantizer.
+    // candle mode: to_out's activation rounding, done by the attention launch
+    // (in its kernels' epilogue where they can; the f32 staging is its scratch)
     const int qb_out = act_qblk(blk, blk->out);
     float *stage_f32 = (float *)(ws + L.f32);
-    const bool att_q8 = qb_out == 32 && !separate_rounding();
-    float *att_f32 = qb_out && !att_q8 ? stage_f32 : nullptr;
+    const bool round_sep = separate_rounding();
+    const int att_q = round_sep ? 0 : qb_out;
+    float *att_f32 = qb_out ? stage_f32 : nullptr;
     // score bound: q and own k from the RmsNorm weights, prefix k from the cache
     const float *kpn = kv ? kv->knorm + layer : nullptr;
     if (img || kvalid)
         QIMM_HIP(ctx, qimm::launch_attention_masked(qb, pk, pvt, P, kb, vt, seq, batch, H, seq, 1.0f, img, kvalid,
                                                     (int32_t *)(ws + L.lim), att, s, att_f32, kpn,
-                                                    blk->q_norm_bound, blk->k_norm_bound, att_q8));
+                                                    blk->q_norm_bound, blk->k_norm_bound, att_q));
     else
         QIMM_HIP(ctx, qimm::launch_attention_log2(qb, pk, pvt, P, kb, vt, seq, batch, H, seq, att, s, att_f32, kpn,
-                                                  blk->q_norm_bound, blk->k_norm_bound, att_q8));
+                                                  blk->q_norm_bound, blk->k_norm_bound, att_q));
     if (kv) {
         const int rc = kv_release(kv, layer, s);
         if (rc) return rc;
     }
     STAGE_MARK(3);
-    if (att_f32) QIMM_HIP(ctx, qimm::launch_quant_rows(att_f32, hid, M, hid, qb_out, att, hid, s));
+    if (round_sep && qb_out) QIMM_HIP(ctx, qimm::launch_quant_rows(att_f32, hid, M, hid, qb_out, att, hid, s));
     STAGE_MARK(4);
     // x1 = x + tanh(gate1) * to_out(attn)                       (:150-151, 271-273)
     qimm::EpiParams er{};

@@ -153,9 +153,12 @@ inline int act_block(int fmt) { return fmt == WF_Q8_0 ? 32 : (fmt == WF_Q4_K || 
 
 // Joint attention over [prefix ; own] keys. q, k_* : [B,H,S,128] bf16;
 // vt_* : [B,H,128,S] bf16; out [B,Sq,H*128] bf16, or outf [B,Sq,H*128] f32
-// instead when outf is set (out is then not written). out_q8 (without outf):
-// out holds candle's Q8_0 activation rounding of the output, bf16(d q) per 32
-// values (quant_act4<32>), the to_out input when its weight is Q8_0.
+// instead when outf is set (out is then not written). out_qblk 32 / 256: out
+// holds candle's activation rounding of the output instead, bf16(d q) per Q8_0
+// (32 values) / Q8_K (256 values) block (quant_act4's arithmetic), the to_out
+// input in the candle mode: Q8_0 in the kernels' epilogue; Q8_K by the paired
+// cached-step kernel where it runs (an even head count), else through outf
+// (then required, f32 scratch) and the rows quantizer.
 hipError_t launch_attention(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp,
                             int64_t p, const uint16_t *ko, const uint16_t *vto, int64_t so,
                             int64_t b, int64_t h, int64_t sq, float scale, uint16_t *out,
@@ -171,14 +174,14 @@ hipError_t launch_attention_masked(const uint16_t *q, const uint16_t *kp, const 
                                    int64_t sq, float sl2, const int32_t *img, const uint8_t *kvalid,
                                    int32_t *lim_scratch, uint16_t *out, hipStream_t stream,
                                    float *outf = nullptr, const float *k_prefix_norm = nullptr,
-                                   float q_norm = 0.f, float k_own_norm = 0.f, int out_q8 = 0);
+                                   float q_norm = 0.f, float k_own_norm = 0.f, int out_qblk = 0);
 // The same with q already multiplied by scale * log2(e) (the QKV epilogue's
 // q_scale), so scores are in log2 units.
 hipError_t launch_attention_log2(const uint16_t *q, const uint16_t *kp, const uint16_t *vtp,
                                  int64_t p, const uint16_t *ko, const uint16_t *vto, int64_t so,
                                  int64_t b, int64_t h, int64_t sq, uint16_t *out, hipStream_t stream,
                                  float *outf = nullptr, const float *k_prefix_norm = nullptr,
-                                 float q_norm = 0.f, float k_own_norm = 0.f, int out_q8 = 0);
+                                 float q_norm = 0.f, float k_own_norm = 0.f, int out_qblk = 0);
 // Score bound of the fast kernels (both launches above): with q_norm >= every
 // query's norm (as passed, before sl2), k_own_norm >= every own key's norm and,
 // when there is a prefix, *k_prefix_norm (device) >= every prefix key's norm,

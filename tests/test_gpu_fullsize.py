@@ -130,6 +130,44 @@ def test_hidden_rounding_in_gate_up_epilogue_bit_identical(torch_cuda, qctx, mon
     assert diff == 0
 
 
+def _tied_heads(w, kpre, vpre, heads):
+    """q, k of head 2j + 1 copied from head 2j, its v (weights and prefix values)
+    negated: the attention outputs of the pair are exact negations of each
+    other, so every query's largest magnitude over the pair's 256 output
+    columns ties across the two heads with opposite signs."""
+    for name, neg in (("to_q", False), ("to_k", False), ("to_v", True)):
+        t, data, rows, cols = w[name]
+        d = np.asarray(data).reshape(rows, -1).copy()
+        for j in range(0, heads, 2):
+            src = d[128 * j:128 * (j + 1)]
+            d[128 * (j + 1):128 * (j + 2)] = _q4k_negated(src) if neg else src
+        w[name] = (t, d.reshape(-1), rows, cols)
+    kpre[:, 1::2] = kpre[:, 0::2]
+    vpre[:, 1::2] = vpre[:, 0::2] ^ np.uint16(0x8000)
+
+
+@pytest.mark.parametrize("case", ["heads_tied"])
+def test_attention_q8k_pair_rounding_bit_identical(torch_cuda, qctx, monkeypatch, case):
+    """The candle-mode Q8_K rounding of the attention output (to_out's input,
+    256 values = two heads of a query), done by the paired cached-step attention
+    kernel (one workgroup per head pair, the first head's f32 output through
+    scratch), against the rows-quantizer pass (QIMM_SEPARATE_ROUNDING=1):
+    bit-identical block outputs, with the pair's maxima tied across the two
+    heads with opposite signs in every query (the first head must win). Hidden
+    4096, 32 heads, 2048 tokens over 256: the 8-wave form. The 1024^2 case of
+    the gate_up test above covers the untied full size."""
+    cfg, b, s, p = dict(hidden=4096, heads=32, head_dim=128, mlp=4096), 1, 2048, 256
+    w, x, mod, pe, kpre, vpre = make_case(23, cfg, b, s, p, synth.Q4_K, synth.Q6_K)
+    _tied_heads(w, kpre, vpre, cfg["heads"])
+    fused, _ = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
+    monkeypatch.setenv("QIMM_SEPARATE_ROUNDING", "1")
+    separate, _ = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
+    assert np.isfinite(fused).all()
+    diff = np.count_nonzero(fused.view(np.uint32) != separate.view(np.uint32))
+    print(f"{case}: outputs differing in any bit: {diff} of {fused.size}", flush=True)
+    assert diff == 0
+
+
 def multi_ref_pe(text_len, cond, grid):
     """RoPE rows of the target over a joint layout of text, condition images and
     the target (EmbedNd::forward, src/rope.rs:104-211): positions run on past the

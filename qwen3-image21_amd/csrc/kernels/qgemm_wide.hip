@@ -261,7 +261,10 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
     // per-token largest magnitude, and the block column of its first
     // occurrence times 2 plus its sign bit (one LDS object, so the compiler
     // tells the direct loads into one stage from the reads of the other)
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE + (PAIR ? 2 * BM * 4 : 0)];
+    // (the q/k/v epilogue stages both heads' rows, 2 x 64 KB, and its
+    // reduction table, 8 KB, past the activation stages' 64 KB)
+    __shared__ __attribute__((aligned(16))) uint8_t
+        lds[2 * STAGE + (PAIR ? 2 * BM * 4 : 0) + (EPI == EPI_QKV ? 2 * STAGE + NW * BM * 4 : 0)];
     float *pair_amax = (float *)(lds + 2 * STAGE);
     int *pair_first = (int *)(lds + 2 * STAGE + BM * 4);
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -627,9 +630,27 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
             const int64_t H = ep.heads, S = ep.seq;
             if (sec < 2) {
                 // RmsNorm over the head: each lane's 16 squares, the partner half
-                // (lane ^ 32), then the head's four waves through LDS
-                float *red = (float *)lds;  // [8 waves][256 tokens]
-                __syncthreads();            // every wave is done with the operand stages
+                // (lane ^ 32), then the head's four waves through LDS. The RoPE
+                // (cos, sin) of the lane's 16 dims for its token of tile i are
+                // loaded one tile ahead (the first before the reduction), with
+                // the row clamped so that every load is unconditional.
+                const int dbase = 32 * sub + 4 * g;  // + 8 j
+                f32x4 cs[2][4];
+                auto load_pe = [&](int i) __attribute__((always_inline)) {
+                    const uint32_t m = (uint32_t)min(m0 + 32 * i + l32, M - 1);
+                    const float *pr = ep.pe + (int64_t)(m % Su) * 128;  // (cos, sin) of pair i at 2i, 2i + 1
+#pragma unroll
+                    for (int j = 0; j < 4; j++) cs[i & 1][j] = *(const f32x4 *)(pr + dbase + 8 * j);
+                };
+                load_pe(0);
+                typedef __attribute__((address_space(4))) const f32x4 cf32x4;
+                const __attribute__((address_space(4))) float *nwt =
+                    (const __attribute__((address_space(4))) float *)(sec == 0 ? ep.norm_q : ep.norm_k);
+                f32x4 wv[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) wv[j] = *(const cf32x4 *)(nwt + dbase + 8 * j);
+                float *red = (float *)(lds + 4 * STAGE);  // [8 waves][256 tokens], past the row staging
+                __syncthreads();                           // every wave is done with the operand stages
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
                     float ss = 0.f;
@@ -640,38 +661,43 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
                     if (g == 0) red[wave * 256 + 32 * i + l32] = lo + hi;
                 }
                 __syncthreads();
-                typedef __attribute__((address_space(4))) const f32x4 cf32x4;
-                const __attribute__((address_space(4))) float *nwt =
-                    (const __attribute__((address_space(4))) float *)(sec == 0 ? ep.norm_q : ep.norm_k);
                 const float osc = sec == 0 ? ep.q_scale : 1.0f;
                 uint16_t *dst = sec == 0 ? ep.q : ep.k;
-                const int dbase = 32 * sub + 4 * g;  // + 8 j
+                // the rows go through LDS: head G's 256 tokens x 128 dims of bf16
+                // in its own 64 KB (256 B rows, 16 B chunk c of row t at slot
+                // c ^ (t % 16)), then both heads are stored as whole 256 B rows
+                uint16_t *stg = (uint16_t *)lds + G * (256 * 128);
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
+                    if (i + 1 < 8) load_pe(i + 1);
                     const int t = 32 * i + l32;
-                    const int64_t m = m0 + t;
-                    if (m >= M) continue;
                     const float *rr = red + 4 * G * 256 + t;
-                    const float tot = (rr[0] + rr[256]) + (rr[512] + rr[768]);
-                    const float rs = 1.0f / sqrtf(tot * (1.0f / 128.0f) + 1e-6f);
-                    const uint32_t s = (uint32_t)m % Su, b = (uint32_t)m / Su;
-                    const float *pr = ep.pe + (int64_t)s * 128;  // (cos, sin) of pair i at 2i, 2i + 1
-                    uint16_t *drow = dst + (((int64_t)b * H + head) * S + s) * 128;
+                    const float rs = 1.0f / sqrtf(((rr[0] + rr[256]) + (rr[512] + rr[768])) * (1.0f / 128.0f) + 1e-6f);
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
-                        const int d = dbase + 8 * j;
-                        const f32x4 cs = *(const f32x4 *)(pr + d);
-                        const f32x4 wv = *(const cf32x4 *)(nwt + d);
                         uint32_t o[2];
 #pragma unroll
                         for (int e = 0; e < 2; e++) {
-                            const float x0 = acc[i][4 * j + 2 * e] * rs * wv[2 * e];
-                            const float x1 = acc[i][4 * j + 2 * e + 1] * rs * wv[2 * e + 1];
-                            const float co = cs[2 * e], sn = cs[2 * e + 1];
+                            const float x0 = acc[i][4 * j + 2 * e] * rs * wv[j][2 * e];
+                            const float x1 = acc[i][4 * j + 2 * e + 1] * rs * wv[j][2 * e + 1];
+                            const float co = cs[i & 1][j][2 * e], sn = cs[i & 1][j][2 * e + 1];
                             o[e] = pack_bf16x2((x0 * co - x1 * sn) * osc, (x0 * sn + x1 * co) * osc);
                         }
-                        *(u32x2 *)(drow + d) = u32x2{o[0], o[1]};
+                        // dims dbase + 8 j: chunk 4 sub + j, half g of it
+                        const int c = (4 * sub + j) ^ (t & 15);
+                        *(u32x2 *)(stg + t * 128 + 8 * c + 4 * g) = u32x2{o[0], o[1]};
                     }
+                }
+                __syncthreads();
+                const int64_t head0 = head - G;  // the tile's first head
+#pragma unroll
+                for (int k = 0; k < 16; k++) {
+                    const int ch = tid + 512 * k, hg = ch >> 12, t = (ch >> 4) & 255, c = ch & 15;
+                    const int64_t m = m0 + t;
+                    if (m >= M) continue;
+                    const uint32_t s = (uint32_t)m % Su, b = (uint32_t)m / Su;
+                    *(u32x4 *)(dst + (((int64_t)b * H + head0 + hg) * S + s) * 128 + 8 * c) =
+                        *(const u32x4 *)((uint16_t *)lds + hg * (256 * 128) + t * 128 + 8 * (c ^ (t & 15)));
                 }
             } else {
                 // v: transposed to vt [B,H,128,S] (consecutive lanes hold

@@ -162,22 +162,13 @@ def main():
 
 
     # ---- per-stage device times inside the step (HIP events on the launch stream) ----
-    stage_sum, nprof = {}, 0
-    for blk in blocks:
-        blk.profile(True)
-    for i in range(args.profile_steps):
-        step(i)
-        for k, v in blocks[i % len(blocks)].stage_times().items():
-            stage_sum[k] = stage_sum.get(k, 0.0) + v
-        nprof += 1
-    for blk in blocks:
-        blk.profile(False)
     att_flop = 4.0 * HEADS * S_IMG * (S_IMG + P_TXT) * HD
-    kernels = roofline = stages = None
-    if nprof == 0:
+    kernels = roofline = None
+    stages = stage_profile(blocks, step, args.profile_steps)
+    if stages is None:
         log("bench: no profiled steps, stage report skipped")
     else:
-        stages = {k: v / nprof for k, v in stage_sum.items()}
+        log(f"bench: stage medians sum to {sum(stages.values()):.3f} ms (timed step {ms_step:.3f} ms)")
         kernels, roofline = stage_report(stages, att_flop, synth)
 
     block_flop = att_flop + 2.0 * S_IMG * HID * (3 * HID + HID + 2 * MLP) + 2.0 * S_IMG * MLP * HID
@@ -186,6 +177,7 @@ def main():
     for blk in blocks:
         blk.set_act_mode(qimm.ACT_BF16)
     ms_bf16 = timed(torch, stream, lambda it=iter(range(1 << 30)): step(next(it)), max(8, args.steps // 2), warmup=2)
+    stages_bf16 = stage_profile(blocks, step, args.profile_steps)
     for blk in blocks:
         blk.set_act_mode(qimm.ACT_CANDLE)
     log(f"bench: block step with bf16 activations {ms_bf16:.3f} ms")
@@ -246,6 +238,7 @@ def main():
         "block_tflops": round(block_flop / ms_step / 1e9, 2),
         "block_frac_bf16_peak": round(block_flop / ms_step / 1e9 / PEAK_BF16_TFLOPS, 4),
         "stages_ms": {k: round(v, 4) for k, v in stages.items()} if stages else None,
+        "stages_bf16_activations_ms": {k: round(v, 4) for k, v in stages_bf16.items()} if stages_bf16 else None,
         "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()} if kernels else None,
         "roofline": roofline,
         "denoise_loop": denoise,
@@ -375,6 +368,28 @@ def denoise_loop(ctx, torch, np, qimm, synth, stream, layers=LAYERS, steps=20, c
             "steps": steps, "cfg": "true CFG, 2 prompts x 256 text tokens, sequential batch-1 forwards",
             "reference_published_s": {"value": 30.0, "hardware": "NVIDIA L20", "source": "README.md:133-139",
                                       "note": "context only: other hardware"}}
+
+
+def stage_profile(blocks, step, nsteps, warm=8):
+    """Median ms per stage over `nsteps` block steps timed stage by stage (HIP
+    events between the stages, read back after each step), after `warm`
+    profiled steps that are not counted: the first steps after a long timed
+    loop run up to 20% slow while the clock settles, the median keeps one
+    such step from moving a stage."""
+    if nsteps <= 0:
+        return None
+    per = {}
+    for blk in blocks:
+        blk.profile(True)
+    for i in range(warm + nsteps):
+        step(i)
+        if i >= warm:
+            for k, v in blocks[i % len(blocks)].stage_times().items():
+                per.setdefault(k, []).append(v)
+    for blk in blocks:
+        blk.profile(False)
+    return {k: sorted(v)[len(v) // 2] if len(v) % 2 else 0.5 * sum(sorted(v)[len(v) // 2 - 1:len(v) // 2 + 1])
+            for k, v in per.items()}
 
 
 def stage_report(stages, att_flop, synth):
@@ -660,10 +675,7 @@ def prefix_fill_8448(ctx, torch, np, qimm, synth, stream, iters=4):
                            image_ids=ids_d.data_ptr(), k_out=k_o.data_ptr(), v_out=v_o.data_ptr(), stream=sh)
 
     ms = timed(torch, stream, call, iters)
-    blk.profile(True)
-    call()
-    st = blk.stage_times()
-    blk.profile(False)
+    st = stage_profile([blk], lambda i: call(), 3, warm=2)
     assert torch.isfinite(xo).all().item(), "non-finite prefix output"
     blk.free()
     text_pairs = T * (T + 1) // 2

@@ -195,9 +195,11 @@ int act_qblk(const qimm_block *blk, const qimm_weight *w) {
 
 // QIMM_SEPARATE_ROUNDING=1 in the environment (read at every forward) rounds
 // the hidden state and the attention output in their own passes even where
-// their producers would round them in their epilogues (the large-M gate_up
-// for Q8_K blocks, the attention kernels for Q8_0 and, paired over two heads,
-// for Q8_K): the reference form the fused ones are checked against bit for bit.
+// their producers would round them in their epilogues (the gate_up kernels
+// for Q8_K blocks at large M and for Q8_0 blocks at large M or in the
+// undivided 128x128 kernel, the attention kernels for Q8_0 and, paired over
+// two heads, for Q8_K): the reference form the fused ones are checked against
+// bit for bit.
 bool separate_rounding() {
     const char *e = getenv("QIMM_SEPARATE_ROUNDING");
     return e && e[0] == '1';
@@ -375,9 +377,11 @@ int block_forward_impl(qimm_block *blk, const float *x, float *x_out, int64_t ba
     // candle mode: the hidden state leaves in f32 for the down matmul's rounding
     const int qb_down = act_qblk(blk, blk->down);
     if (qb_down) eg.hmid_f32 = stage_f32;
-    // Q8_K blocks (K-quant down weights): the gate_up launch rounds them itself
-    const bool round_in_gemm = qb_down == 256 && F % 256 == 0 && !separate_rounding();
-    eg.hmid_q8k = round_in_gemm;
+    // the gate_up launch rounds them itself: Q8_K blocks (K-quant down
+    // weights), Q8_0 blocks (Q8_0 down weights)
+    const bool round_in_gemm = (qb_down == 32 || (qb_down == 256 && F % 256 == 0)) && !separate_rounding();
+    eg.hmid_q8k = round_in_gemm && qb_down == 256;
+    eg.hmid_q8_0 = round_in_gemm && qb_down == 32;
     QIMM_HIP(ctx, qimm::launch_qgemm(blk->gate_up->gw, xn, M, hid, qimm::EPI_SWIGLU, eg, s));
     STAGE_MARK(7);
     if (qb_down && !round_in_gemm) QIMM_HIP(ctx, qimm::launch_quant_rows(stage_f32, F, M, F, qb_down, hm, F, s));

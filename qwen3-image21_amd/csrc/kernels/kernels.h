@@ -54,6 +54,12 @@ struct EpiParams {
     // shape for it (the large-M paired kernel, else the f32 state and then the
     // rows quantizer)
     int hmid_q8k = 0;
+    // EPI_SWIGLU with hmid_q8_0 set: hmid receives the hidden state rounded as
+    // candle's Q8_0 activations (bf16(d q), one d per 32 columns of a row), by
+    // the epilogue of the large-M kernel or the undivided 128x128 kernel;
+    // every other path writes the f32 state to hmid_f32 (which must be set)
+    // and rounds it in its own pass. Needs (N / 2) % 32 == 0.
+    int hmid_q8_0 = 0;
     // f32 scratch of part_ws_bytes for the short-M split-K path (optional;
     // without it short M takes the 128x128 kernel)
     float *part_ws = nullptr;

@@ -345,7 +345,22 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(const uint16_t *__restric
 #pragma unroll
             for (int i = 0; i < 8; i++) h[i] = silu(cr[j0 + i]) * cr[64 + j0 + i];
             const int64_t o = m * ep.ldh + n0 / 2 + j0;
-            if (ep.hmid_f32) {
+            if (ep.hmid_q8_0) {
+                // the Q8_0 block of these 8 columns is the 32 of lanes 4q .. 4q + 3
+                // (one row: all four in or out of range together)
+                float a = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(h[i]));
+                a = fmaxf(a, __shfl_xor(a, 1));
+                a = fmaxf(a, __shfl_xor(a, 2));
+                float sc, dq;
+                q8_0_scales(a, sc, dq);
+                uint32_t pk[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    pk[i] = pack_bf16x2(q8_0_value(h[2 * i], sc, dq), q8_0_value(h[2 * i + 1], sc, dq));
+                *(u32x4 *)(ep.hmid + o) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+            } else if (ep.hmid_f32) {
                 *(f32x4 *)(ep.hmid_f32 + o) = f32x4{h[0], h[1], h[2], h[3]};
                 *(f32x4 *)(ep.hmid_f32 + o + 4) = f32x4{h[4], h[5], h[6], h[7]};
             } else {
@@ -543,12 +558,20 @@ size_t small_workspace(const GemmWeight &w, int64_t m) {
 // M < 512: the short-M path when it fits and its scratch is there, else the
 // 128x128 kernel, split over K when its tiles leave CUs idle and scratch is
 // there.
+enum class SmallPath { STREAM, SPLIT, WHOLE };
+SmallPath small_path(const GemmWeight &w, int64_t m, const EpiParams &ep) {
+    if (qgemm_stream_fits(w, m) && ep.part_ws && ep.part_ws_bytes >= qgemm_stream_workspace(w, m))
+        return SmallPath::STREAM;
+    if (qgemm_mid_splits(w, m) > 1 && ep.part_ws && ep.part_ws_bytes >= qgemm_workspace(w, m)) return SmallPath::SPLIT;
+    return SmallPath::WHOLE;
+}
+
 hipError_t launch_small(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi, const EpiParams &ep,
                         hipStream_t stream) {
-    if (qgemm_stream_fits(w, m) && ep.part_ws && ep.part_ws_bytes >= qgemm_stream_workspace(w, m))
-        return launch_qgemm_stream(w, a, m, lda, epi, ep, ep.part_ws, stream);
-    const int splits = qgemm_mid_splits(w, m);
-    if (splits > 1 && ep.part_ws && ep.part_ws_bytes >= qgemm_workspace(w, m)) {
+    const SmallPath path = small_path(w, m, ep);
+    if (path == SmallPath::STREAM) return launch_qgemm_stream(w, a, m, lda, epi, ep, ep.part_ws, stream);
+    if (path == SmallPath::SPLIT) {
+        const int splits = qgemm_mid_splits(w, m);
         // partial sums [splits][m][n] after the counter area, then the fixed-order
         // reduction that applies the epilogue
         float *part = (float *)((char *)ep.part_ws + STREAM_COUNTER_BYTES);
@@ -585,6 +608,20 @@ hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64
         const hipError_t err = launch_qgemm(w, a, m, lda, EPI_SWIGLU, e, stream);
         if (err != hipSuccess) return err;
         return launch_quant_rows(ep.hmid_f32, ep.ldh, m, w.n / 2, 256, ep.hmid, ep.ldh, stream);
+    }
+    if (epi == EPI_SWIGLU && ep.hmid_q8_0) {
+        // the Q8_0 rounding of the hidden state: in the epilogue of the large-M
+        // kernel or the undivided 128x128 kernel where one of them runs, else
+        // the f32 state and then the rows quantizer
+        if (!ep.hmid || !ep.hmid_f32 || (w.n / 2) % 32) return hipErrorInvalidValue;
+        if (qgemm_large_fits(w, m) ? qgemm_wide_fits(w) : small_path(w, m, ep) == SmallPath::WHOLE)
+            return qgemm_large_fits(w, m) ? launch_qgemm_large(w, a, m, lda, epi, ep, stream)
+                                          : launch_small(w, a, m, lda, epi, ep, stream);
+        EpiParams e = ep;
+        e.hmid_q8_0 = 0;
+        const hipError_t err = launch_qgemm(w, a, m, lda, EPI_SWIGLU, e, stream);
+        if (err != hipSuccess) return err;
+        return launch_quant_rows(ep.hmid_f32, ep.ldh, m, w.n / 2, 32, ep.hmid, ep.ldh, stream);
     }
     if (qgemm_large_fits(w, m)) {
         const int64_t tail = (epi == EPI_F32 || epi == EPI_BF16) ? large_tail_rows(w, m) : 0;

@@ -487,20 +487,56 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
             // same hidden columns
             const int G = wave >> 2, sub = wave & 3;
             const int64_t hc = (n0 + 128 * G) / 2 + 16 * sub + 4 * g;  // + 8 j
+            auto hval = [&](int i, int r) __attribute__((always_inline)) { return silu(acc[i][r]) * acc[i][8 + r]; };
+            if (ep.hmid_q8_0) {
+                // candle's Q8_0 rounding: a 32-column block is the 16 columns of
+                // waves sub and sub ^ 1, so each token's largest magnitude comes
+                // from the lane's 8, its partner half (lane ^ 32) and the sibling
+                // wave's through LDS; the values are formed again for the stores
+                float *red = (float *)lds;  // [8 waves][256 tokens]
+                __syncthreads();            // every wave is done with the operand stages
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int64_t m = m0 + 32 * i + l32;
-                if (m >= M) continue;
+                for (int i = 0; i < 8; i++) {
+                    float a = 0.f;
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    float h[4];
+                    for (int r = 0; r < 8; r++) a = fmaxf(a, fabsf(hval(i, r)));
+                    float lo = a, hi = a;
+                    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lo), "+v"(hi));
+                    if (g == 0) red[wave * BM + 32 * i + l32] = fmaxf(lo, hi);
+                }
+                __syncthreads();
 #pragma unroll
-                    for (int e = 0; e < 4; e++) h[e] = silu(acc[i][4 * j + e]) * acc[i][8 + 4 * j + e];
-                    const int64_t o = m * ep.ldh + hc + 8 * j;
-                    if (ep.hmid_f32)
-                        *(f32x4 *)(ep.hmid_f32 + o) = f32x4{h[0], h[1], h[2], h[3]};
-                    else
-                        *(u32x2 *)(ep.hmid + o) = u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+                for (int i = 0; i < 8; i++) {
+                    const int tk = 32 * i + l32;
+                    const int64_t m = m0 + tk;
+                    if (m >= M) continue;
+                    float sc, dq;
+                    q8_0_scales(fmaxf(red[wave * BM + tk], red[(wave ^ 1) * BM + tk]), sc, dq);
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        float q[4];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) q[e] = q8_0_value(hval(i, 4 * j + e), sc, dq);
+                        *(u32x2 *)(ep.hmid + m * ep.ldh + hc + 8 * j) =
+                            u32x2{pack_bf16x2(q[0], q[1]), pack_bf16x2(q[2], q[3])};
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int64_t m = m0 + 32 * i + l32;
+                    if (m >= M) continue;
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        float h[4];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) h[e] = hval(i, 4 * j + e);
+                        const int64_t o = m * ep.ldh + hc + 8 * j;
+                        if (ep.hmid_f32)
+                            *(f32x4 *)(ep.hmid_f32 + o) = f32x4{h[0], h[1], h[2], h[3]};
+                        else
+                            *(u32x2 *)(ep.hmid + o) = u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+                    }
                 }
             }
         } else if constexpr (PAIR) {

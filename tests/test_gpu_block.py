@@ -274,6 +274,32 @@ def test_block_reserve_then_forward(torch_cuda, qctx):
     assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("case", ["config1_128x128", "wide_ragged", "two_k_shares"])
+def test_hidden_q8_0_rounding_in_gate_up_epilogue_bit_identical(torch_cuda, qctx, monkeypatch, case):
+    """Q8_0 down weights in candle mode: the Q8_0 rounding of the SwiGLU hidden
+    state (the down projection's input, one scale per 32 columns of a token row)
+    done by the gate_up kernel's epilogue against the same rounding as the
+    rows-quantizer pass (QIMM_SEPARATE_ROUNDING=1): bit-identical block outputs.
+    Cases: config 1 (MLP 9216 at 256 tokens over 64: the undivided 128x128
+    kernel, four lanes per block), hidden 1024 / MLP 4096 at 1100 tokens (the
+    256x256 kernel, two waves per block, a last token tile of 76 rows), and the
+    same block at 256 tokens (two K shares: the f32 state and the rows quantizer
+    on both sides)."""
+    if case == "config1_128x128":
+        cfg, b, s, p = dict(hidden=3072, heads=24, head_dim=128, mlp=9216), 1, 256, 64
+    else:
+        cfg, b, s, p = dict(hidden=1024, heads=8, head_dim=128, mlp=4096), 1, 1100 if case == "wide_ragged" else 256, 64
+    print(f"case: {case}, hidden {cfg['hidden']}, MLP {cfg['mlp']}, {s} tokens", flush=True)
+    w, x, mod, pe, kpre, vpre = make_case(43, cfg, b, s, p, synth.Q8_0, synth.Q8_0)
+    fused, _ = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
+    monkeypatch.setenv("QIMM_SEPARATE_ROUNDING", "1")
+    separate, _ = run_block(torch_cuda, qctx, cfg, w, x, mod, pe, kpre, vpre)
+    assert np.isfinite(fused).all()
+    diff = np.count_nonzero(fused.view(np.uint32) != separate.view(np.uint32))
+    print(f"{case}: outputs differing in any bit: {diff} of {fused.size}", flush=True)
+    assert diff == 0
+
+
 @pytest.mark.parametrize("case", ["config1_fast_4wave", "ragged_any_length"])
 def test_attention_q8_0_rounding_in_epilogue_bit_identical(torch_cuda, qctx, monkeypatch, case):
     """Q8_0 weights in candle mode: the attention output's Q8_0 rounding (to_out's

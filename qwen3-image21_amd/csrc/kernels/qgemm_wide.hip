@@ -664,6 +664,23 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
             const int64_t head = (nb % ep.hidden) / 128;
             const uint32_t Su = (uint32_t)ep.seq;
             const int64_t H = ep.heads, S = ep.seq;
+            // (batch, position) of token m0 + t: with sequences of at least 256
+            // tokens the tile's 256 consecutive tokens span at most two, so one
+            // division for the tile's first token and a compare per row; shorter
+            // sequences divide per row. (Rows past M get a position below S.)
+            const uint32_t b0 = (uint32_t)m0 / Su, s0 = (uint32_t)m0 % Su;
+            auto tok = [&](int t, uint32_t &b, uint32_t &s) __attribute__((always_inline)) {
+                if (Su >= 256) {
+                    const uint32_t x = s0 + (uint32_t)t;
+                    const bool w = x >= Su;
+                    s = w ? x - Su : x;
+                    b = b0 + (w ? 1u : 0u);
+                } else {
+                    const uint32_t m = (uint32_t)min(m0 + t, M - 1);
+                    s = m % Su;
+                    b = m / Su;
+                }
+            };
             if (sec < 2) {
                 // RmsNorm over the head: each lane's 16 squares, the partner half
                 // (lane ^ 32), then the head's four waves through LDS. The RoPE
@@ -673,8 +690,9 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
                 const int dbase = 32 * sub + 4 * g;  // + 8 j
                 f32x4 cs[2][4];
                 auto load_pe = [&](int i) __attribute__((always_inline)) {
-                    const uint32_t m = (uint32_t)min(m0 + 32 * i + l32, M - 1);
-                    const float *pr = ep.pe + (int64_t)(m % Su) * 128;  // (cos, sin) of pair i at 2i, 2i + 1
+                    uint32_t b, s;
+                    tok(32 * i + l32, b, s);
+                    const float *pr = ep.pe + (int64_t)s * 128;  // (cos, sin) of pair i at 2i, 2i + 1
 #pragma unroll
                     for (int j = 0; j < 4; j++) cs[i & 1][j] = *(const f32x4 *)(pr + dbase + 8 * j);
                 };
@@ -729,9 +747,9 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
 #pragma unroll
                 for (int k = 0; k < 16; k++) {
                     const int ch = tid + 512 * k, hg = ch >> 12, t = (ch >> 4) & 255, c = ch & 15;
-                    const int64_t m = m0 + t;
-                    if (m >= M) continue;
-                    const uint32_t s = (uint32_t)m % Su, b = (uint32_t)m / Su;
+                    if (m0 + t >= M) continue;
+                    uint32_t b, s;
+                    tok(t, b, s);
                     *(u32x4 *)(dst + (((int64_t)b * H + head0 + hg) * S + s) * 128 + 8 * c) =
                         *(const u32x4 *)((uint16_t *)lds + hg * (256 * 128) + t * 128 + 8 * (c ^ (t & 15)));
                 }
@@ -741,9 +759,9 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
                 const int dbase = 32 * sub + 4 * g;
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
-                    const int64_t m = m0 + 32 * i + l32;
-                    if (m >= M) continue;
-                    const uint32_t s = (uint32_t)m % Su, b = (uint32_t)m / Su;
+                    if (m0 + 32 * i + l32 >= M) continue;
+                    uint32_t b, s;
+                    tok(32 * i + l32, b, s);
                     uint16_t *vrow = ep.vt + ((int64_t)b * H + head) * 128 * S + s;
 #pragma unroll
                     for (int r = 0; r < 16; r++) {

@@ -118,8 +118,9 @@ def check(got, ref, x, exact=False):
 @pytest.mark.parametrize("b,s,p", [(1, 16, 8), (2, 24, 16),  # M <= 64: split-K weight-streaming GEMM
                                    (1, 96, 40), (2, 64, 64), (1, 130, 0),
                                    # M >= 512 takes the 256x256 GEMM: partial tiles, a batch
-                                   # boundary inside a tile, and S % 4 != 0
-                                   (1, 520, 24), (2, 300, 16), (1, 514, 0)])
+                                   # boundary inside a tile, S % 4 != 0, and sequences shorter
+                                   # than a tile (three in one tile)
+                                   (1, 520, 24), (2, 300, 16), (1, 514, 0), (3, 200, 8)])
 def test_block_matches_oracle(torch_cuda, qctx, attn_type, down_type, b, s, p):
     w, x, mod, pe, kpre, vpre = make_case(b * 1000 + s + p, SMALL, b, s, p, attn_type, down_type)
     runs = run_modes(torch_cuda, qctx, SMALL, w, x, mod, pe, kpre, vpre, want_kv=True)

@@ -133,6 +133,17 @@ __device__ __forceinline__ float round_half_away(float x) {
     return __builtin_truncf(x + __builtin_copysignf(0.49999997f, x));
 }
 
+// round_half_away(v * s) with the product rounded to f32 first, as candle
+// computes iscale * x. Contraction is off here: HIP device code contracts by
+// default, and v * s fused into the add above rounds once, which differs
+// where v s lies within half an f32 ulp of k + 1/2 (2.4999999 rounds to the
+// float 2.5 and then to 3, but 2.4999999 + 0.49999997 rounds to 2.9999998).
+__device__ __forceinline__ float round_half_away_product(float v, float s) {
+#pragma clang fp contract(off)
+    const float x = v * s;
+    return __builtin_truncf(x + __builtin_copysignf(0.49999997f, x));
+}
+
 // The activation rounding of candle's CPU QMatMul (candle-core 0.11
 // quantized/k_quants.rs, the vec-dot type of the weight): each lane holds four
 // consecutive values of a row, consecutive lanes continue the row.
@@ -176,7 +187,7 @@ __device__ __forceinline__ void q8k_scales(float a, float xmax, float &s, float 
     d = a == 0.f ? 0.f : 1.f / s;
 }
 __device__ __forceinline__ float q8k_value(float v, float s, float d) {
-    return product_for_bf16(d, fminf(round_half_away(v * s), 127.f));
+    return product_for_bf16(d, fminf(round_half_away_product(v, s), 127.f));
 }
 // Q8_0 block rounding from the block's largest magnitude a: q = round(v s) with
 // s = 1 / (a / 127) (0 for an all-zero block), the value d q with d = a / 127
@@ -186,7 +197,9 @@ __device__ __forceinline__ void q8_0_scales(float a, float &s, float &d) {
     s = d32 != 0.f ? 1.f / d32 : 0.f;
     d = (float)(_Float16)d32;
 }
-__device__ __forceinline__ float q8_0_value(float v, float s, float d) { return product_for_bf16(d, round_half_away(v * s)); }
+__device__ __forceinline__ float q8_0_value(float v, float s, float d) {
+    return product_for_bf16(d, round_half_away_product(v, s));
+}
 
 template <int QBLK>
 __device__ __forceinline__ u32x2 quant_act4(f32x4 v) {
@@ -207,7 +220,7 @@ __device__ __forceinline__ u32x2 quant_act4(f32x4 v) {
     float p[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        float q = round_half_away(v[i] * s);
+        float q = round_half_away_product(v[i], s);
         if constexpr (QBLK == 256) q = fminf(q, 127.f);
         p[i] = product_for_bf16(d, q);
     }

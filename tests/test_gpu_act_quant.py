@@ -16,6 +16,7 @@ import pytest
 import oracle as O
 import synth
 from gpu_util import cos_sim, dev, host, max_abs_rel, stream
+from test_oracle_act_quant import near_half_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -46,6 +47,19 @@ def _quant_gpu(torch, qctx, wt, x, ldx=None):
                                     (synth.Q8_0, 2, 16384)])
 def test_quantize_act_bit_exact(torch_cuda, qctx, wt, m, k):
     x = _rows(m * 7 + k, m, k)
+    got = _quant_gpu(torch_cuda, qctx, wt, x)
+    want = O.quant_act_bf16(wt, x)
+    assert np.array_equal(got, want), np.count_nonzero(got != want)
+
+
+@pytest.mark.parametrize("wt", [synth.Q4_K, synth.Q8_0])
+def test_quantize_act_products_near_a_half_bit_exact(torch_cuda, qctx, wt):
+    """Blocks whose products v * s round to exactly a half in float32 without
+    being one (near_half_rows: ~100 values per 64 Q8_K blocks where a fused
+    v * s + c, the contraction HIP device code allows by default, truncates to
+    another code): the kernels round the float32 product first, as candle does,
+    bit-identical to the oracle."""
+    x = near_half_rows(wt, 11, 64).reshape(-1, 1024)
     got = _quant_gpu(torch_cuda, qctx, wt, x)
     want = O.quant_act_bf16(wt, x)
     assert np.array_equal(got, want), np.count_nonzero(got != want)

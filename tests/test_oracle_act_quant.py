@@ -66,6 +66,86 @@ def numpy_q8_0(x):
     return out.reshape(-1)
 
 
+def _near_half(s, kmax, vmax):
+    """float32 values v (|v| < vmax) whose product with the float32 scale s
+    rounds to exactly k + 1/2 (|k| < kmax) in float32 while the exact product
+    is not k + 1/2: where rounding the product first (candle) and a fused
+    v * s + c (a contracted multiply-add) may truncate to different codes."""
+    s = np.float32(s)
+    t = np.concatenate([np.arange(kmax) + 0.5, -(np.arange(kmax) + 0.5)])
+    bits = (t / np.float64(s)).astype(np.float32).view(np.int32)
+    cand = np.concatenate([(bits + o).view(np.float32) for o in range(-4, 5)])
+    tt = np.tile(t, 9)
+    p64 = cand.astype(np.float64) * np.float64(s)  # exact: 24 x 24 bits
+    ok = (p64.astype(np.float32) == tt.astype(np.float32)) & (p64 != tt) & (np.abs(cand) < vmax)
+    return np.unique(cand[ok])
+
+
+def near_half_rows(wtype, seed, nblocks):
+    """Rows of activation blocks for the weight type's rounding (Q8_K: 256
+    values, Q8_0: 32), each block's largest magnitude first, the rest values
+    whose products with the block's scale lie within half an float32 ulp of a
+    half (_near_half), padded with zeros: the inputs on which an FMA
+    contraction of the kernels' rounding would differ from candle's."""
+    rng = np.random.default_rng(seed)
+    qk = 256 if wtype in (O.Q4_K, O.Q6_K) else 32
+    blocks = []
+    while len(blocks) < nblocks:
+        big = np.float32(rng.uniform(0.3, 5.0) * (1 if rng.integers(2) else -1))
+        if qk == 256:
+            s = np.float32(-128.0) / big
+            v = _near_half(s, 127, abs(big))
+        else:
+            d = np.float32(abs(big)) / np.float32(127.0)
+            v = _near_half(np.float32(1.0) / d, 127, abs(big))
+        if len(v) == 0:
+            continue
+        b = np.zeros(qk, np.float32)
+        b[0] = big
+        v = rng.permutation(v)[:qk - 1]
+        b[1:1 + len(v)] = v
+        blocks.append(b)
+    return np.concatenate(blocks)
+
+
+def _f32_nearest(q):
+    """The float32 nearest to the rational q, ties to even (one rounding)."""
+    from fractions import Fraction
+    f = np.float32(float(q))
+    best = None
+    for c in (np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))):
+        e = abs(Fraction(float(c)) - q)
+        if best is None or e < best[0] or (e == best[0] and (int(c.view(np.uint32)) & 1) == 0):
+            best = (e, c)
+    return best[1]
+
+
+def test_rounding_of_products_near_a_half():
+    """On rows built from products that round to a half in float32 but are not
+    one (near_half_rows), the oracle's activation rounding equals the numpy
+    restatement (the product rounded to float32, then rounded half away from
+    zero), and the rows hold such values: for each, the exact product plus the
+    kernels' 0.49999997, rounded once (a fused multiply-add), truncates to a
+    different code than the twice-rounded form in at least some cases."""
+    from fractions import Fraction
+    for wt, qk, restated in ((O.Q4_K, 256, numpy_q8_k), (O.Q8_0, 32, numpy_q8_0)):
+        x = near_half_rows(wt, 5, 24)
+        assert np.array_equal(O.quant_act_bf16(wt, x.reshape(-1, qk)).reshape(-1), restated(x))
+        differs = 0
+        for b in x.reshape(-1, qk):
+            if qk == 256:
+                s = np.float32(-128.0) / b[0]
+            else:
+                s = np.float32(1.0) / (np.float32(abs(b[0])) / np.float32(127.0))
+            for v in b[1:][b[1:] != 0]:
+                p32 = np.float32(v * s)
+                c = np.float32(np.copysign(np.float32(0.49999997), p32))
+                twice = np.trunc(np.float32(p32 + c))
+                once = np.trunc(_f32_nearest(Fraction(float(v)) * Fraction(float(s)) + Fraction(float(c))))
+                differs += int(once != twice)
+        assert differs > 0, wt
+
+
 def _rows(seed, m, k):
     rng = np.random.default_rng(seed)
     x = (rng.standard_normal((m, k)) * np.exp(rng.standard_normal((m, 1)))).astype(np.float32)

@@ -176,12 +176,15 @@ __device__ __forceinline__ void stage_out_bf16(uint16_t *os, const f32x16 (&o)[4
             float sc, dq;
             q8_0_scales(xmax32(a), sc, dq);
 #pragma unroll
-            for (int r = 0; r < 16; r++) v[r] = q8_0_value(v[r], sc, dq);
-        }
+            for (int rq = 0; rq < 4; rq++)
+                *(u32x2 *)(os + l32 * PITCH + dt * 32 + 8 * rq + 4 * g) =
+                    q8_0_values4(f32x4{v[4 * rq], v[4 * rq + 1], v[4 * rq + 2], v[4 * rq + 3]}, sc, dq);
+        } else {
 #pragma unroll
-        for (int rq = 0; rq < 4; rq++)
-            *(u32x2 *)(os + l32 * PITCH + dt * 32 + 8 * rq + 4 * g) =
-                u32x2{pack_bf16x2(v[4 * rq], v[4 * rq + 1]), pack_bf16x2(v[4 * rq + 2], v[4 * rq + 3])};
+            for (int rq = 0; rq < 4; rq++)
+                *(u32x2 *)(os + l32 * PITCH + dt * 32 + 8 * rq + 4 * g) =
+                    u32x2{pack_bf16x2(v[4 * rq], v[4 * rq + 1]), pack_bf16x2(v[4 * rq + 2], v[4 * rq + 3])};
+        }
     }
 }
 
@@ -751,12 +754,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fast_kernel(const uint16
                     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
                         for (int rq = 0; rq < 4; rq++) {
-                            float x[4];
+                            f32x4 x;
 #pragma unroll
-                            for (int e = 0; e < 4; e++)
-                                x[e] = q8k_value(hd == 0 ? va[dt][4 * rq + e] : o[dt][4 * rq + e] * inv, sc, dq);
-                            *(u32x2 *)(os + l32 * OP + dt * 32 + 8 * rq + 4 * g) =
-                                u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+                            for (int e = 0; e < 4; e++) x[e] = hd == 0 ? va[dt][4 * rq + e] : o[dt][4 * rq + e] * inv;
+                            *(u32x2 *)(os + l32 * OP + dt * 32 + 8 * rq + 4 * g) = q8k_values4(x, sc, dq);
                         }
                     __syncthreads();
                     store_rows((hh - 1 + hd) * HD);

@@ -201,6 +201,38 @@ __device__ __forceinline__ float q8_0_value(float v, float s, float d) {
     return product_for_bf16(d, round_half_away_product(v, s));
 }
 
+// Four bf16 operands bf16(d * q_e), packed, each as product_for_bf16 gives it:
+// the products rounded once to f32, the rare halfway test made once for the
+// four (one branch instead of four), and the exact form taken for all four
+// when any of them sits on a bf16 halfway point.
+__device__ __forceinline__ u32x2 products4_bf16(float d, f32x4 q) {
+    float p[4];
+    bool half = false;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        p[e] = __builtin_fmaf(d, q[e], 0.f);
+        half |= (__float_as_uint(p[e]) & 0xffffu) == 0x8000u;
+    }
+    if (__builtin_expect(half, 0)) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) p[e] = product_for_bf16(d, q[e]);
+    }
+    return u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
+}
+// four values' Q8_K / Q8_0 operands (q8k_value / q8_0_value), packed bf16
+__device__ __forceinline__ u32x2 q8k_values4(f32x4 v, float s, float d) {
+    f32x4 q;
+#pragma unroll
+    for (int e = 0; e < 4; e++) q[e] = fminf(round_half_away_product(v[e], s), 127.f);
+    return products4_bf16(d, q);
+}
+__device__ __forceinline__ u32x2 q8_0_values4(f32x4 v, float s, float d) {
+    f32x4 q;
+#pragma unroll
+    for (int e = 0; e < 4; e++) q[e] = round_half_away_product(v[e], s);
+    return products4_bf16(d, q);
+}
+
 template <int QBLK>
 __device__ __forceinline__ u32x2 quant_act4(f32x4 v) {
     static_assert(QBLK == 32 || QBLK == 256, "Q8_0 or Q8_K blocks");
@@ -217,14 +249,7 @@ __device__ __forceinline__ u32x2 quant_act4(f32x4 v) {
     } else {
         q8_0_scales(max8_lanes(a), s, d);
     }
-    float p[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float q = round_half_away_product(v[i], s);
-        if constexpr (QBLK == 256) q = fminf(q, 127.f);
-        p[i] = product_for_bf16(d, q);
-    }
-    return u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
+    return QBLK == 256 ? q8k_values4(v, s, d) : q8_0_values4(v, s, d);
 }
 
 }  // namespace qimm

@@ -355,11 +355,9 @@ __global__ __launch_bounds__(256, 2) void qgemm_kernel(const uint16_t *__restric
                 a = fmaxf(a, __shfl_xor(a, 2));
                 float sc, dq;
                 q8_0_scales(a, sc, dq);
-                uint32_t pk[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    pk[i] = pack_bf16x2(q8_0_value(h[2 * i], sc, dq), q8_0_value(h[2 * i + 1], sc, dq));
-                *(u32x4 *)(ep.hmid + o) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+                const u32x2 lo = q8_0_values4(f32x4{h[0], h[1], h[2], h[3]}, sc, dq);
+                const u32x2 hi = q8_0_values4(f32x4{h[4], h[5], h[6], h[7]}, sc, dq);
+                *(u32x4 *)(ep.hmid + o) = u32x4{lo[0], lo[1], hi[0], hi[1]};
             } else if (ep.hmid_f32) {
                 *(f32x4 *)(ep.hmid_f32 + o) = f32x4{h[0], h[1], h[2], h[3]};
                 *(f32x4 *)(ep.hmid_f32 + o + 4) = f32x4{h[4], h[5], h[6], h[7]};

@@ -514,11 +514,10 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
                     q8_0_scales(fmaxf(red[wave * BM + tk], red[(wave ^ 1) * BM + tk]), sc, dq);
 #pragma unroll
                     for (int j = 0; j < 2; j++) {
-                        float q[4];
+                        f32x4 hv;
 #pragma unroll
-                        for (int e = 0; e < 4; e++) q[e] = q8_0_value(hval(i, 4 * j + e), sc, dq);
-                        *(u32x2 *)(ep.hmid + m * ep.ldh + hc + 8 * j) =
-                            u32x2{pack_bf16x2(q[0], q[1]), pack_bf16x2(q[2], q[3])};
+                        for (int e = 0; e < 4; e++) hv[e] = hval(i, 4 * j + e);
+                        *(u32x2 *)(ep.hmid + m * ep.ldh + hc + 8 * j) = q8_0_values4(hv, sc, dq);
                     }
                 }
             } else {
@@ -648,10 +647,8 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
                     for (int j = 0; j < 2; j++) {
                         const float *v = &h[i][4 * j];
                         const f32x4 u = ha[i][j];
-                        *(u32x2 *)(hrow + 8 * j) = u32x2{pack_bf16x2(q8k_value(v[0], sc, dq), q8k_value(v[1], sc, dq)),
-                                                         pack_bf16x2(q8k_value(v[2], sc, dq), q8k_value(v[3], sc, dq))};
-                        *(u32x2 *)(hrow - 128 + 8 * j) = u32x2{pack_bf16x2(q8k_value(u[0], sc, dq), q8k_value(u[1], sc, dq)),
-                                                               pack_bf16x2(q8k_value(u[2], sc, dq), q8k_value(u[3], sc, dq))};
+                        *(u32x2 *)(hrow + 8 * j) = q8k_values4(f32x4{v[0], v[1], v[2], v[3]}, sc, dq);
+                        *(u32x2 *)(hrow - 128 + 8 * j) = q8k_values4(u, sc, dq);
                     }
                 }
             }

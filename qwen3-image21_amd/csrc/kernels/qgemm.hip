@@ -533,8 +533,8 @@ namespace {
 // kernel runs whole waves: when the 256x256 tiles leave a last, partial wave
 // of at most a quarter of the CUs made of whole 256-row tile rows (4352 tokens
 // x N = 4096: 272 tiles for 256 CUs), those rows go to the split-K 128x128
-// kernel (or the short-M path) instead. Plain outputs only (their rows are
-// independent of the token index); 0 = none.
+// kernel (or the short-M path) instead (tail_rows below names the epilogues
+// whose rows can be shifted); 0 = none.
 int64_t large_tail_rows(const GemmWeight &w, int64_t m) {
     if (!qgemm_large_fits(w, m)) return 0;
     const int64_t mt = (m + 255) / 256, nt = w.n / 256, tiles = mt * nt, cus = device_cus();
@@ -593,9 +593,51 @@ size_t qgemm_workspace(const GemmWeight &w, int64_t m) {
     return small_workspace(w, m);
 }
 
+namespace {
+
+// The large-M tail (large_tail_rows) of a product whose epilogue's rows can be
+// shifted: plain outputs, SwiGLU, and the gated residual when the tail's rows
+// share one gate row; 0 = none (the q/k/v epilogue maps rows to whole
+// sequences, and its split reduction takes whole sequences only).
+int64_t tail_rows(const GemmWeight &w, int64_t m, int epi, const EpiParams &ep) {
+    const int64_t tail = large_tail_rows(w, m);
+    if (!tail || !ep.part_ws || ep.part_ws_bytes < small_workspace(w, tail)) return 0;
+    if (epi == EPI_F32 || epi == EPI_BF16 || epi == EPI_SWIGLU) return tail;
+    if (epi == EPI_RESID && ep.g_rows_per > 0 && (m - tail) / ep.g_rows_per == (m - 1) / ep.g_rows_per)
+        return tail;
+    return 0;
+}
+
+// The epilogue of rows head .. of a product as that of a product of its own
+EpiParams rows_from(const EpiParams &ep, int epi, const GemmWeight &w, int64_t head) {
+    EpiParams e = ep;
+    if (epi == EPI_F32 || epi == EPI_BF16) {
+        e.out = (char *)ep.out + (size_t)head * (size_t)ep.ldo * (epi == EPI_F32 ? 4 : 2);
+    } else if (epi == EPI_RESID) {
+        e.x_in = ep.x_in + head * w.n;
+        e.x_out = ep.x_out + head * w.n;
+        e.gvec = ep.gvec + (head / ep.g_rows_per) * ep.g_stride;
+    } else if (epi == EPI_SWIGLU) {
+        e.hmid = ep.hmid + head * ep.ldh;
+        if (ep.hmid_f32) e.hmid_f32 = ep.hmid_f32 + head * ep.ldh;
+    }
+    return e;
+}
+
+}  // namespace
+
 hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64_t lda, int epi,
                         const EpiParams &ep, hipStream_t stream) {
     if (m <= 0) return hipSuccess;
+    // a last, nearly empty round of 256x256 tiles: those rows as a shorter-M
+    // product of their own (whole rounds above, the 128x128 or short-M path
+    // for the tail), each part with its own form of the epilogue
+    if (const int64_t tail = tail_rows(w, m, epi, ep)) {
+        const int64_t head = m - tail;
+        const hipError_t e = launch_qgemm(w, a, head, lda, epi, ep, stream);
+        if (e != hipSuccess) return e;
+        return launch_qgemm(w, a + head * lda, tail, lda, epi, rows_from(ep, epi, w, head), stream);
+    }
     if (epi == EPI_SWIGLU && ep.hmid_q8k) {
         // the Q8_K rounding of the hidden state: inside the paired large-M
         // kernel where it runs, else the f32 state and then the rows quantizer
@@ -621,18 +663,7 @@ hipError_t launch_qgemm(const GemmWeight &w, const uint16_t *a, int64_t m, int64
         if (err != hipSuccess) return err;
         return launch_quant_rows(ep.hmid_f32, ep.ldh, m, w.n / 2, 32, ep.hmid, ep.ldh, stream);
     }
-    if (qgemm_large_fits(w, m)) {
-        const int64_t tail = (epi == EPI_F32 || epi == EPI_BF16) ? large_tail_rows(w, m) : 0;
-        if (tail && ep.part_ws && ep.part_ws_bytes >= small_workspace(w, tail)) {
-            const int64_t head = m - tail;
-            const hipError_t e = launch_qgemm_large(w, a, head, lda, epi, ep, stream);
-            if (e != hipSuccess) return e;
-            EpiParams et = ep;
-            et.out = (char *)ep.out + (size_t)head * (size_t)ep.ldo * (epi == EPI_F32 ? 4 : 2);
-            return launch_small(w, a + head * lda, tail, lda, epi, et, stream);
-        }
-        return launch_qgemm_large(w, a, m, lda, epi, ep, stream);
-    }
+    if (qgemm_large_fits(w, m)) return launch_qgemm_large(w, a, m, lda, epi, ep, stream);
     return launch_small(w, a, m, lda, epi, ep, stream);
 }
 

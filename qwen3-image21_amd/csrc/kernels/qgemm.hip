@@ -596,14 +596,19 @@ size_t qgemm_workspace(const GemmWeight &w, int64_t m) {
 namespace {
 
 // The large-M tail (large_tail_rows) of a product whose epilogue's rows can be
-// shifted: plain outputs, SwiGLU, and the gated residual when the tail's rows
-// share one gate row; 0 = none (the q/k/v epilogue maps rows to whole
-// sequences, and its split reduction takes whole sequences only).
+// shifted: plain outputs, SwiGLU, the gated residual when the tail's rows
+// share one gate row, and q/k/v when they lie in one sequence and take the
+// undivided 128x128 kernel (its epilogue then sees positions 0 .. of outputs
+// shifted to the tail's first position; the split q/k/v reduction takes whole
+// sequences only); 0 = none.
 int64_t tail_rows(const GemmWeight &w, int64_t m, int epi, const EpiParams &ep) {
     const int64_t tail = large_tail_rows(w, m);
     if (!tail || !ep.part_ws || ep.part_ws_bytes < small_workspace(w, tail)) return 0;
     if (epi == EPI_F32 || epi == EPI_BF16 || epi == EPI_SWIGLU) return tail;
     if (epi == EPI_RESID && ep.g_rows_per > 0 && (m - tail) / ep.g_rows_per == (m - 1) / ep.g_rows_per)
+        return tail;
+    if (epi == EPI_QKV && ep.seq > 0 && (m - tail) / ep.seq == (m - 1) / ep.seq &&
+        small_path(w, tail, ep) == SmallPath::WHOLE)
         return tail;
     return 0;
 }
@@ -620,6 +625,15 @@ EpiParams rows_from(const EpiParams &ep, int epi, const GemmWeight &w, int64_t h
     } else if (epi == EPI_SWIGLU) {
         e.hmid = ep.hmid + head * ep.ldh;
         if (ep.hmid_f32) e.hmid_f32 = ep.hmid_f32 + head * ep.ldh;
+    } else if (epi == EPI_QKV) {
+        // sequence b0 from position s0: with positions 0 .. (m < seq - s0) the
+        // epilogue's rows ((b H + h) S + s) land at ((b0 H + h) S + s0 + m)
+        const int64_t S = ep.seq, H = ep.heads, b0 = head / S, s0 = head % S;
+        if (ep.q) e.q = ep.q + (b0 * H * S + s0) * 128;
+        if (ep.k) e.k = ep.k + (b0 * H * S + s0) * 128;
+        if (ep.vt) e.vt = ep.vt + b0 * H * 128 * S + s0;
+        if (ep.v_bhsd) e.v_bhsd = ep.v_bhsd + (b0 * H * S + s0) * 128;
+        if (ep.pe) e.pe = ep.pe + s0 * 128;
     }
     return e;
 }

@@ -77,25 +77,33 @@ def test_block_1024_q4km_full_size(torch_cuda, qctx):
     kv_close(vb, vre)
 
 
-@pytest.mark.parametrize("attn_type,down_type", [(synth.Q8_0, synth.Q8_0), (synth.Q4_K, synth.Q6_K)])
-def test_block_4352_tokens_tail_rows(torch_cuda, qctx, attn_type, down_type):
-    """4352 tokens at hidden 4096 (17 rows of 256x256 tiles): out and down make
-    272 tiles for 256 CUs, so their last 256 token rows run as a 256-token
-    product of their own (the 128x128 or split path, the gated residual on
-    rows shifted by 4096 tokens), the rest as whole rounds. Sampled rows, the
-    seam at 4096 and 48 of the last 256 rows against the candle-mode oracle."""
-    b, s, p = 1, 4352, 64
-    print(f"case: block hidden 4096, {s} tokens over {p}, types {attn_type}/{down_type}", flush=True)
+@pytest.mark.parametrize("attn_type,down_type,b,s", [(synth.Q8_0, synth.Q8_0, 1, 4352),
+                                                     (synth.Q4_K, synth.Q6_K, 1, 4352),
+                                                     (synth.Q8_0, synth.Q8_0, 2, 2176)])
+def test_block_4352_tokens_tail_rows(torch_cuda, qctx, attn_type, down_type, b, s):
+    """4352 token rows at hidden 4096 (17 rows of 256x256 tiles): q/k/v makes
+    816 tiles and out and down 272 for 256 CUs, so their last 256 token rows
+    run as a 256-token product of their own (the 128x128 or split path; the
+    gated residual on rows shifted by 4096, the q/k/v outputs, V^T and RoPE rows
+    shifted to the tail's sequence and position: sequence 0 from position 4096,
+    or with two sequences of 2176 tokens sequence 1 from position 1920), the
+    rest as whole rounds. Sampled rows, the seam at 4096 and 48 of the last 256
+    rows, and every token's K and V, against the candle-mode oracle."""
+    p = 64
+    m = b * s
+    print(f"case: block hidden 4096, {b} x {s} tokens over {p}, types {attn_type}/{down_type}", flush=True)
     w, x, mod, pe, kpre, vpre = make_case(6, CFG4, b, s, p, attn_type, down_type)
-    got, _ = run_block(torch_cuda, qctx, CFG4, w, x, mod, pe, kpre, vpre)
+    got, (k, v) = run_block(torch_cuda, qctx, CFG4, w, x, mod, pe, kpre, vpre, want_kv=True)
     assert np.isfinite(got).all()
     rng = np.random.default_rng(41)
-    rows = np.unique(np.concatenate([sampled_rows(rng, s), rng.choice(np.arange(4096, s), 48, replace=False)]))
-    ref, _, _ = O.block_forward_rows(CFG4, w, x, mod, pe, rows, kpre, vpre, mode=O.CANDLE)
-    g = got.reshape(s, -1)[rows]
-    c, m = cos_sim(g, ref), max_abs_rel(g, ref)
-    print(f"sampled rows: cos {c:.7f} mar {m:.2e}", flush=True)
-    assert c >= 0.9999 and m <= 2e-2
+    rows = np.unique(np.concatenate([sampled_rows(rng, m), rng.choice(np.arange(4096, m), 48, replace=False)]))
+    ref, kr, vr = O.block_forward_rows(CFG4, w, x, mod, pe, rows, kpre, vpre, mode=O.CANDLE)
+    g = got.reshape(m, -1)[rows]
+    c, mr = cos_sim(g, ref), max_abs_rel(g, ref)
+    print(f"sampled rows: cos {c:.7f} mar {mr:.2e}", flush=True)
+    assert c >= 0.9999 and mr <= 2e-2
+    kv_close(k, kr)
+    kv_close(v, vr)
 
 
 def _q4k_negated(rows):

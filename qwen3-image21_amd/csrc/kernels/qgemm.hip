@@ -534,10 +534,11 @@ namespace {
 // of at most a quarter of the CUs made of whole 256-row tile rows (4352 tokens
 // x N = 4096: 272 tiles for 256 CUs), those rows go to the split-K 128x128
 // kernel (or the short-M path) instead (tail_rows below names the epilogues
-// whose rows can be shifted); 0 = none.
-int64_t large_tail_rows(const GemmWeight &w, int64_t m) {
+// whose rows can be shifted); 0 = none. `pairs`: the paired SwiGLU form, whose
+// workgroups take two tiles each (its rounds are counted in pairs).
+int64_t large_tail_rows(const GemmWeight &w, int64_t m, bool pairs = false) {
     if (!qgemm_large_fits(w, m)) return 0;
-    const int64_t mt = (m + 255) / 256, nt = w.n / 256, tiles = mt * nt, cus = device_cus();
+    const int64_t mt = (m + 255) / 256, nt = w.n / 256 / (pairs ? 2 : 1), tiles = mt * nt, cus = device_cus();
     const int64_t r = cus > 0 ? tiles % cus : 0;
     if (tiles <= cus || r == 0 || r > cus / 4 || r % nt) return 0;
     const int64_t tail = m - (mt - r / nt) * 256;
@@ -587,8 +588,10 @@ hipError_t launch_small(const GemmWeight &w, const uint16_t *a, int64_t m, int64
 
 size_t qgemm_workspace(const GemmWeight &w, int64_t m) {
     if (qgemm_large_fits(w, m)) {
-        const int64_t tail = large_tail_rows(w, m);
-        return tail ? small_workspace(w, tail) : 0;
+        size_t need = 0;
+        for (bool pairs : {false, true})
+            if (const int64_t tail = large_tail_rows(w, m, pairs)) need = std::max(need, small_workspace(w, tail));
+        return need;
     }
     return small_workspace(w, m);
 }
@@ -602,7 +605,7 @@ namespace {
 // shifted to the tail's first position; the split q/k/v reduction takes whole
 // sequences only); 0 = none.
 int64_t tail_rows(const GemmWeight &w, int64_t m, int epi, const EpiParams &ep) {
-    const int64_t tail = large_tail_rows(w, m);
+    const int64_t tail = large_tail_rows(w, m, epi == EPI_SWIGLU && ep.hmid_q8k && qgemm_wide_pairs_fit(w));
     if (!tail || !ep.part_ws || ep.part_ws_bytes < small_workspace(w, tail)) return 0;
     if (epi == EPI_F32 || epi == EPI_BF16 || epi == EPI_SWIGLU) return tail;
     if (epi == EPI_RESID && ep.g_rows_per > 0 && (m - tail) / ep.g_rows_per == (m - 1) / ep.g_rows_per)

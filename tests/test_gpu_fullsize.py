@@ -79,7 +79,8 @@ def test_block_1024_q4km_full_size(torch_cuda, qctx):
 
 @pytest.mark.parametrize("attn_type,down_type,b,s", [(synth.Q8_0, synth.Q8_0, 1, 4352),
                                                      (synth.Q4_K, synth.Q6_K, 1, 4352),
-                                                     (synth.Q8_0, synth.Q8_0, 2, 2176)])
+                                                     (synth.Q8_0, synth.Q8_0, 2, 2176),
+                                                     (synth.Q4_K, synth.Q6_K, 1, 4160)])
 def test_block_4352_tokens_tail_rows(torch_cuda, qctx, attn_type, down_type, b, s):
     """4352 token rows at hidden 4096 (17 rows of 256x256 tiles): q/k/v makes
     816 tiles and out and down 272 for 256 CUs, so their last 256 token rows
@@ -87,8 +88,10 @@ def test_block_4352_tokens_tail_rows(torch_cuda, qctx, attn_type, down_type, b, 
     gated residual on rows shifted by 4096, the q/k/v outputs, V^T and RoPE rows
     shifted to the tail's sequence and position: sequence 0 from position 4096,
     or with two sequences of 2176 tokens sequence 1 from position 1920), the
-    rest as whole rounds. Sampled rows, the seam at 4096 and 48 of the last 256
-    rows, and every token's K and V, against the candle-mode oracle."""
+    rest as whole rounds; with 4160 tokens the last 64 rows take the short-M
+    kernels (the gated residual and the f32 hidden state with its rows pass;
+    q/k/v keeps them). Sampled rows, the seam at 4096 and 48 of the last rows,
+    and every token's K and V, against the candle-mode oracle."""
     p = 64
     m = b * s
     print(f"case: block hidden 4096, {b} x {s} tokens over {p}, types {attn_type}/{down_type}", flush=True)

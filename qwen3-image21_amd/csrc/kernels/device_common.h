@@ -180,25 +180,19 @@ __device__ __forceinline__ float max_wave(float a) {
 
 // Q8_K block rounding from the block's largest magnitude a and the signed value
 // xmax at its first occurrence: iscale s = -128 / xmax and d = 1 / s (both 0
-// for an all-zero block); one value's operand is bf16(d * min(127, round(v s))),
-// q8k_value giving the f32 to round to bf16.
+// for an all-zero block); one value's operand is bf16(d * min(127, round(v s)))
+// (q8k_values4).
 __device__ __forceinline__ void q8k_scales(float a, float xmax, float &s, float &d) {
     s = a == 0.f ? 0.f : -128.f / xmax;
     d = a == 0.f ? 0.f : 1.f / s;
 }
-__device__ __forceinline__ float q8k_value(float v, float s, float d) {
-    return product_for_bf16(d, fminf(round_half_away_product(v, s), 127.f));
-}
 // Q8_0 block rounding from the block's largest magnitude a: q = round(v s) with
 // s = 1 / (a / 127) (0 for an all-zero block), the value d q with d = a / 127
-// kept as f16; q8_0_value gives the f32 to round to bf16.
+// kept as f16 (q8_0_values4).
 __device__ __forceinline__ void q8_0_scales(float a, float &s, float &d) {
     const float d32 = a / 127.f;
     s = d32 != 0.f ? 1.f / d32 : 0.f;
     d = (float)(_Float16)d32;
-}
-__device__ __forceinline__ float q8_0_value(float v, float s, float d) {
-    return product_for_bf16(d, round_half_away_product(v, s));
 }
 
 // Four bf16 operands bf16(d * q_e), packed, each as product_for_bf16 gives it:
@@ -219,7 +213,8 @@ __device__ __forceinline__ u32x2 products4_bf16(float d, f32x4 q) {
     }
     return u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
 }
-// four values' Q8_K / Q8_0 operands (q8k_value / q8_0_value), packed bf16
+// four values' Q8_K operands bf16(d * min(127, round(v s))) / Q8_0 operands
+// bf16(d * round(v s)), packed
 __device__ __forceinline__ u32x2 q8k_values4(f32x4 v, float s, float d) {
     f32x4 q;
 #pragma unroll

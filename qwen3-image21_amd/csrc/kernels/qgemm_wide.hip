@@ -448,6 +448,45 @@ __global__ __launch_bounds__(64 * NW, 1) void qgemm_wide_kernel(const uint16_t *
         if constexpr (EPI == EPI_F32 || EPI == EPI_BF16 || EPI == EPI_RESID) {
             const int64_t nw = n0 + 32 * wave + 4 * g;  // + 8 j: the lane's run j of four rows
             const int64_t N = w.n;
+            // the gated residual of a tile whose rows share one gate row: the
+            // x_in loads of four token rows in flight before their stores
+            // (x_out may alias x_in: each element is read and written by the
+            // same lane, its load before its store)
+            bool resid_done = false;
+            if constexpr (EPI == EPI_RESID) {
+                const int64_t gp = ep.g_rows_per, last = (m0 + BM < M ? m0 + BM : M) - 1;
+                if (m0 / gp == last / gp) {
+                    const float *grow = ep.gvec + (m0 / gp) * ep.g_stride;
+                    f32x4 gv[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) gv[j] = *(const f32x4 *)(grow + nw + 8 * j);
+#pragma unroll
+                    for (int i0 = 0; i0 < 8; i0 += 4) {
+                        f32x4 xv[4][4];
+#pragma unroll
+                        for (int ii = 0; ii < 4; ii++) {
+                            const int64_t m = m0 + 32 * (i0 + ii) + l32;
+                            if (m < M)
+#pragma unroll
+                                for (int j = 0; j < 4; j++) xv[ii][j] = *(const f32x4 *)(ep.x_in + m * N + nw + 8 * j);
+                        }
+#pragma unroll
+                        for (int ii = 0; ii < 4; ii++) {
+                            const int64_t m = m0 + 32 * (i0 + ii) + l32;
+                            if (m >= M) continue;
+#pragma unroll
+                            for (int j = 0; j < 4; j++) {
+                                f32x4 o;
+#pragma unroll
+                                for (int e = 0; e < 4; e++) o[e] = xv[ii][j][e] + gv[j][e] * acc[i0 + ii][4 * j + e];
+                                *(f32x4 *)(ep.x_out + m * N + nw + 8 * j) = o;
+                            }
+                        }
+                    }
+                    resid_done = true;
+                }
+            }
+            if (!resid_done)
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const int64_t m = m0 + 32 * i + l32;

@@ -228,23 +228,92 @@ __device__ __forceinline__ u32x2 q8_0_values4(f32x4 v, float s, float d) {
     return products4_bf16(d, q);
 }
 
+// Magnitudes (non-negative floats) compared as their bit patterns, whose
+// unsigned order is theirs, so each DPP move folds into one integer max (and
+// the wave's four row maxima combine on the scalar unit): the largest over
+// each aligned group of 8 lanes, and over the wave. The same values as
+// max8_lanes / max_wave for inputs without NaN.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_umax(uint32_t a) {
+    return max(a, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a, CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float mag_max8_lanes(float a) {
+    uint32_t u = __float_as_uint(a);
+    u = dpp_umax<0xb1>(u);   // quad_perm [1,0,3,2]
+    u = dpp_umax<0x4e>(u);   // quad_perm [2,3,0,1]
+    u = dpp_umax<0x141>(u);  // row_half_mirror
+    return __uint_as_float(u);
+}
+__device__ __forceinline__ float mag_max_wave(float a) {
+    const uint32_t u = dpp_umax<0x140>(__float_as_uint(mag_max8_lanes(a)));  // row_mirror
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)u, 0);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)u, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)u, 32);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)u, 48);
+    return __uint_as_float(max(max(r0, r1), max(r2, r3)));
+}
+
+// quant_act4 over N chunks of four values at once (chunk i its own Q8_K block,
+// or its own eight Q8_0 blocks), each step taken for all chunks before the
+// next, without branches but the one rare halfway test for all N x 4 products,
+// so the chunks' reduction chains interleave.
+template <int QBLK, int N>
+__device__ __forceinline__ void quant_act4_n(const f32x4 (&v)[N], u32x2 (&out)[N]) {
+    static_assert(QBLK == 32 || QBLK == 256, "Q8_0 or Q8_K blocks");
+    float a[N], s[N], d[N];  // value = d * q, q from x * s
+#pragma unroll
+    for (int i = 0; i < N; i++)
+        a[i] = fmaxf(fmaxf(fabsf(v[i][0]), fabsf(v[i][1])), fmaxf(fabsf(v[i][2]), fabsf(v[i][3])));
+    if constexpr (QBLK == 256) {
+#pragma unroll
+        for (int i = 0; i < N; i++) a[i] = mag_max_wave(a[i]);
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            // the lane's first value of the largest magnitude, then the first lane holding one
+            float mine = v[i][3];
+            bool hit = fabsf(v[i][3]) == a[i];
+#pragma unroll
+            for (int e = 2; e >= 0; e--) {
+                const bool h = fabsf(v[i][e]) == a[i];
+                mine = h ? v[i][e] : mine;
+                hit = hit || h;
+            }
+            const uint64_t lanes = __ballot(hit);
+            const int first = lanes ? (int)__builtin_ctzll(lanes) : 0;
+            const float xmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), first));
+            q8k_scales(a[i], xmax, s[i], d[i]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; i++) q8_0_scales(mag_max8_lanes(a[i]), s[i], d[i]);
+    }
+    float q[N][4], p[N][4];
+    bool half = false;
+#pragma unroll
+    for (int i = 0; i < N; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float r = round_half_away_product(v[i][e], s[i]);
+            q[i][e] = QBLK == 256 ? fminf(r, 127.f) : r;
+            p[i][e] = __builtin_fmaf(d[i], q[i][e], 0.f);
+            half |= (__float_as_uint(p[i][e]) & 0xffffu) == 0x8000u;
+        }
+    if (__builtin_expect(half, 0)) {
+#pragma unroll
+        for (int i = 0; i < N; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) p[i][e] = product_for_bf16(d[i], q[i][e]);
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = u32x2{pack_bf16x2(p[i][0], p[i][1]), pack_bf16x2(p[i][2], p[i][3])};
+}
+
 template <int QBLK>
 __device__ __forceinline__ u32x2 quant_act4(f32x4 v) {
-    static_assert(QBLK == 32 || QBLK == 256, "Q8_0 or Q8_K blocks");
-    float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    float d, s;  // value = d * q, q from x * s
-    if constexpr (QBLK == 256) {
-        a = max_wave(a);
-        const int e = fabsf(v[0]) == a ? 0 : fabsf(v[1]) == a ? 1 : fabsf(v[2]) == a ? 2 : fabsf(v[3]) == a ? 3 : -1;
-        const uint64_t hit = __ballot(e >= 0);
-        const int first = hit ? (int)__builtin_ctzll(hit) : 0;
-        const float mine = e == 0 ? v[0] : e == 1 ? v[1] : e == 2 ? v[2] : v[3];
-        const float xmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), first));
-        q8k_scales(a, xmax, s, d);
-    } else {
-        q8_0_scales(max8_lanes(a), s, d);
-    }
-    return QBLK == 256 ? q8k_values4(v, s, d) : q8_0_values4(v, s, d);
+    const f32x4 c[1] = {v};
+    u32x2 o[1];
+    quant_act4_n<QBLK, 1>(c, o);
+    return o[0];
 }
 
 }  // namespace qimm

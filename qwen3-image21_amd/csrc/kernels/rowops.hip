@@ -155,6 +155,19 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x
     const float var = (red[4] + red[5] + red[6] + red[7]) / (float)hidden;
     const float rstd = 1.0f / sqrtf(var + 1e-6f);
     uint16_t *orow = out + row * hidden;
+    if constexpr (NI > 0 && QBLK != 0) {
+        // the NI chunks rounded together (their reductions interleave)
+        f32x4 y[NI];
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[i][e] = (v[i][e] - mean) * rstd * sv[i][e];
+        u32x2 o[NI];
+        quant_act4_n<QBLK, NI>(y, o);
+#pragma unroll
+        for (int i = 0; i < NI; i++) *(u32x2 *)(orow + 4 * (tid + 256 * i)) = o[i];
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < (NI > 0 ? NI : LN_MAXV); i++) {
         const int c = tid + 256 * i;
@@ -193,11 +206,12 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *__restrict
         const int64_t c = c0 + 256 * j;
         v[j] = c < k ? *(const f32x4 *)(x + row * ldx + c) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    u32x2 r[QR_CH];
+    quant_act4_n<QBLK, QR_CH>(v, r);
 #pragma unroll
     for (int j = 0; j < QR_CH; j++) {
         const int64_t c = c0 + 256 * j;
-        const u32x2 r = quant_act4<QBLK>(v[j]);
-        if (c < k) *(u32x2 *)(out + row * ldo + c) = r;
+        if (c < k) *(u32x2 *)(out + row * ldo + c) = r[j];
     }
 }
 

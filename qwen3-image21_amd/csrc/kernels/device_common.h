@@ -144,18 +144,6 @@ __device__ __forceinline__ float round_half_away_product(float v, float s) {
     return __builtin_truncf(x + __builtin_copysignf(0.49999997f, x));
 }
 
-// The activation rounding of candle's CPU QMatMul (candle-core 0.11
-// quantized/k_quants.rs, the vec-dot type of the weight): each lane holds four
-// consecutive values of a row, consecutive lanes continue the row.
-//  QBLK 256, BlockQ8K::from_float: the wave's 256 values are one block; x_max is
-//    the first value (in row order) of largest magnitude, iscale = -128/x_max,
-//    q = min(127, round(iscale * x)) (round half away from zero), d = 1/iscale.
-//  QBLK 32, BlockQ8_0::from_float: each aligned group of 8 lanes is one block;
-//    d = amax/127, q = round(x / d) computed as x * (1/d), and the block keeps d
-//    as f16 (round to nearest even).
-// Returns the four bf16 operands bf16(d * q) (product_for_bf16), packed in
-// pairs. Every lane of the block must take part (whole waves for 256, whole
-// 8-lane groups for 32); all-zero blocks give zeros, as candle's d = 0 does.
 // max over each aligned group of 8 lanes (a >= 0 or any floats): DPP moves
 // within quads (xor 1, xor 2), then the half-row mirror (lane i <-> 7 - i)
 template <int CTRL>
@@ -253,10 +241,23 @@ __device__ __forceinline__ float mag_max_wave(float a) {
     return __uint_as_float(max(max(r0, r1), max(r2, r3)));
 }
 
-// quant_act4 over N chunks of four values at once (chunk i its own Q8_K block,
-// or its own eight Q8_0 blocks), each step taken for all chunks before the
-// next, without branches but the one rare halfway test for all N x 4 products,
-// so the chunks' reduction chains interleave.
+// The activation rounding of candle's CPU QMatMul (candle-core 0.11
+// quantized/k_quants.rs, the vec-dot type of the weight): each lane holds four
+// consecutive values of a row, consecutive lanes continue the row.
+//  QBLK 256, BlockQ8K::from_float: the wave's 256 values are one block; x_max is
+//    the first value (in row order) of largest magnitude, iscale = -128/x_max,
+//    q = min(127, round(iscale * x)) (round half away from zero), d = 1/iscale.
+//  QBLK 32, BlockQ8_0::from_float: each aligned group of 8 lanes is one block;
+//    d = amax/127, q = round(x / d) computed as x * (1/d), and the block keeps d
+//    as f16 (round to nearest even).
+// Returns the four bf16 operands bf16(d * q) (product_for_bf16), packed in
+// pairs. Every lane of the block must take part (whole waves for 256, whole
+// 8-lane groups for 32); all-zero blocks give zeros, as candle's d = 0 does.
+// quant_act4 rounds one chunk of four values per lane; quant_act4_n rounds N
+// chunks at once (chunk i its own Q8_K block, or its own eight Q8_0 blocks),
+// each step taken for all chunks before the next, without branches but the one
+// rare halfway test for all N x 4 products, so the chunks' reduction chains
+// interleave.
 template <int QBLK, int N>
 __device__ __forceinline__ void quant_act4_n(const f32x4 (&v)[N], u32x2 (&out)[N]) {
     static_assert(QBLK == 32 || QBLK == 256, "Q8_0 or Q8_K blocks");

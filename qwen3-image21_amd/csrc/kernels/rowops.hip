@@ -183,6 +183,98 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const float *__restrict__ x
     }
 }
 
+// The same for hidden == 1024 NI, RPW consecutive rows per workgroup: the
+// next row's x loads are issued before the current row's reductions, so they
+// are in flight while it is normalised, rounded and stored (one resident round
+// of workgroups streams the rows, instead of rounds that all load, then all
+// compute). The rows are straight-line code (rows past m clamped to the last
+// row, which is then written again with the same values), so every wait for a
+// load is exact. The modulation row is loaded again only where the row's
+// changes. The same arithmetic as ln_mod_kernel.
+template <int QBLK, int NI, int RPW>
+__global__ __launch_bounds__(256) void ln_mod_run_kernel(const float *__restrict__ x, int64_t m,
+                                                         const float *__restrict__ scale, int64_t stride,
+                                                         int64_t rows_per, uint16_t *__restrict__ out,
+                                                         const float *__restrict__ mod, float *__restrict__ prep,
+                                                         int64_t prep_n) {
+    constexpr int64_t hidden = 1024 * NI;
+    __shared__ float red[8];
+    const int tid = threadIdx.x;
+    if (prep)
+        for (int64_t i = (int64_t)blockIdx.x * 256 + tid; i < prep_n; i += (int64_t)gridDim.x * 256)
+            prep[i] = mod_prep_value(mod, i, hidden);
+    const int64_t r0 = (int64_t)blockIdx.x * RPW;
+    f32x4 v[NI], sv[NI];
+    auto load_scale = [&](int64_t sr) __attribute__((always_inline)) {
+        const float *sc = scale + sr * stride;
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            sv[i] = *(const f32x4 *)(sc + 4 * (tid + 256 * i));
+            // 1 + scale, the same rounding as the prepared rows
+            if (prep)
+#pragma unroll
+                for (int e = 0; e < 4; e++) sv[i][e] = sv[i][e] + 1.0f;
+        }
+    };
+    int64_t srow = min(r0, m - 1) / rows_per;
+#pragma unroll
+    for (int i = 0; i < NI; i++) v[i] = *(const f32x4 *)(x + min(r0, m - 1) * hidden + 4 * (tid + 256 * i));
+    load_scale(srow);
+#pragma unroll
+    for (int k = 0; k < RPW; k++) {
+        const int64_t row = min(r0 + k, m - 1), next = min(r0 + k + 1, m - 1);
+        f32x4 vn[NI];
+        if (k + 1 < RPW)
+#pragma unroll
+            for (int i = 0; i < NI; i++) vn[i] = *(const f32x4 *)(x + next * hidden + 4 * (tid + 256 * i));
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < NI; i++) s += v[i][0] + v[i][1] + v[i][2] + v[i][3];
+        s = wave_sum(s);
+        if ((tid & 63) == 0) red[tid >> 6] = s;
+        __syncthreads();
+        const float mean = (red[0] + red[1] + red[2] + red[3]) / (float)hidden;
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float t = v[i][e] - mean;
+                ss += t * t;
+            }
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0) red[4 + (tid >> 6)] = ss;
+        __syncthreads();
+        const float var = (red[4] + red[5] + red[6] + red[7]) / (float)hidden;
+        const float rstd = 1.0f / sqrtf(var + 1e-6f);
+        f32x4 y[NI];
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[i][e] = (v[i][e] - mean) * rstd * sv[i][e];
+        uint16_t *orow = out + row * hidden;
+        if constexpr (QBLK == 0) {
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+                *(u32x2 *)(orow + 4 * (tid + 256 * i)) = u32x2{pack_bf16x2(y[i][0], y[i][1]), pack_bf16x2(y[i][2], y[i][3])};
+        } else {
+            u32x2 o[NI];
+            quant_act4_n<QBLK, NI>(y, o);
+#pragma unroll
+            for (int i = 0; i < NI; i++) *(u32x2 *)(orow + 4 * (tid + 256 * i)) = o[i];
+        }
+        if (k + 1 < RPW) {
+#pragma unroll
+            for (int i = 0; i < NI; i++) v[i] = vn[i];
+            const int64_t sr = next / rows_per;
+            if (sr != srow) {
+                srow = sr;
+                load_scale(sr);
+            }
+        }
+    }
+}
+
 // ---- candle's activation quantization of f32 rows (QMatMul::forward's
 // quantize step, src/quantized_transformer.rs:19-29 -> candle-core 0.11
 // BlockQ8_0 / BlockQ8K::from_float) to the bf16 operands bf16(d * q) ----
@@ -342,11 +434,23 @@ hipError_t launch_ln_mod(const float *x, int64_t m, int64_t hidden, const float 
     if (hidden > LN_MAX_HIDDEN || hidden % 4) return hipErrorInvalidValue;
     if (qblk && hidden % 256) return hipErrorInvalidValue;
     if (qblk != 0 && qblk != 32 && qblk != 256) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)m), block(256);
+    const dim3 block(256);
+    // hidden = 1024 n with 16 to 20 rows per CU: runs of 4 rows per workgroup,
+    // 4 or 5 workgroups per CU, all resident at once (at most 88 VGPRs
+    // allocated: 5 waves per SIMD). More rows would leave a short second round.
+    const int64_t cus = device_cu_count();
+    const bool runs = cus > 0 && m >= 16 * cus && m <= 20 * cus;
     auto go = [&](auto qb, auto ni) {
-        ln_mod_kernel<decltype(qb)::value, decltype(ni)::value>
-            <<<grid, block, 0, stream>>>(x, hidden, scale, stride, rows_per, out, scale, prep,
-                                         prep ? prep_rows * 4 * hidden : 0);
+        constexpr int QB = decltype(qb)::value, NI = decltype(ni)::value;
+        const int64_t prep_n = prep ? prep_rows * 4 * hidden : 0;
+        if constexpr (NI > 0)
+            if (runs) {
+                ln_mod_run_kernel<QB, NI, 4><<<dim3((unsigned)((m + 3) / 4)), block, 0, stream>>>(
+                    x, m, scale, stride, rows_per, out, scale, prep, prep_n);
+                return;
+            }
+        ln_mod_kernel<QB, NI><<<dim3((unsigned)m), block, 0, stream>>>(x, hidden, scale, stride, rows_per, out,
+                                                                      scale, prep, prep_n);
     };
     using Q0 = std::integral_constant<int, 0>;
     using Q32 = std::integral_constant<int, 32>;

@@ -80,7 +80,8 @@ def test_block_1024_q4km_full_size(torch_cuda, qctx):
 @pytest.mark.parametrize("attn_type,down_type,b,s", [(synth.Q8_0, synth.Q8_0, 1, 4352),
                                                      (synth.Q4_K, synth.Q6_K, 1, 4352),
                                                      (synth.Q8_0, synth.Q8_0, 2, 2176),
-                                                     (synth.Q4_K, synth.Q6_K, 1, 4160)])
+                                                     (synth.Q4_K, synth.Q6_K, 1, 4160),
+                                                     (synth.Q8_0, synth.Q8_0, 1, 4102)])
 def test_block_4352_tokens_tail_rows(torch_cuda, qctx, attn_type, down_type, b, s):
     """4352 token rows at hidden 4096 (17 rows of 256x256 tiles): q/k/v makes
     816 tiles and out and down 272 for 256 CUs, so their last 256 token rows
@@ -90,8 +91,10 @@ def test_block_4352_tokens_tail_rows(torch_cuda, qctx, attn_type, down_type, b, 
     or with two sequences of 2176 tokens sequence 1 from position 1920), the
     rest as whole rounds; with 4160 tokens the last 64 rows take the short-M
     kernels (the gated residual and the f32 hidden state with its rows pass;
-    q/k/v keeps them). Sampled rows, the seam at 4096 and 48 of the last rows,
-    and every token's K and V, against the candle-mode oracle."""
+    q/k/v keeps them; with 4102 tokens, a token count that is not a multiple of
+    the LayerNorm's four rows per workgroup, its last workgroup repeats the last
+    row). Sampled rows, the seam at 4096 and up to 48 of the last rows, and every
+    token's K and V, against the candle-mode oracle."""
     p = 64
     m = b * s
     print(f"case: block hidden 4096, {b} x {s} tokens over {p}, types {attn_type}/{down_type}", flush=True)
@@ -99,7 +102,7 @@ def test_block_4352_tokens_tail_rows(torch_cuda, qctx, attn_type, down_type, b, 
     got, (k, v) = run_block(torch_cuda, qctx, CFG4, w, x, mod, pe, kpre, vpre, want_kv=True)
     assert np.isfinite(got).all()
     rng = np.random.default_rng(41)
-    rows = np.unique(np.concatenate([sampled_rows(rng, m), rng.choice(np.arange(4096, m), 48, replace=False)]))
+    rows = np.unique(np.concatenate([sampled_rows(rng, m), rng.choice(np.arange(4096, m), min(48, m - 4096), replace=False)]))
     ref, kr, vr = O.block_forward_rows(CFG4, w, x, mod, pe, rows, kpre, vpre, mode=O.CANDLE)
     g = got.reshape(m, -1)[rows]
     c, mr = cos_sim(g, ref), max_abs_rel(g, ref)

@@ -81,7 +81,8 @@ def test_block_1024_q4km_full_size(torch_cuda, qctx):
                                                      (synth.Q4_K, synth.Q6_K, 1, 4352),
                                                      (synth.Q8_0, synth.Q8_0, 2, 2176),
                                                      (synth.Q4_K, synth.Q6_K, 1, 4160),
-                                                     (synth.Q8_0, synth.Q8_0, 1, 4102)])
+                                                     (synth.Q8_0, synth.Q8_0, 1, 4102),
+                                                     (synth.Q4_K, synth.Q6_K, 2, 2050)])
 def test_block_4352_tokens_tail_rows(torch_cuda, qctx, attn_type, down_type, b, s):
     """4352 token rows at hidden 4096 (17 rows of 256x256 tiles): q/k/v makes
     816 tiles and out and down 272 for 256 CUs, so their last 256 token rows
@@ -93,8 +94,11 @@ def test_block_4352_tokens_tail_rows(torch_cuda, qctx, attn_type, down_type, b, 
     kernels (the gated residual and the f32 hidden state with its rows pass;
     q/k/v keeps them; with 4102 tokens, a token count that is not a multiple of
     the LayerNorm's four rows per workgroup, its last workgroup repeats the last
-    row). Sampled rows, the seam at 4096 and up to 48 of the last rows, and every
-    token's K and V, against the candle-mode oracle."""
+    row; with two sequences of 2050 tokens a workgroup's four rows span the
+    sequence boundary, so it loads the second modulation row midway). Sampled
+    rows, the seam at 4096, up to 48 of the last rows and the rows around a
+    sequence boundary, and every token's K and V, against the candle-mode
+    oracle."""
     p = 64
     m = b * s
     print(f"case: block hidden 4096, {b} x {s} tokens over {p}, types {attn_type}/{down_type}", flush=True)
@@ -102,7 +106,9 @@ def test_block_4352_tokens_tail_rows(torch_cuda, qctx, attn_type, down_type, b, 
     got, (k, v) = run_block(torch_cuda, qctx, CFG4, w, x, mod, pe, kpre, vpre, want_kv=True)
     assert np.isfinite(got).all()
     rng = np.random.default_rng(41)
-    rows = np.unique(np.concatenate([sampled_rows(rng, m), rng.choice(np.arange(4096, m), min(48, m - 4096), replace=False)]))
+    seam = np.arange(s - 4, s + 4) if b > 1 else np.arange(0)
+    rows = np.unique(np.concatenate([sampled_rows(rng, m), rng.choice(np.arange(4096, m), min(48, m - 4096), replace=False),
+                                     seam]))
     ref, kr, vr = O.block_forward_rows(CFG4, w, x, mod, pe, rows, kpre, vpre, mode=O.CANDLE)
     g = got.reshape(m, -1)[rows]
     c, mr = cos_sim(g, ref), max_abs_rel(g, ref)
